@@ -1,0 +1,19 @@
+"""CPU oracle for the conductance-LIF hot path — TEST INFRASTRUCTURE ONLY.
+
+This package restates, on the CPU, the reference algorithm the HIP kernels must
+reproduce. It is the checker: only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import it, and never as the thing measured or
+shipped. The product path (``wiretorch_amd``) never imports it and has no CPU fallback.
+
+Modules:
+
+* ``oracle.dynamics`` — ``simulate`` restated op for op from the reference's PyTorch
+  step ``src/wiretorch/network_simulators/conductance/dynamics.py:95-237``, with the
+  surrogate spike of ``src/wiretorch/training_utils/surrogate_gradients.py:9-33``.
+  Gradients come from torch autograd through the restated step, as in the reference.
+  Pinned by the reference's recorded fixtures (``tests/golden/reference/*.npz``:
+  lockstep, free run, gradients), see ``tests/test_oracle_fixtures.py``.
+* ``oracle.sparse`` — the compressed-connectome propagation used at fly scale, where
+  the reference's dense per-pathway rows cannot be built. Pinned against the dense
+  product on small networks (``tests/test_oracle_sparse.py``).
+"""

@@ -1,0 +1,160 @@
+"""The conductance-LIF step restated on the CPU — TEST INFRASTRUCTURE ONLY (see
+``oracle/__init__.py``).
+
+Op for op the reference's PyTorch step, so that recorded CPU fixtures reproduce
+bit for bit (same torch CPU kernels, same association order):
+
+* ``SurrGradSpike`` — ``src/wiretorch/training_utils/surrogate_gradients.py:9-33``;
+* ``jumps`` — ``conductance/dynamics.py:95-100``;
+* ``spike`` — ``conductance/dynamics.py:103-107``;
+* ``membrane`` — ``conductance/dynamics.py:116-143`` (no Mg block, no adaptation);
+* ``simulate`` — ``conductance/dynamics.py:146-237`` (no gating, no adaptation);
+* ``refractory_mask`` / ``held_at_reset`` / ``count_down`` —
+  ``network_simulators/network.py:294-318``;
+* ``recurrent_activations`` — ``network_simulators/network.py:260-271``;
+* ``Drive.feedforward_activations`` — ``network_simulators/network.py:142-157``.
+
+A drive given in compressed form (``sparse_recurrent`` / ``sparse_feedforward``)
+propagates through ``oracle.sparse.activations`` instead of the dense products.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from oracle import sparse as _sparse
+
+
+class SurrGradSpike(torch.autograd.Function):
+    """Heaviside forward; fast-sigmoid surrogate ``g / (k |x| + 1)^2`` backward."""
+
+    @staticmethod
+    def forward(x, scale):
+        return (x > 0).to(x.dtype)
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        x, scale = inputs
+        ctx.save_for_backward(x)
+        ctx.scale = scale
+
+    @staticmethod
+    def backward(ctx, grad):
+        (x,) = ctx.saved_tensors
+        return grad / (ctx.scale * torch.abs(x) + 1.0) ** 2, None
+
+
+def jumps(drive, jump):
+    """Per pathway, the ``(N, 2, S)`` conductance jump per unit activation."""
+    return [
+        jump[None] * drive.scale[k][:, None, None] * drive.made[k]
+        for k in range(drive.made.shape[0])
+    ]
+
+
+def refractory_mask(counter, n_ref):
+    return None if n_ref is None else (counter > 0).float()
+
+
+def held_at_reset(s, held):
+    return s.detach() if held is None else torch.maximum(s.detach(), held)
+
+
+def count_down(s, counter, n_ref):
+    if n_ref is None:
+        return counter
+    return torch.where(s.detach() > 0, n_ref, (counter - 1).clamp(min=0))
+
+
+def spike(v, p, held=None):
+    s = SurrGradSpike.apply(v - p.theta, p.surr_scale)
+    return s if held is None else s * (1 - held)
+
+
+def membrane(v, s, g, p):
+    """Currents and the voltage after the exponential-Euler step, reset where ``s``."""
+    g_total = torch.minimum(g.sum(dim=2).clamp(min=0.0), p.g_clip)
+    I = g_total * (v[:, :, None] - p.E_syn)
+    rate = -torch.log1p(p.beta - 1) / p.dt
+    g_L = p.C_m * rate
+    I_leak = g_L * (v - p.E_L)
+    G = g_total.sum(dim=2)
+    J = I.sum(dim=2) + I_leak
+    x = p.dt * rate + p.dt * G / p.C_m
+    step = -torch.expm1(-x) / (g_L + G)
+    s = s.detach()
+    v_next = (v - step * J) * (1 - s) + p.U_reset * s
+    return v_next, I, I_leak
+
+
+def recurrent_activations(drive, s):
+    if drive.sparse_recurrent is not None:
+        return list(_sparse.activations(drive.sparse_recurrent, s))
+    return [s[:, rows] @ W for rows, W in drive.recurrent]
+
+
+def feedforward_activations(drive, x):
+    """``(K_ff, B, T, N)``."""
+    if drive.sparse_feedforward is not None:
+        B, T, n_in = x.shape
+        A = _sparse.activations(drive.sparse_feedforward, x.reshape(B * T, n_in))
+        return A.reshape(A.shape[0], B, T, -1)
+    return drive.feedforward_activations(x)
+
+
+def stack_steps(tensors):
+    return torch.stack([t.contiguous() for t in tensors], dim=1)
+
+
+def simulate(
+    v, g, x, drive, p, *, refractory=None, gating=None, adaptation=None,
+    probabilities=False, track=False, track_batch_idx=None, retain=None,
+):  # fmt: skip
+    """Simulate ``x.shape[1]`` steps from ``(v, g)``; returns a ``Run``."""
+    from wiretorch_amd.network import Run
+
+    if gating is not None or adaptation is not None or p.adapt is not None:
+        raise NotImplementedError("gating and adaptation are not restated")
+    A_ff = feedforward_activations(drive, x)
+    kernels = jumps(drive, p.jump)
+    keep = (
+        slice(None)
+        if track_batch_idx is None
+        else slice(track_batch_idx, track_batch_idx + 1)
+    )
+    spikes, probs, tracked = [], [], {"v": [], "I": [], "g": []}
+    if refractory is None:
+        refractory = torch.zeros(v.shape, dtype=torch.int32, device=v.device)
+    for t in range(x.shape[1]):
+        held = refractory_mask(refractory, p.n_ref)
+        s = spike(v, p, held)
+        if probabilities:
+            prob = torch.sigmoid(p.surr_scale * (v - p.theta))
+            probs.append(prob if held is None else prob * (1 - held))
+        v_next, I, I_leak = membrane(v, held_at_reset(s, held), g, p)
+        refractory = count_down(s, refractory, p.n_ref)
+        s_rec = s if drive.recurrent_gradients else s.detach()
+        activations = recurrent_activations(drive, s_rec)
+        activations += list(A_ff[:, :, t])
+        g = g * p.decay
+        for a, kernel in zip(activations, kernels):
+            g = g + a[:, :, None, None] * kernel
+        v = v_next
+        spikes.append(s)
+        if retain is not None:
+            for tensor in (v, g, s):
+                if tensor.requires_grad:
+                    tensor.retain_grad()
+            retain.append((v, g, s))
+        if track:
+            tracked["v"].append(v[keep].detach())
+            tracked["I"].append(torch.cat([I, I_leak[..., None]], dim=-1)[keep].detach())
+            tracked["g"].append(g[keep].detach())
+    return Run(
+        output=torch.stack(spikes, dim=1),
+        v=v,
+        syn=g,
+        probabilities=torch.stack(probs, dim=1) if probabilities else None,
+        tracked={k: stack_steps(val) for k, val in tracked.items() if val} if track else None,
+        refractory=refractory,
+    )

@@ -1,0 +1,824 @@
+"""Conductance-based LIF networks: connectivity, pathways, physiology tables, state.
+
+This is the host side of the drop-in boundary. A network organises its projections
+into *pathways* (one per source cell type and input side, recurrent first) and builds,
+per forward call, the ``Drive`` (per-pathway rows, weights, kernel scale and synapse
+types made) and the ``Physiology`` (per-neuron and per-synapse tables) that
+``engine.simulate`` consumes — the same contract as the reference's
+``ProjectionNetwork._simulate`` (``src/wiretorch/network_simulators/network.py:889-921``)
+calling ``conductance/engine.py:71-89``.
+
+Table values and their order follow the reference so that both engines see
+bit-identical inputs:
+
+* per-neuron tables and ``C_m = tau_mem * g_L``: ``conductance/synapses.py:18-29``;
+* per-synapse tables, ``g_clip`` inf by default: ``conductance/synapses.py:32-36``;
+* kernel jump ``(-g_bar, g_bar) / peak``: ``conductance/synapses.py:70-87``;
+* ``alpha = exp(-dt / tau_syn)``, ``beta = exp(-dt / tau_mem)``:
+  ``conductance/network.py:195-205``; ``n_ref = round(tau_ref / dt)``:
+  ``network.py:553-558``;
+* pathway order (per side, ascending source cell type, recurrent first) and rows:
+  ``network.py:640-729``; weight assembly ``network.py:731-764``; ``Drive``:
+  ``network.py:816-854``;
+* learnt physiology: ``network.py:560-638``, ``conductance/network.py:210-246``;
+* state at rest (``v = U_reset``, ``g = 0`` laid out ``(B, 2, S, N)``):
+  ``conductance/network.py:248-255``.
+
+Presynaptic dynamics (short-term plasticity, receptor saturation), the NMDA Mg block
+and spike-frequency adaptation are not part of this build: a network configured with
+any of them raises ``NotImplementedError``.
+
+``Drive`` also accepts a sparse form (``connectome.Connectome``) for connectomes too
+large for the reference's dense per-pathway rows (fly scale).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+from torch import nn
+
+from wiretorch_amd.projections import Projection, projection_mask
+from wiretorch_amd.synapses import SynapseRegistry
+from wiretorch_amd.type_parameters import (
+    TypeParameters,
+    learnt_synapses,
+    learnt_types,
+)
+
+NEURON_PARAMETERS = ("tau_mem", "theta", "U_reset", "E_L", "g_L")
+SYNAPSE_PARAMETERS = ("tau_rise", "tau_decay", "E_syn", "g_bar")
+#: Learnable physiology: cell parameters (default value, None if required) and
+#: synapse parameters; positive ones are learnt as logarithms.
+LEARNABLE = {"tau_mem": None, "theta": None, "U_reset": None, "E_L": None, "g_L": None}
+LEARNABLE_SYNAPSE = SYNAPSE_PARAMETERS
+POSITIVE = {"tau_mem", "g_L", "tau_rise", "tau_decay", "g_bar"}
+STORAGE_DTYPES = (torch.float32, torch.float16)
+
+
+# =====================================================================
+# What the engine consumes
+# =====================================================================
+
+
+@dataclass
+class Drive:
+    """The synaptic drive of one forward call, pathway by pathway (recurrent first).
+
+    ``made`` ``(K, S)`` bool: the synapse types each pathway makes; ``scale`` ``(K, N)``:
+    its kernel's factor per target neuron. ``recurrent[k]`` / ``feedforward[k]`` are
+    ``(rows, W)``: source rows (network neurons / input columns) and ``(n_rows, N)``
+    weights. Alternatively ``sparse_recurrent`` / ``sparse_feedforward`` hold the
+    connectome in compressed form (``connectome.Connectome``) and the dense lists are
+    empty; the pathway count then comes from the connectome.
+    """
+
+    made: torch.Tensor
+    scale: torch.Tensor
+    recurrent: list = field(default_factory=list)
+    feedforward: list = field(default_factory=list)
+    differentiable_inputs: slice | None = None
+    recurrent_gradients: bool = False
+    gates: list = field(default_factory=list)
+    sparse_recurrent: object | None = None
+    sparse_feedforward: object | None = None
+
+    @property
+    def K_rec(self) -> int:
+        if self.sparse_recurrent is not None:
+            return self.sparse_recurrent.n_pathways
+        return len(self.recurrent)
+
+    @property
+    def K_ff(self) -> int:
+        if self.sparse_feedforward is not None:
+            return self.sparse_feedforward.n_pathways
+        return len(self.feedforward)
+
+    def feedforward_activations(self, x: torch.Tensor) -> torch.Tensor:
+        """``(K_ff, B, T, N)``: each feedforward pathway's input times its weights."""
+        B, T = x.shape[:2]
+        if not self.feedforward:
+            return x.new_zeros((0, B, T, 0))
+        return torch.stack([x[:, :, rows] @ W for rows, W in self.feedforward])
+
+
+@dataclass
+class Physiology:
+    """Every parameter of the dynamics (``conductance/dynamics.py:56-92``).
+
+    Per neuron ``(N,)``: ``theta``, ``U_reset``, ``E_L``, ``C_m``, ``beta``. Per synapse
+    type ``(S,)``: ``E_syn``, ``g_clip``; ``decay`` and ``jump`` ``(2, S)`` (rise, decay
+    component). ``dt`` and ``surr_scale`` are 0-d tensors; ``n_ref`` ``(N,)`` int32 or
+    None when no neuron has a refractory period.
+    """
+
+    theta: torch.Tensor
+    U_reset: torch.Tensor
+    E_L: torch.Tensor
+    C_m: torch.Tensor
+    beta: torch.Tensor
+    E_syn: torch.Tensor
+    g_clip: torch.Tensor
+    decay: torch.Tensor
+    jump: torch.Tensor
+    dt: torch.Tensor
+    surr_scale: torch.Tensor
+    spike_mode: str = "deterministic"
+    storage_dtype: torch.dtype = torch.float32
+    n_ref: torch.Tensor | None = None
+    mg_c: torch.Tensor | None = None
+    mg_a: torch.Tensor | None = None
+    adapt: torch.Tensor | None = None
+    adapt_decay: torch.Tensor | None = None
+    E_adapt: torch.Tensor | None = None
+
+
+@dataclass
+class Run:
+    """What a simulation produced (``network.py:321-351``): ``output`` ``(B, T, N)``,
+    the state after the last step, and optional probabilities / tracked variables."""
+
+    output: torch.Tensor
+    v: torch.Tensor
+    syn: torch.Tensor
+    probabilities: torch.Tensor | None = None
+    tracked: dict | None = None
+    refractory: torch.Tensor | None = None
+    gating: torch.Tensor | None = None
+    adaptation: torch.Tensor | None = None
+
+    @property
+    def spikes(self) -> torch.Tensor:
+        return self.output
+
+    @property
+    def g(self) -> torch.Tensor:
+        return self.syn
+
+
+def conductance_kernel(tau_rise, tau_decay, g_bar) -> torch.Tensor:
+    """``(2, S)`` jump of the rise and decay components per unit input: ``-g_bar`` and
+    ``+g_bar`` over the peak of the difference of exponentials, so the waveform peaks at
+    ``g_bar`` (``conductance/synapses.py:70-87``)."""
+    r = tau_rise / tau_decay
+    peak = r ** (r / (1 - r)) - r ** (1 / (1 - r))
+    return torch.stack([-g_bar, g_bar], dim=0) / peak
+
+
+@dataclass
+class InputSide:
+    """One source of synaptic input (``network.py:55-77``)."""
+
+    projections: dict
+    cell_params: list
+    synapse_params: list
+    cell_type_indices: np.ndarray
+    recurrent: bool
+    attribute: str
+    mask_buffer: str
+
+
+@dataclass(frozen=True)
+class Pathway:
+    """One source cell type on one input side."""
+
+    index: int
+    side: int
+    cell_type: int
+    mode: str
+
+
+def _long(values) -> torch.Tensor:
+    return torch.from_numpy(np.asarray(values)).long()
+
+
+def _check_ids(params, key, what):
+    ids = sorted(p[key] for p in params)
+    assert ids == list(range(len(ids))), f"{what} must be 0-indexed contiguous, got {ids}"
+
+
+def validate(dt, cell_params, cell_type_indices, sides) -> None:
+    """Construction checks with messages naming what is wrong (``network.py:1059-1109``)."""
+    assert isinstance(dt, (int, float)) and dt > 0, f"dt must be positive, got {dt}"
+    assert dt <= 100.0, f"dt unusually large ({dt} ms), check units"
+    _check_ids(cell_params, "cell_id", "cell_ids in cell_params")
+    assert cell_type_indices.ndim == 1 and cell_type_indices.shape[0] > 0
+    assert np.all((cell_type_indices >= 0) & (cell_type_indices < len(cell_params)))
+    targets = {p["name"]: p["cell_id"] for p in cell_params}
+    n_target = np.bincount(cell_type_indices, minlength=len(cell_params))
+    for side in sides:
+        _check_ids(side.cell_params, "cell_id", f"{side.attribute} source cell_ids")
+        assert side.synapse_params, f"{side.attribute}: synapse_params must not be empty"
+        _check_ids(side.synapse_params, "synapse_id", f"{side.attribute} synapse_ids")
+        types = side.cell_type_indices
+        assert types.ndim == 1 and np.all((types >= 0) & (types < len(side.cell_params)))
+        sources = {p["name"]: p["cell_id"] for p in side.cell_params}
+        n_source = np.bincount(types, minlength=len(side.cell_params))
+        for (src, tgt), projection in side.projections.items():
+            assert src in sources, f"{side.attribute}: source {src!r} not in its cell_params"
+            assert tgt in targets, f"{side.attribute}: target {tgt!r} not in cell_params"
+            want = (int(n_source[sources[src]]), int(n_target[targets[tgt]]))
+            got = (projection.n_source, projection.n_target)
+            assert got == want, f"{side.attribute} projection ({src!r}, {tgt!r}) {got} != {want}"
+
+
+def _unsupported(cell_params, synapse_lists, stp) -> None:
+    for cell in cell_params:
+        if cell.get("adapt", 0.0):
+            raise NotImplementedError("spike-frequency adaptation is not supported")
+    for synapses in synapse_lists:
+        for syn in synapses:
+            if syn.get("mg", 0.0):
+                raise NotImplementedError("the NMDA Mg block is not supported")
+            if syn.get("saturation", 0.0):
+                raise NotImplementedError("saturating synapses are not supported")
+    if any(stp):
+        raise NotImplementedError("short-term plasticity is not supported")
+
+
+# =====================================================================
+# The network
+# =====================================================================
+
+
+class ConductanceNetwork(nn.Module):
+    """Base of the conductance-based LIF networks (``network.py:354-1026`` and
+    ``conductance/network.py:44-255`` for the mechanisms this build supports).
+
+    State ``v`` ``(B, N)``, conductances ``(B, N, 2, S)`` (stored ``(B, 2, S, N)``) and
+    refractory counters ``(B, N)`` int32 continue from one ``forward`` call to the next
+    until ``reset_state``.
+    """
+
+    state_name = "g"
+    output_name = "s"
+    recurrent_gradients = False
+    has_refractory = True
+
+    def __init__(
+        self,
+        *,
+        dt: float,
+        cell_params: list[dict],
+        cell_type_indices: np.ndarray,
+        sides: list[InputSide],
+        unify_synapses: bool,
+        surrgrad_scale: float,
+        batch_size: int,
+        spike_mode: str,
+        track_variables: bool,
+        track_gradients: bool,
+        track_batch_idx: int | None,
+        storage_dtype=torch.float32,
+        learn: dict | None = None,
+    ):
+        super().__init__()
+        assert isinstance(surrgrad_scale, (int, float)) and surrgrad_scale > 0
+        validate(dt, cell_params, cell_type_indices, sides)
+        if spike_mode != "deterministic":
+            raise NotImplementedError("only spike_mode='deterministic' is supported")
+        self.learn = dict(learn or {})
+        self.spike_mode = spike_mode
+        self.batch_size = batch_size
+        self.track_variables = track_variables
+        self.track_gradients = track_gradients
+        self.track_batch_idx = track_batch_idx
+        self.storage_dtype = storage_dtype
+        self.differentiable_inputs = None
+        self.cell_params = cell_params
+        self.n_cell_types = len(cell_params)
+        self.n_neurons = int(cell_type_indices.shape[0])
+        self._sides = sides
+        self._names = {c["cell_id"]: c["name"] for c in cell_params}
+        self.registry = SynapseRegistry.build(
+            [(s.cell_params, s.synapse_params) for s in sides], unify=unify_synapses
+        )
+        self.register_buffer("cell_type_indices", _long(cell_type_indices))
+        for side in sides:
+            modules = {f"{s}__{t}": p for (s, t), p in side.projections.items()}
+            setattr(self, side.attribute, nn.ModuleDict(modules))
+            self.register_buffer(side.mask_buffer, torch.from_numpy(self._mask(side)))
+        self._register_physiology(surrgrad_scale)
+        self.pathways = self._build_pathways()
+        self.set_timestep(float(dt))
+
+    # ------------------------------------------------------------------
+    # Construction
+    # ------------------------------------------------------------------
+
+    @property
+    def storage_dtype(self) -> torch.dtype:
+        """What the kernels store conductances in (arithmetic stays float32)."""
+        return self._storage_dtype
+
+    @storage_dtype.setter
+    def storage_dtype(self, dtype) -> None:
+        dtype = getattr(torch, dtype) if isinstance(dtype, str) else dtype
+        if dtype not in STORAGE_DTYPES:
+            raise ValueError(f"storage_dtype must be one of {STORAGE_DTYPES}, got {dtype}")
+        self._storage_dtype = dtype
+
+    def _block(self, side: InputSide, src: str, tgt: str):
+        src_id = next(c["cell_id"] for c in side.cell_params if c["name"] == src)
+        tgt_id = next(c["cell_id"] for c in self.cell_params if c["name"] == tgt)
+        rows = np.flatnonzero(side.cell_type_indices == src_id)
+        cols = np.flatnonzero(self.cell_type_indices.cpu().numpy() == tgt_id)
+        return rows, cols
+
+    def _mask(self, side: InputSide) -> np.ndarray:
+        mask = np.zeros((len(side.cell_type_indices), self.n_neurons), dtype=bool)
+        for (src, tgt), projection in side.projections.items():
+            rows, cols = self._block(side, src, tgt)
+            if rows.size and cols.size:
+                mask[np.ix_(rows, cols)] = projection_mask(projection)
+        return mask
+
+    def _per_neuron(self, name: str, default: float | None = None) -> torch.Tensor:
+        lookup = np.zeros(self.n_cell_types, dtype=np.float32)
+        for cell in self.cell_params:
+            lookup[cell["cell_id"]] = cell[name] if default is None else cell.get(name, default)
+        return torch.from_numpy(lookup[self.cell_type_indices.cpu().numpy()])
+
+    def _register_physiology(self, surrgrad_scale: float) -> None:
+        for name in NEURON_PARAMETERS:
+            self.register_buffer(name, self._per_neuron(name))
+        self.register_buffer("C_m", self.tau_mem * self.g_L)
+        for name in SYNAPSE_PARAMETERS:
+            self.register_buffer(name, self.registry.table(name))
+        self.register_buffer("g_clip", self.registry.table("g_clip", default=float("inf")))
+        tau_ref = self._per_neuron("tau_ref", 0.0)
+        assert bool((tau_ref >= 0).all()), "cell_params: tau_ref must be >= 0"
+        self.register_buffer("tau_ref", tau_ref, persistent=False)
+        self.register_buffer(
+            "surrgrad_scale", torch.tensor(float(surrgrad_scale), dtype=torch.float32)
+        )
+        self._register_learnt()
+
+    def _register_learnt(self) -> None:
+        learn = self.learn
+        unknown = set(learn) - set(LEARNABLE) - set(LEARNABLE_SYNAPSE)
+        assert not unknown, f"learn: unknown parameters {sorted(unknown)}"
+        cells = sorted(self.cell_params, key=lambda c: c["cell_id"])
+        names = [c["name"] for c in cells]
+        learnt = {
+            name: learnt_types(learn[name], names, f"learn[{name!r}]")
+            for name in LEARNABLE
+            if learn.get(name)
+        }
+        if learnt:
+            values = {name: [c[name] for c in cells] for name in learnt}
+            self.cell_parameters = TypeParameters(
+                values, learnt=learnt, positive=POSITIVE & set(learnt)
+            )
+            for name, types in learnt.items():
+                mask = torch.isin(self.cell_type_indices, torch.tensor(types))
+                self.register_buffer(f"_learnt_{name}", mask, persistent=False)
+        synapses = self.registry.synapses
+        learnt = {
+            name: learnt_synapses(learn[name], synapses, f"learn[{name!r}]")
+            for name in LEARNABLE_SYNAPSE
+            if learn.get(name)
+        }
+        if learnt:
+            values = {name: self.registry.table(name).tolist() for name in learnt}
+            self.synapse_parameters = TypeParameters(
+                values, learnt=learnt, positive=POSITIVE & set(learnt)
+            )
+            for name, types in learnt.items():
+                mask = torch.zeros(len(synapses), dtype=torch.bool)
+                mask[types] = True
+                self.register_buffer(f"_learnt_{name}", mask, persistent=False)
+
+    def _learnt(self, name: str, fixed: torch.Tensor, decay: bool = False):
+        """``fixed`` with the learnt types' values in place (``decay``: as
+        ``exp(-dt / value)``), ``network.py:621-634``."""
+        mask = getattr(self, f"_learnt_{name}", None)
+        if mask is None:
+            return fixed
+        if name in LEARNABLE_SYNAPSE:
+            value = self.synapse_parameters.value(name)
+        else:
+            value = self.cell_parameters.value(name)[self.cell_type_indices]
+        if decay:
+            value = torch.exp(-self.dt / value)
+        return torch.where(mask, value, fixed)
+
+    def _learns(self, *names: str) -> bool:
+        return any(hasattr(self, f"_learnt_{n}") for n in names)
+
+    def _build_pathways(self) -> list[Pathway]:
+        pathways, made = [], []
+        for side_no, side in enumerate(self._sides):
+            names = {c["cell_id"]: c["name"] for c in side.cell_params}
+            modes: dict[str, str] = {}
+            for (src, _), projection in side.projections.items():
+                mode = modes.setdefault(src, projection.caching_mode)
+                if mode != projection.caching_mode:
+                    raise ValueError(
+                        f"source cell type {src!r} has projections with mixed caching modes"
+                    )
+            for cell_type, synapses in self.registry.made_by(
+                side_no, side.synapse_params
+            ).items():
+                mode = modes.get(names[cell_type])
+                if mode is None:
+                    continue
+                index = len(pathways)
+                rows = np.flatnonzero(side.cell_type_indices == cell_type)
+                self.register_buffer(f"_rows_{index}", _long(rows), persistent=False)
+                pathways.append(Pathway(index, side_no, cell_type, mode))
+                made.append(synapses)
+        self.register_buffer(
+            "_made",
+            torch.stack(made) if made else torch.zeros((0, len(self.registry)), dtype=torch.bool),
+            persistent=False,
+        )
+        # Recurrent pathways first: the order the dynamics inject them in.
+        return sorted(pathways, key=lambda p: not self._sides[p.side].recurrent)
+
+    def _assemble(self, pathway: Pathway, connectome: bool = False) -> torch.Tensor:
+        """The pathway's ``(n_rows, N)`` weights from its projections."""
+        side = self._sides[pathway.side]
+        rows = getattr(self, f"_rows_{pathway.index}")
+        W = torch.zeros((rows.numel(), self.n_neurons), **self._float)
+        projections = getattr(self, side.attribute)
+        src = next(c["name"] for c in side.cell_params if c["cell_id"] == pathway.cell_type)
+        for tgt_id, tgt in self._names.items():
+            key = f"{src}__{tgt}"
+            if key not in projections:
+                continue
+            cols = (self.cell_type_indices == tgt_id).nonzero(as_tuple=True)[0]
+            if cols.numel():
+                projection = projections[key]
+                W[:, cols] = projection.connectome if connectome else projection()
+        return W
+
+    def _cache_weights(self) -> None:
+        for pathway in self.pathways:
+            if pathway.mode != "weights":
+                W = self._assemble(pathway, connectome=pathway.mode == "scaling_factors")
+                self.register_buffer(f"_weights_{pathway.index}", W.detach(), persistent=False)
+
+    def set_timestep(self, dt: float) -> None:
+        """Set the time step, recompute what depends on it, reset the state."""
+        assert isinstance(dt, float) and dt > 0, "dt must be a positive float"
+        self.register_buffer("dt", torch.tensor(dt, device=self.device))
+        self.register_buffer("tau_syn", torch.stack((self.tau_rise, self.tau_decay)))
+        self.register_buffer("alpha", torch.exp(-self.dt / self.tau_syn))
+        self.register_buffer("beta", torch.exp(-self.dt / self.tau_mem))
+        self.register_buffer(
+            "g_scale", conductance_kernel(self.tau_rise, self.tau_decay, self.g_bar)
+        )
+        n_ref = torch.round(self.tau_ref / self.dt).to(torch.int32)
+        self.register_buffer("n_ref", n_ref, persistent=False)
+        self._refractory = bool(n_ref.any())
+        self._cache_weights()
+        self.reset_state()
+
+    # ------------------------------------------------------------------
+    # Per call
+    # ------------------------------------------------------------------
+
+    @property
+    def device(self) -> torch.device:
+        return self.cell_type_indices.device
+
+    @property
+    def _float(self) -> dict:
+        return {"device": self.device, "dtype": self.dt.dtype}
+
+    def _scaling_matrix(self, side_index: int) -> torch.Tensor:
+        side = self._sides[side_index]
+        src_ids = {c["name"]: c["cell_id"] for c in side.cell_params}
+        tgt_ids = {c["name"]: c["cell_id"] for c in self.cell_params}
+        sf = torch.ones((len(side.cell_params), self.n_cell_types), **self._float)
+        for key, projection in getattr(self, side.attribute).items():
+            if projection.caching_mode == "scaling_factors":
+                src, tgt = key.split("__", 1)
+                sf[src_ids[src], tgt_ids[tgt]] = projection.kernel_factor()
+        return sf
+
+    def _drive(self) -> Drive:
+        """Per pathway: rows, current weights and kernel scale (``network.py:816-854``)."""
+        scaling, assembled = {}, {}
+        ones = torch.ones(self.n_neurons, **self._float)
+        scales, recurrent, feedforward = [], [], []
+        for pathway in self.pathways:
+            if pathway.mode != "weights":
+                W = getattr(self, f"_weights_{pathway.index}")
+            else:
+                W = assembled[pathway.index] = self._assemble(pathway)
+            if pathway.mode == "scaling_factors":
+                if pathway.side not in scaling:
+                    scaling[pathway.side] = self._scaling_matrix(pathway.side)
+                scales.append(scaling[pathway.side][pathway.cell_type, self.cell_type_indices])
+            else:
+                scales.append(ones)
+            rows = getattr(self, f"_rows_{pathway.index}")
+            target = recurrent if self._sides[pathway.side].recurrent else feedforward
+            target.append((rows, W))
+        order = [p.index for p in self.pathways]
+        return Drive(
+            made=self._made[order],
+            scale=torch.stack(scales) if scales else ones.new_zeros((0, self.n_neurons)),
+            recurrent=recurrent,
+            feedforward=feedforward,
+            differentiable_inputs=self.differentiable_inputs,
+            recurrent_gradients=self.recurrent_gradients,
+        )
+
+    def _physiology(self) -> Physiology:
+        """The engine's parameters for one call (``conductance/network.py:210-246``)."""
+        learnt = self._learnt
+        C_m, decay, jump = self.C_m, self.alpha, self.g_scale
+        if self._learns("tau_mem", "g_L"):
+            C_m = learnt("tau_mem", self.tau_mem) * learnt("g_L", self.g_L)
+        if self._learns("tau_rise", "tau_decay", "g_bar"):
+            tau_rise = learnt("tau_rise", self.tau_rise)
+            tau_decay = learnt("tau_decay", self.tau_decay)
+            decay = torch.exp(-self.dt / torch.stack((tau_rise, tau_decay)))
+            jump = conductance_kernel(tau_rise, tau_decay, learnt("g_bar", self.g_bar))
+        return Physiology(
+            theta=learnt("theta", self.theta),
+            U_reset=learnt("U_reset", self.U_reset),
+            E_L=learnt("E_L", self.E_L),
+            C_m=C_m,
+            beta=learnt("tau_mem", self.beta, decay=True),
+            E_syn=learnt("E_syn", self.E_syn),
+            g_clip=self.g_clip,
+            decay=decay,
+            jump=jump,
+            dt=self.dt,
+            surr_scale=self.surrgrad_scale,
+            spike_mode=self.spike_mode,
+            storage_dtype=self.storage_dtype,
+            n_ref=self.n_ref if self._refractory else None,
+        )
+
+    def _initial_state(self):
+        v = self.U_reset.expand(self.batch_size, self.n_neurons).clone()
+        g = torch.zeros(
+            (self.batch_size, 2, len(self.registry), self.n_neurons), device=self.device
+        ).permute(0, 3, 1, 2)
+        return v, g
+
+    @torch.compiler.disable
+    def _simulate(self, input_spikes, probabilities: bool = False) -> Run:
+        if isinstance(input_spikes, np.ndarray):
+            input_spikes = torch.from_numpy(input_spikes).to(self.device)
+        self._validate_forward(input_spikes)
+        retain = [] if self.track_gradients else None
+        run = self._engine.simulate(
+            self.v,
+            self._synaptic,
+            input_spikes.to(self.dt.dtype),
+            self._drive(),
+            self._physiology(),
+            refractory=self.refractory,
+            probabilities=probabilities,
+            track=self.track_variables,
+            track_batch_idx=self.track_batch_idx,
+            retain=retain,
+        )
+        if retain is not None:
+            self._retained = retain
+        self.v = run.v.detach()
+        self._synaptic = run.syn.detach()
+        if run.refractory is not None:
+            self.refractory = run.refractory
+        return run
+
+    def _validate_forward(self, input_spikes: torch.Tensor) -> None:
+        assert isinstance(input_spikes, torch.Tensor), "input_spikes must be a Tensor"
+        assert input_spikes.device == self.device, (
+            f"input_spikes on {input_spikes.device}, model on {self.device}"
+        )
+        assert input_spikes.ndim == 3, f"input_spikes must be 3D, got {input_spikes.shape}"
+        assert input_spikes.shape[2] == self.n_inputs, (
+            f"input_spikes shape[2]={input_spikes.shape[2]}, expected {self.n_inputs}"
+        )
+        if input_spikes.shape[0] != self.batch_size:
+            raise ValueError(
+                f"Input batch size {input_spikes.shape[0]} != model batch size "
+                f"{self.batch_size}; call reset_state(batch_size=...) first"
+            )
+
+    # ------------------------------------------------------------------
+    # State
+    # ------------------------------------------------------------------
+
+    @property
+    def _synaptic(self) -> torch.Tensor:
+        return getattr(self, self.state_name)
+
+    @_synaptic.setter
+    def _synaptic(self, value: torch.Tensor) -> None:
+        setattr(self, self.state_name, value)
+
+    def reset_state(self, batch_size: int | None = None) -> None:
+        if batch_size is not None:
+            self.batch_size = batch_size
+        v, g = self._initial_state()
+        self.register_buffer("v", v, persistent=False)
+        self.register_buffer(self.state_name, g, persistent=False)
+        counter = torch.zeros((self.batch_size, self.n_neurons), dtype=torch.int32, device=self.device)
+        self.register_buffer("refractory", counter, persistent=False)
+
+    def get_checkpoint_state(self) -> dict[str, np.ndarray]:
+        state = {"v": self.v.cpu().numpy(), self.state_name: self._synaptic.cpu().numpy()}
+        if self._refractory:
+            state["refractory"] = self.refractory.cpu().numpy()
+        return state
+
+    def load_checkpoint_state(self, state: dict[str, np.ndarray]) -> None:
+        self.v = torch.from_numpy(state["v"]).to(self.device)
+        self._synaptic = torch.from_numpy(state[self.state_name]).to(self.device)
+        self.refractory = (
+            torch.from_numpy(state["refractory"]).to(self.device)
+            if "refractory" in state
+            else torch.zeros_like(self.v, dtype=torch.int32)
+        )
+
+    def _weight_matrix(self, side_index: int) -> torch.Tensor:
+        side = self._sides[side_index]
+        W = torch.zeros((len(side.cell_type_indices), self.n_neurons), **self._float)
+        for (src, tgt), _ in side.projections.items():
+            rows, cols = self._block(side, src, tgt)
+            if rows.size and cols.size:
+                W[np.ix_(rows, cols)] = getattr(self, side.attribute)[f"{src}__{tgt}"]()
+        return W
+
+
+def _engine_module():
+    from wiretorch_amd import engine
+
+    return engine
+
+
+class ConductanceLIFNetwork(ConductanceNetwork):
+    """Recurrent conductance-based LIF network (``conductance/recurrent.py:19-208``).
+
+    ``rec_projections`` and ``ff_projections`` map ``(source type, target type)`` to a
+    ``Projection``; synapse types with the same (cell type, synapse) signature on both
+    sides share one conductance. Gradients flow through the recurrent spikes only if
+    ``recurrent_gradients``.
+    """
+
+    def __init__(
+        self,
+        dt: float,
+        rec_projections: dict,
+        ff_projections: dict,
+        cell_type_indices: np.ndarray,
+        cell_type_indices_FF: np.ndarray,
+        cell_params: list[dict],
+        cell_params_FF: list[dict],
+        synapse_params: list[dict],
+        synapse_params_FF: list[dict],
+        surrgrad_scale: float,
+        batch_size: int,
+        spike_mode: str = "deterministic",
+        track_variables: bool = False,
+        track_gradients: bool = False,
+        track_batch_idx: int | None = None,
+        storage_dtype=torch.float32,
+        learn: dict | None = None,
+        recurrent_gradients: bool = False,
+        rec_stp: dict | None = None,
+        ff_stp: dict | None = None,
+    ):
+        _unsupported(cell_params, (synapse_params, synapse_params_FF), (rec_stp, ff_stp))
+        self.synapse_params = synapse_params
+        self.cell_params_FF = cell_params_FF
+        self.synapse_params_FF = synapse_params_FF
+        self.n_synapse_types = len(synapse_params)
+        self.n_cell_types_FF = len(cell_params_FF)
+        self.n_inputs = int(cell_type_indices_FF.shape[0])
+        super().__init__(
+            dt=dt,
+            cell_params=cell_params,
+            cell_type_indices=cell_type_indices,
+            sides=[
+                InputSide(rec_projections, cell_params, synapse_params, cell_type_indices,
+                          True, "rec_projections", "weights_mask"),
+                InputSide(ff_projections, cell_params_FF, synapse_params_FF,
+                          cell_type_indices_FF, False, "ff_projections", "weights_mask_FF"),
+            ],
+            unify_synapses=True,
+            surrgrad_scale=surrgrad_scale,
+            batch_size=batch_size,
+            spike_mode=spike_mode,
+            track_variables=track_variables,
+            track_gradients=track_gradients,
+            track_batch_idx=track_batch_idx,
+            storage_dtype=storage_dtype,
+            learn=learn,
+        )  # fmt: skip
+        self.register_buffer("cell_type_indices_FF", _long(cell_type_indices_FF))
+        self.recurrent_gradients = recurrent_gradients
+        self._engine = _engine_module()
+
+    def forward(self, input_spikes):
+        run = self._simulate(input_spikes)
+        if not self.track_variables:
+            return run.spikes
+        S = len(self.registry)
+        return {
+            "spikes": run.spikes,
+            "voltages": run.tracked["v"],
+            "currents": run.tracked["I"][..., :S],
+            "currents_leak": run.tracked["I"][..., S],
+            "conductances": run.tracked["g"],
+        }
+
+    @property
+    def weights(self) -> torch.Tensor:
+        return self._weight_matrix(0)
+
+    @property
+    def weights_FF(self) -> torch.Tensor:
+        return self._weight_matrix(1)
+
+    @property
+    def n_unified_synapse_types(self) -> int:
+        return len(self.registry)
+
+
+class FeedforwardConductanceLIFNetwork(ConductanceNetwork):
+    """Conductance-based LIF neurons driven only by input rows
+    (``conductance/feedforward.py:19-143``)."""
+
+    state_name = "g_FF"
+
+    def __init__(
+        self,
+        dt: float,
+        projections: dict,
+        cell_type_indices: np.ndarray,
+        cell_type_indices_FF: np.ndarray,
+        cell_params: list[dict],
+        cell_params_FF: list[dict],
+        synapse_params_FF: list[dict],
+        surrgrad_scale: float,
+        batch_size: int,
+        spike_mode: str = "deterministic",
+        track_variables: bool = False,
+        track_gradients: bool = False,
+        track_batch_idx: int | None = None,
+        storage_dtype=torch.float32,
+        return_probabilities: bool = False,
+        learn: dict | None = None,
+        stp: dict | None = None,
+    ):
+        _unsupported(cell_params, (synapse_params_FF,), (stp,))
+        self.cell_params_FF = cell_params_FF
+        self.synapse_params_FF = synapse_params_FF
+        self.n_cell_types_FF = len(cell_params_FF)
+        self.n_synapse_types_FF = len(synapse_params_FF)
+        self.n_inputs = int(cell_type_indices_FF.shape[0])
+        self.return_probabilities = return_probabilities
+        super().__init__(
+            dt=dt,
+            cell_params=cell_params,
+            cell_type_indices=cell_type_indices,
+            sides=[
+                InputSide(projections, cell_params_FF, synapse_params_FF,
+                          cell_type_indices_FF, False, "projections", "weights_mask_FF"),
+            ],
+            unify_synapses=False,
+            surrgrad_scale=surrgrad_scale,
+            batch_size=batch_size,
+            spike_mode=spike_mode,
+            track_variables=track_variables,
+            track_gradients=track_gradients,
+            track_batch_idx=track_batch_idx,
+            storage_dtype=storage_dtype,
+            learn=learn,
+        )  # fmt: skip
+        self.register_buffer("cell_type_indices_FF", _long(cell_type_indices_FF))
+        self._engine = _engine_module()
+
+    def forward(self, input_spikes):
+        run = self._simulate(input_spikes, probabilities=self.return_probabilities)
+        if self.track_variables:
+            S = self.n_synapse_types_FF
+            out = {
+                "spikes": run.spikes,
+                "voltages": run.tracked["v"],
+                "currents_feedforward": run.tracked["I"][..., :S],
+                "currents_leak": run.tracked["I"][..., S],
+                "conductances_feedforward": run.tracked["g"],
+            }
+            if self.return_probabilities:
+                out["probabilities"] = run.probabilities
+            return out
+        if self.return_probabilities:
+            return run.probabilities, run.spikes
+        return run.spikes
+
+    @property
+    def weights_FF(self) -> torch.Tensor:
+        return self._weight_matrix(0)
