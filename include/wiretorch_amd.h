@@ -1,0 +1,173 @@
+/* wiretorch_amd.h — C-ABI of the MI355X (gfx950) conductance-LIF hot path.
+ *
+ * The reference (rory-bedford/wiretorch) drives this path from Python with Triton
+ * launches; it has no C/C++ FFI of its own. Each entry point below replaces the
+ * launches named in its comment (file:line in the reference), behind the reference's
+ * unchanged Python contract `conductance/engine.py:71-89` (`simulate`) and its
+ * autograd functions `_FeedforwardScan` (:444-474) / `_RecurrentRun` (:477-544).
+ *
+ * Conventions
+ *  - All pointers are device pointers (hipMalloc / torch CUDA tensors) unless noted;
+ *    sizes are int64_t. Nothing here allocates device memory or synchronises the host.
+ *  - Layouts are the reference's (conductance/kernels.py:20-35):
+ *      v (B,N) f32; g (B,2,S,N) f32 (component 0 = rise, 1 = decay); counter (B,N) i32;
+ *      spikes/prob/v_saved (B,T,N) f32; G_saved (B,T,N,S) f32; held (B,T,N) i8;
+ *      A (K,B,T,N) f32 (pathway activations, recurrent pathways first).
+ *  - dt and surr_scale are device pointers to 0-d f32 tensors (no host sync).
+ *  - Connectivity is passed compressed, by source (see wt_side): the reference's dense
+ *    per-pathway rows (network.py:106-157) are converted by the host once per call.
+ *  - Every entry point takes the hipStream_t to enqueue on and returns a hipError_t
+ *    value as int (0 = success); invalid arguments return hipErrorInvalidValue (1)
+ *    without launching.
+ */
+#ifndef WIRETORCH_AMD_H
+#define WIRETORCH_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* wt_stream_t; /* a hipStream_t */
+
+/* Per-neuron and per-synapse tables of one call (the reference's Physiology,
+ * conductance/dynamics.py:56-92, padded: S <= WT_MAX_S). */
+#define WT_MAX_S 8
+#define WT_MAX_K 8
+typedef struct {
+  const float* theta;    /* (N,) */
+  const float* U_reset;  /* (N,) */
+  const float* E_L;      /* (N,) */
+  const float* C_m;      /* (N,) */
+  const float* beta;     /* (N,) */
+  const int32_t* n_ref;  /* (N,) or NULL: no refractory period */
+  const float* E_syn;    /* (S,) */
+  const float* g_clip;   /* (S,) */
+  const float* decay;    /* (2,S) */
+  const float* jump;     /* (2,S) */
+  const float* made;     /* (K,S) 0/1 */
+  const float* scale;    /* (K,N) */
+  const float* dt;       /* 0-d */
+  const float* surr;     /* 0-d */
+  int64_t N, S, K, K_rec;
+} wt_tables;
+
+/* One input side's connectivity, compressed by source and split by target range.
+ * Source j's synapses onto targets in range r = [r*range_n, (r+1)*range_n) are
+ * edges split[j*(R+1)+r] .. split[j*(R+1)+r+1]-1 (targets ascending); pathway[j] is
+ * the pathway its activation feeds (-1: none). Built by wt_split_ranges. */
+typedef struct {
+  const int64_t* indptr;   /* (n_src+1,) */
+  const int64_t* split;    /* (n_src, R+1) */
+  const int32_t* targets;  /* (E,) */
+  const float* weights;    /* (E,) */
+  const int32_t* pathway;  /* (n_src,) */
+  int64_t n_src;
+} wt_side;
+
+/* Launch geometry of wt_cond_run: groups*R workgroups; group g owns the trials
+ * b = g, g+groups, ...; workgroup slot r of a group owns targets [r*range_n, ...).
+ * frac_bits: activations are accumulated exactly as int64 multiples of 2^-frac_bits. */
+typedef struct {
+  int64_t groups, R, range_n, frac_bits;
+} wt_geometry;
+
+/* wt_split_ranges — (re)build side->split for R target ranges of range_n targets
+ * (binary search of each source's ascending targets). split: (n_src, R+1) int64. */
+int wt_split_ranges(const int64_t* indptr, const int32_t* targets, int64_t n_src,
+                    int64_t R, int64_t range_n, int64_t* split, wt_stream_t stream);
+
+/* wt_cond_run — T steps of the conductance-LIF network, forward.
+ * Replaces: conductance/kernels.py:159-289 scan_forward (feedforward networks,
+ * K_rec = 0) and the per-step pair network_simulators/kernels.py:133-204
+ * compact_spikes + conductance/kernels.py:572-700 recurrent_step launched by the host
+ * loop conductance/engine.py:306-355 — here one persistent launch for all T steps.
+ *   x (B,T,n_in) f32 input; rec/ff: recurrent side (sources = the N neurons) and
+ *   feedforward side (sources = the n_in input columns), rec may have n_src = 0.
+ *   State v, g, counter is updated in place. Outputs: spikes (required); prob,
+ *   v_saved, G_saved, held, A_saved (K,B,T,N) and the tracked v/I/g of trial track_b
+ *   (-1: all) may each be NULL.
+ *   scratch: device workspace of wt_cond_run_scratch_bytes bytes, zeroed by the
+ *   caller before each launch. */
+typedef struct {
+  const float* x;
+  int64_t B, T, n_in;
+  float* v;
+  float* g;
+  int32_t* counter;
+  float* spikes;
+  float* prob;
+  float* v_saved;
+  float* G_saved;
+  int8_t* held;
+  float* A_saved;
+  float* track_v;  /* (Bt,T,N) */
+  float* track_I;  /* (Bt,T,N,S+1) */
+  float* track_g;  /* (Bt,T,N,2,S) */
+  int64_t track_b;
+} wt_run_io;
+
+int64_t wt_cond_run_scratch_bytes(const wt_geometry* geo, int64_t B, int64_t N);
+int wt_cond_run(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
+                const wt_geometry* geo, const wt_run_io* io, void* scratch,
+                wt_stream_t stream);
+
+/* wt_cond_scan_backward — reverse-time adjoint of T steps whose activations A are
+ * known (the recurrent activations treated as input).
+ * Replaces: conductance/kernels.py:383-568 scan_backward (+ _membrane_adjoint
+ * :315-379), launched by conductance/engine.py:358-383.
+ *   Reads grad_spikes, grad_prob (may be NULL), spikes, v_saved, G_saved, held (NULL
+ *   without refractory), A, g_init (NULL unless want_decay). Writes (each may be NULL
+ *   when not wanted) grad_A (K,B,T,N), grad_scale partials (K,B,N), and per-(trial,
+ *   neuron) partials: theta, U_reset, E_L, C_m, beta (B,N); E_syn (B,S,N);
+ *   decay, jump (B,2,S,N). The caller sums the partials over trials. */
+typedef struct {
+  const float* grad_spikes;
+  const float* grad_prob;
+  const float* spikes;
+  const float* v_saved;
+  const float* G_saved;
+  const int8_t* held;
+  const float* A;
+  const float* g_init;
+  int64_t B, T;
+  float* grad_A;
+  float* grad_scale;
+  float* grad_theta;
+  float* grad_reset;
+  float* grad_E_L;
+  float* grad_C_m;
+  float* grad_beta;
+  float* grad_E_syn;
+  float* grad_decay;
+  float* grad_jump;
+} wt_backward_io;
+
+int wt_cond_scan_backward(const wt_tables* tab, const wt_backward_io* io,
+                          wt_stream_t stream);
+
+/* wt_edge_sources — edge_src[e] = the source of edge e (E = indptr[n_src]). */
+int wt_edge_sources(const int64_t* indptr, int64_t n_src, int64_t* edge_src,
+                    wt_stream_t stream);
+
+/* wt_weight_gradient — dL/dW on the connectome's support (its edges), event-driven:
+ * grad_w[e] = sum over the events i of src(e) of ev_val[i] * grad_A[k, ev_bt[i], tgt(e)]
+ * with k = pathway_offset + pathway(src(e)). Events of source j are ev_indptr[j] ..
+ * ev_indptr[j+1]-1; ev_bt = b*T + t ascending, ev_val the presynaptic activity there.
+ * Replaces: network_simulators/engine.py:327-350 weight_gradient (a dense GEMM over
+ * every (source, target) pair, most of whose products are zero); the reference's
+ * learnt projections multiply the gradient by a mask that is zero off the support
+ * (projections.py:164, :216). grad_A (K,B,T,N); grad_w (E,) f32 overwritten. */
+int wt_weight_gradient(const wt_side* side, const int64_t* edge_src, int64_t n_edges,
+                       const int64_t* ev_indptr, const int64_t* ev_bt, const float* ev_val,
+                       const float* grad_A, int64_t B, int64_t T, int64_t N,
+                       int64_t pathway_offset, float* grad_w, wt_stream_t stream);
+
+/* wt_device_info — compute units of the current device (for the geometry). */
+int wt_device_info(int64_t* n_cu, int64_t* max_lds_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WIRETORCH_AMD_H */

@@ -1,0 +1,98 @@
+"""ctypes binding of ``libwiretorch_amd.so`` (declarations: ``include/wiretorch_amd.h``).
+
+The library is built in-tree by ``python -m wiretorch_amd.build``. There is no
+fallback: calling into the engine without the library raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIBRARY = Path(__file__).resolve().parent / "libwiretorch_amd.so"
+
+P = ctypes.c_void_p
+I64 = ctypes.c_int64
+
+
+class Tables(ctypes.Structure):
+    _fields_ = [
+        ("theta", P), ("U_reset", P), ("E_L", P), ("C_m", P), ("beta", P), ("n_ref", P),
+        ("E_syn", P), ("g_clip", P), ("decay", P), ("jump", P), ("made", P), ("scale", P),
+        ("dt", P), ("surr", P), ("N", I64), ("S", I64), ("K", I64), ("K_rec", I64),
+    ]  # fmt: skip
+
+
+class Side(ctypes.Structure):
+    _fields_ = [
+        ("indptr", P), ("split", P), ("targets", P), ("weights", P), ("pathway", P),
+        ("n_src", I64),
+    ]  # fmt: skip
+
+
+class Geometry(ctypes.Structure):
+    _fields_ = [("groups", I64), ("R", I64), ("range_n", I64), ("frac_bits", I64)]
+
+
+class RunIO(ctypes.Structure):
+    _fields_ = [
+        ("x", P), ("B", I64), ("T", I64), ("n_in", I64), ("v", P), ("g", P), ("counter", P),
+        ("spikes", P), ("prob", P), ("v_saved", P), ("G_saved", P), ("held", P),
+        ("A_saved", P), ("track_v", P), ("track_I", P), ("track_g", P), ("track_b", I64),
+    ]  # fmt: skip
+
+
+class BackwardIO(ctypes.Structure):
+    _fields_ = [
+        ("grad_spikes", P), ("grad_prob", P), ("spikes", P), ("v_saved", P),
+        ("G_saved", P), ("held", P), ("A", P), ("g_init", P), ("B", I64), ("T", I64),
+        ("grad_A", P), ("grad_scale", P), ("grad_theta", P), ("grad_reset", P),
+        ("grad_E_L", P), ("grad_C_m", P), ("grad_beta", P), ("grad_E_syn", P),
+        ("grad_decay", P), ("grad_jump", P),
+    ]  # fmt: skip
+
+
+#: Every entry point the header declares, with its ctypes signature.
+SIGNATURES = {
+    "wt_split_ranges": (ctypes.c_int, [P, P, I64, I64, I64, P, P]),
+    "wt_cond_run_scratch_bytes": (I64, [ctypes.POINTER(Geometry), I64, I64]),
+    "wt_cond_run": (ctypes.c_int, [ctypes.POINTER(Tables), ctypes.POINTER(Side),
+                                   ctypes.POINTER(Side), ctypes.POINTER(Geometry),
+                                   ctypes.POINTER(RunIO), P, P]),
+    "wt_cond_scan_backward": (ctypes.c_int, [ctypes.POINTER(Tables),
+                                             ctypes.POINTER(BackwardIO), P]),
+    "wt_edge_sources": (ctypes.c_int, [P, I64, P, P]),
+    "wt_weight_gradient": (ctypes.c_int, [ctypes.POINTER(Side), P, I64, P, P, P, P, I64,
+                                          I64, I64, I64, P, P]),
+    "wt_device_info": (ctypes.c_int, [ctypes.POINTER(I64), ctypes.POINTER(I64)]),
+}  # fmt: skip
+
+_lib = None
+
+
+def load(path: Path = LIBRARY) -> ctypes.CDLL:
+    """The library, loaded once; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not path.exists():
+            raise RuntimeError(
+                f"{path} is missing: build the HIP extension with "
+                "`python -m wiretorch_amd.build` (there is no CPU fallback)"
+            )
+        lib = ctypes.CDLL(str(path))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        raise RuntimeError(f"{what} failed with HIP error {status}")
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a tensor (None for None)."""
+    return None if t is None else t.data_ptr()

@@ -1,0 +1,673 @@
+// wt_kernels.hip — MI355X (gfx950) kernels of the conductance-LIF hot path and their
+// C-ABI (include/wiretorch_amd.h).
+//
+// Forward (wt_cond_run): one persistent launch runs all T steps.
+//   * Workgroups form `groups` groups of R (workgroup i is in group i % groups, slot
+//     i / groups; with 8 groups this is one group per XCD, since the dispatcher places
+//     workgroup i on XCD i % 8). Group g owns trials g, g + groups, ...; slot r owns the
+//     targets [r * range_n, (r + 1) * range_n) of those trials, for the whole run.
+//   * Step t, per workgroup: (A) update the owned neurons — inject step t-1's
+//     activations, spike, membrane, refractory — and list the neurons that fired in a
+//     workgroup-private segment; group barrier; (P) every workgroup walks the group's
+//     fired lists (and the nonzero inputs of step t) and adds the weights of synapses
+//     onto its own targets into an LDS accumulator.
+//   * Accumulation is exact: int64 multiples of 2^-frac_bits (LDS 64-bit atomic adds),
+//     converted to float32 once, so the sum is the exactly rounded one whatever order
+//     the events arrive in — deterministic without float atomics, and only active
+//     synapses are touched.
+//   * Cross-workgroup data (fired lists, their counts, the barrier counter) is moved with
+//     agent-scope atomic loads/stores (coherent at device scope); each thread waits for
+//     its stores to complete before its workgroup arrives at the barrier.
+//     Per-XCD groups keep the barrier to R arrivals per counter (≈0.8 µs measured for 32
+//     workgroups, against ≈3.7 µs for one device-wide counter of 256).
+// Backward (wt_cond_scan_backward): one thread per (trial, neuron), reverse time loop,
+// the adjoint state in registers.
+// Weight gradient (wt_weight_gradient): one thread per synapse, summing over the
+// (trial, step) events of its source.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/wiretorch_amd.h"
+#include "wt_math.h"
+
+namespace wt {
+
+constexpr int kRunBlock = 1024;
+constexpr int kMaxGroups = 64;
+
+struct RunArgs {
+  wt_tables tab;
+  wt_side rec, ff;
+  wt_geometry geo;
+  wt_run_io io;
+  // scratch
+  uint32_t* err;        // [0]: error flags
+  uint32_t* barrier;    // one counter per group, 128 bytes apart
+  int32_t* fired;       // [2][wgs][tpg_max][range_n]
+  int32_t* fired_count; // [2][wgs][tpg_max]
+  int64_t tpg_max;
+};
+
+__device__ inline void store_agent(int32_t* p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline int32_t load_agent(const int32_t* p) {
+  return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Group barrier: every thread's stores complete, then one arrival per workgroup on
+// the group's counter; the wait is bounded (2 s of wall clock) and gives up as soon as
+// any workgroup has flagged an error. Returns false on error.
+__device__ inline bool group_barrier(uint32_t* counter, uint32_t target, uint32_t* err,
+                                     uint32_t* s_flag) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t bad = 0;
+    __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint64_t start = wall_clock64();
+    uint32_t polls = 0;
+    while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      __builtin_amdgcn_s_sleep(1);
+      if ((++polls & 63u) == 0) {
+        if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) { bad = 1; break; }
+        if (wall_clock64() - start > 200000000ull) {  // 2 s at the 100 MHz wall clock
+          __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          bad = 1;
+          break;
+        }
+      }
+    }
+    *s_flag = bad;
+  }
+  __syncthreads();
+  return *s_flag == 0;
+}
+
+template <int S>
+__device__ inline void load_synapses(const wt_tables& tab, Synapses<S>& syn) {
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    syn.E[s] = tab.E_syn[s];
+    syn.clip[s] = tab.g_clip[s];
+    syn.decay_r[s] = tab.decay[s];
+    syn.decay_d[s] = tab.decay[S + s];
+    syn.jump_r[s] = tab.jump[s];
+    syn.jump_d[s] = tab.jump[S + s];
+  }
+}
+
+// Adds the synapses of `edges` [e0, e1) onto this workgroup's targets (local index
+// target - lo) of pathway k, trial slot q, to the LDS accumulator.
+__device__ inline void push_edges(long long* acc, const wt_side& side, int64_t e0,
+                                  int64_t e1, int64_t lo, int64_t slot_base, float value,
+                                  float fscale) {
+  if (value == 1.0f) {
+    for (int64_t e = e0; e < e1; ++e) {
+      int64_t t = side.targets[e] - lo;
+      atomicAdd(reinterpret_cast<unsigned long long*>(acc + slot_base + t),
+                (unsigned long long)to_fixed(side.weights[e], fscale));
+    }
+  } else {
+    for (int64_t e = e0; e < e1; ++e) {
+      int64_t t = side.targets[e] - lo;
+      atomicAdd(reinterpret_cast<unsigned long long*>(acc + slot_base + t),
+                (unsigned long long)to_fixed(value * side.weights[e], fscale));
+    }
+  }
+}
+
+template <int S>
+__global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
+  extern __shared__ long long acc[];  // [K][tpg][range_n]
+  __shared__ int32_t s_fcnt[64];
+  __shared__ int32_t s_pre[64 * 65];  // per trial slot: prefix of the R fired counts
+  __shared__ uint32_t s_flag;
+
+  const wt_tables& tab = A.tab;
+  const int64_t groups = A.geo.groups, R = A.geo.R, range_n = A.geo.range_n;
+  const int64_t N = tab.N, K = tab.K, K_rec = tab.K_rec, B = A.io.B, T = A.io.T;
+  const int64_t wg = blockIdx.x;
+  const int64_t g = wg % groups, r = wg / groups;
+  const int64_t tpg = g < B ? (B - g + groups - 1) / groups : 0;
+  if (tpg == 0) return;  // no trial in this group: it takes part in nothing
+  const int64_t lo = r * range_n;
+  const int64_t nr = lo < N ? (N - lo < range_n ? N - lo : range_n) : 0;
+  const int64_t items = tpg * nr;
+  const int64_t acc_len = K * tpg * range_n;
+  const bool refractory = tab.n_ref != nullptr;
+  const bool recurrent = K_rec > 0 && A.rec.n_src > 0;
+  const float dt = *tab.dt;
+  const float fscale = ldexpf(1.0f, (int)A.geo.frac_bits);
+  const float inv_fscale = ldexpf(1.0f, -(int)A.geo.frac_bits);
+  const wt_run_io& io = A.io;
+  Synapses<S> syn;
+  load_synapses<S>(tab, syn);
+
+  for (int64_t i = threadIdx.x; i < acc_len; i += blockDim.x) acc[i] = 0;
+  __syncthreads();
+
+  uint32_t* my_barrier = A.barrier + g * 32;
+  const int64_t fstride = A.tpg_max * range_n;  // one workgroup's fired segment
+  const int64_t wgs = groups * R;
+
+  for (int64_t t = 0; t <= T; ++t) {
+    const int buf = (int)(t & 1);
+    if (threadIdx.x < 64) s_fcnt[threadIdx.x] = 0;
+    __syncthreads();
+    int32_t* my_fired = A.fired + ((int64_t)buf * wgs + wg) * fstride;
+
+    // ---------------- (A) update the owned neurons ----------------
+    for (int64_t it = threadIdx.x; it < items; it += blockDim.x) {
+      const int64_t q = it / nr, ln = it - q * nr, n = lo + ln;
+      const int64_t b = g + q * groups;
+      const int64_t bn = b * N + n;
+      float v = io.v[bn];
+      float gr[S], gd[S];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        gr[s] = io.g[(b * 2 * S + s) * N + n];
+        gd[s] = io.g[(b * 2 * S + S + s) * N + n];
+      }
+      if (t > 0) {
+        // g <- g * decay, then each pathway's activation times its kernel, in order
+        // (dynamics.py:206-208; kernel = jump * scale * made, dynamics.py:95-100).
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          gr[s] = gr[s] * syn.decay_r[s];
+          gd[s] = gd[s] * syn.decay_d[s];
+        }
+        for (int64_t k = 0; k < K; ++k) {
+          long long* cell = acc + (k * tpg + q) * range_n + ln;
+          const float a = from_fixed(*cell, inv_fscale);
+          *cell = 0;
+          if (io.A_saved) io.A_saved[((k * B + b) * T + (t - 1)) * N + n] = a;
+          const float sc = tab.scale[k * N + n];
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            if (tab.made[k * S + s] != 0.0f) {
+              gr[s] = gr[s] + a * (syn.jump_r[s] * sc * tab.made[k * S + s]);
+              gd[s] = gd[s] + a * (syn.jump_d[s] * sc * tab.made[k * S + s]);
+            }
+          }
+        }
+        if (io.track_g && (io.track_b < 0 || io.track_b == b)) {
+          const int64_t bt = io.track_b < 0 ? b : 0;
+          float* out = io.track_g + ((bt * T + (t - 1)) * N + n) * 2 * S;
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            out[s] = gr[s];
+            out[S + s] = gd[s];
+          }
+        }
+      }
+      if (t < T) {
+        const float theta = tab.theta[n];
+        int32_t counter = refractory ? io.counter[bn] : 0;
+        float r_hold, held;
+        const float s_out = spike_step(v, theta, counter, refractory ? tab.n_ref[n] : 0,
+                                       refractory, r_hold, held);
+        const int64_t out = (b * T + t) * N + n;
+        io.spikes[out] = s_out;
+        if (io.prob) {
+          float p = 1.0f / (1.0f + expf(-(*tab.surr * (v - theta))));
+          io.prob[out] = refractory ? p * (1.0f - held) : p;
+        }
+        const Leak lk = leak(tab.C_m[n], tab.beta[n], dt);
+        float G[S], I[S], I_leak;
+        const float v_next = membrane<S>(v, r_hold, gr, gd, syn, tab.E_L[n], tab.C_m[n],
+                                         tab.U_reset[n], lk, dt, G, I, I_leak);
+        if (io.v_saved) {
+          io.v_saved[out] = v;
+#pragma unroll
+          for (int s = 0; s < S; ++s) io.G_saved[out * S + s] = G[s];
+          if (refractory && io.held) io.held[out] = (int8_t)(held != 0.0f);
+        }
+        if (io.track_v && (io.track_b < 0 || io.track_b == b)) {
+          const int64_t bt = io.track_b < 0 ? b : 0;
+          const int64_t row = (bt * T + t) * N + n;
+          io.track_v[row] = v_next;
+#pragma unroll
+          for (int s = 0; s < S; ++s) io.track_I[row * (S + 1) + s] = I[s];
+          io.track_I[row * (S + 1) + S] = I_leak;
+        }
+        if (recurrent && s_out != 0.0f && A.rec.pathway[n] >= 0) {
+          const int32_t pos = atomicAdd(&s_fcnt[q], 1);
+          store_agent(my_fired + q * range_n + pos, (int32_t)n);
+        }
+        v = v_next;
+        if (refractory) io.counter[bn] = counter;
+      }
+      io.v[bn] = v;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        io.g[(b * 2 * S + s) * N + n] = gr[s];
+        io.g[(b * 2 * S + S + s) * N + n] = gd[s];
+      }
+    }
+    if (t == T) break;
+
+    // ---------------- publish the fired lists; group barrier ----------------
+    if (recurrent) {
+      __syncthreads();
+      int32_t* my_count = A.fired_count + ((int64_t)buf * wgs + wg) * A.tpg_max;
+      if (threadIdx.x < tpg) store_agent(my_count + threadIdx.x, s_fcnt[threadIdx.x]);
+      if (!group_barrier(my_barrier, (uint32_t)((t + 1) * R), A.err, &s_flag)) return;
+      // prefix of the fired counts of the group's R workgroups, per trial slot
+      for (int64_t q = threadIdx.x; q < tpg; q += blockDim.x) {
+        int32_t run = 0;
+        for (int64_t rr = 0; rr < R; ++rr) {
+          s_pre[q * 65 + rr] = run;
+          run += load_agent(A.fired_count + ((int64_t)buf * wgs + g + rr * groups) * A.tpg_max + q);
+        }
+        s_pre[q * 65 + R] = run;
+      }
+    }
+    __syncthreads();
+
+    // ---------------- (P) push step t's events onto the owned targets ----------------
+    if (recurrent) {
+      for (int64_t q = 0; q < tpg; ++q) {
+        const int32_t total = s_pre[q * 65 + R];
+        for (int32_t f = threadIdx.x; f < total; f += blockDim.x) {
+          int32_t a = 0, z = (int32_t)R;  // find rr with pre[rr] <= f < pre[rr+1]
+          while (z - a > 1) {
+            int32_t m = (a + z) >> 1;
+            if (s_pre[q * 65 + m] <= f) a = m; else z = m;
+          }
+          const int64_t src_wg = g + (int64_t)a * groups;
+          const int32_t j = load_agent(A.fired + ((int64_t)buf * wgs + src_wg) * fstride +
+                                       q * range_n + (f - s_pre[q * 65 + a]));
+          const int32_t k = A.rec.pathway[j];
+          const int64_t* sp = A.rec.split + (int64_t)j * (R + 1) + r;
+          push_edges(acc, A.rec, sp[0], sp[1], lo, (k * tpg + q) * range_n, 1.0f, fscale);
+        }
+      }
+    }
+    if (A.ff.n_src > 0) {
+      const int64_t n_in = io.n_in;
+      for (int64_t q = 0; q < tpg; ++q) {
+        const int64_t b = g + q * groups;
+        const float* xrow = io.x + (b * T + t) * n_in;
+        for (int64_t j = threadIdx.x; j < n_in; j += blockDim.x) {
+          const float xv = xrow[j];
+          if (xv == 0.0f) continue;
+          const int32_t k = A.ff.pathway[j];
+          if (k < 0) continue;
+          const int64_t* sp = A.ff.split + j * (R + 1) + r;
+          push_edges(acc, A.ff, sp[0], sp[1], lo, ((K_rec + k) * tpg + q) * range_n, xv, fscale);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Ranges of each source's ascending targets: split[j][r] = first edge with target >=
+// r * range_n (r = 0..R), by binary search.
+__global__ void split_ranges_kernel(const int64_t* indptr, const int32_t* targets,
+                                    int64_t n_src, int64_t R, int64_t range_n,
+                                    int64_t* split) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n_src * (R + 1)) return;
+  const int64_t j = i / (R + 1), rr = i - j * (R + 1);
+  const int64_t bound = rr * range_n;
+  int64_t a = indptr[j], z = indptr[j + 1];
+  while (a < z) {
+    int64_t m = (a + z) >> 1;
+    if ((int64_t)targets[m] < bound) a = m + 1; else z = m;
+  }
+  split[i] = a;
+}
+
+// ---------------------------------------------------------------------------------
+// Backward: one thread per (trial, neuron), steps t = T-1 .. 0.
+struct BackArgs {
+  wt_tables tab;
+  wt_backward_io io;
+};
+
+template <int S>
+__global__ __launch_bounds__(256) void cond_backward_kernel(BackArgs P) {
+  const wt_tables& tab = P.tab;
+  const wt_backward_io& io = P.io;
+  const int64_t N = tab.N, K = tab.K, B = io.B, T = io.T;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= B * N) return;
+  const int64_t b = idx / N, n = idx - b * N;
+  const float dt = *tab.dt, k_surr = *tab.surr;
+  Synapses<S> syn;
+  load_synapses<S>(tab, syn);
+  const float theta = tab.theta[n], E_L = tab.E_L[n], C_m = tab.C_m[n], beta = tab.beta[n];
+  const Leak lk = leak(C_m, beta, dt);
+  const bool refractory = io.held != nullptr;
+  const bool want_A = io.grad_A != nullptr, want_scale = io.grad_scale != nullptr;
+  const bool want_decay = io.grad_decay != nullptr, want_jump = io.grad_jump != nullptr;
+  const bool want_E = io.grad_E_syn != nullptr;
+
+  float dv = 0.0f;
+  float lr[S], ld[S], Hr[S], Hd[S], accE[S], accDr[S], accDd[S], accJr[S], accJd[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    lr[s] = ld[s] = Hr[s] = Hd[s] = accE[s] = accDr[s] = accDd[s] = accJr[s] = accJd[s] = 0.0f;
+  }
+  float acc_scale[WT_MAX_K];
+  for (int k = 0; k < WT_MAX_K; ++k) acc_scale[k] = 0.0f;
+  float acc_theta = 0.0f, acc_reset = 0.0f, acc_EL = 0.0f, acc_Cm = 0.0f, acc_beta = 0.0f;
+
+  for (int64_t t = T - 1; t >= 0; --t) {
+    const int64_t out = (b * T + t) * N + n;
+    const float v = io.v_saved[out];
+    const float s_sp = io.spikes[out];
+    const float held = refractory ? (float)io.held[out] : 0.0f;
+    const float r = refractory ? fmaxf(s_sp, held) : s_sp;
+    float G[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) G[s] = io.G_saved[out * S + s];
+
+    // Injections of step t: per unit jump, sum_k a_k scale_k made_k (jump, decay).
+    if (want_decay || want_jump) {
+      float base[S];
+#pragma unroll
+      for (int s = 0; s < S; ++s) base[s] = 0.0f;
+      for (int64_t k = 0; k < K; ++k) {
+        const float as = io.A[((k * B + b) * T + t) * N + n] * tab.scale[k * N + n];
+#pragma unroll
+        for (int s = 0; s < S; ++s) base[s] += as * tab.made[k * S + s];
+      }
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        if (want_jump) {
+          accJr[s] += lr[s] * base[s];
+          accJd[s] += ld[s] * base[s];
+        }
+        if (want_decay) {
+          accDr[s] += syn.jump_r[s] * base[s] * Hr[s];
+          accDd[s] += syn.jump_d[s] * base[s] * Hd[s];
+          Hr[s] = lr[s] + syn.decay_r[s] * Hr[s];
+          Hd[s] = ld[s] + syn.decay_d[s] * Hd[s];
+        }
+      }
+    }
+    // dL/da_k of step t: the adjoint of the conductances it was injected into.
+#pragma unroll
+    for (int k = 0; k < WT_MAX_K; ++k) {
+      if (k >= K) break;
+      float qk = 0.0f;
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+        qk += (syn.jump_r[s] * lr[s] + syn.jump_d[s] * ld[s]) * tab.made[k * S + s];
+      const int64_t ka = ((k * B + b) * T + t) * N + n;
+      if (want_A) io.grad_A[ka] = qk * tab.scale[k * N + n];
+      if (want_scale) acc_scale[k] += qk * io.A[ka];
+    }
+    // Membrane.
+    const float gx = dv * (1.0f - r);
+    float dG[S], Gc[S];
+    const MembraneAdjoint m = membrane_adjoint<S>(gx, v, G, syn, E_L, C_m, lk, dt, dG, Gc);
+    acc_reset += dv * r;
+    acc_EL += gx * m.phi * lk.g_L;
+    if (io.grad_C_m || io.grad_beta) {
+      const float g_v = v - E_L;
+      if (io.grad_C_m) {  // g_L = C rate and a both depend on C
+        const float inv_C = 1.0f / C_m;
+        const float dphi = -(m.a * dt * m.Gt * inv_C * inv_C + m.phi * lk.g_L * inv_C) * m.inv_g;
+        acc_Cm -= gx * (dphi * m.J + m.phi * g_v * lk.g_L * inv_C);
+      }
+      if (io.grad_beta) {  // rate = -log(beta) / dt
+        const float dg_L = -C_m / (beta * dt);
+        const float dphi = -(m.a / beta + m.phi * dg_L) * m.inv_g;
+        acc_beta -= gx * (dphi * m.J + m.phi * g_v * dg_L);
+      }
+    }
+    if (want_E) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) accE[s] += gx * m.phi * Gc[s];
+    }
+    dv = m.dv;
+    // Spike (and probability) of step t, both functions of v - theta.
+    const float x = v - theta;
+    float g_x = surrogate(x, io.grad_spikes[out], k_surr);
+    if (io.grad_prob) {
+      const float p = 1.0f / (1.0f + expf(-(k_surr * x)));
+      g_x += io.grad_prob[out] * k_surr * p * (1.0f - p);
+    }
+    if (refractory) g_x *= 1.0f - held;
+    dv += g_x;
+    acc_theta -= g_x;
+    // Conductances decay into step t+1 and feed the currents of step t.
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      lr[s] = lr[s] * syn.decay_r[s] + dG[s];
+      ld[s] = ld[s] * syn.decay_d[s] + dG[s];
+    }
+  }
+  if (want_scale) {
+#pragma unroll
+    for (int k = 0; k < WT_MAX_K; ++k)
+      if (k < K) io.grad_scale[k * B * N + idx] = acc_scale[k];
+  }
+  if (io.grad_theta) io.grad_theta[idx] = acc_theta;
+  if (io.grad_reset) io.grad_reset[idx] = acc_reset;
+  if (io.grad_E_L) io.grad_E_L[idx] = acc_EL;
+  if (io.grad_C_m) io.grad_C_m[idx] = acc_Cm;
+  if (io.grad_beta) io.grad_beta[idx] = acc_beta;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    if (want_E) io.grad_E_syn[(b * S + s) * N + n] = accE[s];
+    if (want_jump) {
+      io.grad_jump[(b * 2 * S + s) * N + n] = accJr[s];
+      io.grad_jump[(b * 2 * S + S + s) * N + n] = accJd[s];
+    }
+    if (want_decay) {  // the conductances entering the chunk
+      const float gr0 = io.g_init[(b * 2 * S + s) * N + n];
+      const float gd0 = io.g_init[(b * 2 * S + S + s) * N + n];
+      io.grad_decay[(b * 2 * S + s) * N + n] = accDr[s] + gr0 * Hr[s];
+      io.grad_decay[(b * 2 * S + S + s) * N + n] = accDd[s] + gd0 * Hd[s];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Weight gradient on the support: one thread per synapse; it walks its source's
+// events (the (trial, step) where the source was active, ascending) and sums the
+// target's dL/da of that step.
+__global__ void weight_gradient_kernel(wt_side side, const int64_t* edge_src, int64_t E,
+                                       const int64_t* ev_indptr, const int64_t* ev_bt,
+                                       const float* ev_val, const float* grad_A, int64_t BT,
+                                       int64_t N, int64_t k0, float* grad_w) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  const int64_t j = edge_src[e];
+  const int32_t k = side.pathway[j];
+  float sum = 0.0f;
+  if (k >= 0) {
+    const int64_t n = side.targets[e];
+    const float* gA = grad_A + (k0 + k) * BT * N + n;
+    for (int64_t i = ev_indptr[j]; i < ev_indptr[j + 1]; ++i) sum += ev_val[i] * gA[ev_bt[i] * N];
+  }
+  grad_w[e] = sum;
+}
+
+__global__ void edge_source_kernel(const int64_t* indptr, int64_t n_src, int64_t* edge_src) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= n_src) return;
+  for (int64_t e = indptr[j]; e < indptr[j + 1]; ++e) edge_src[e] = j;
+}
+
+}  // namespace wt
+
+// ===================================================================================
+// C-ABI
+// ===================================================================================
+using namespace wt;
+
+template <template <int> class F, typename... Args>
+static hipError_t dispatch_S(int64_t S, Args&&... args) {
+  switch (S) {
+    case 1: return F<1>::run(args...);
+    case 2: return F<2>::run(args...);
+    case 3: return F<3>::run(args...);
+    case 4: return F<4>::run(args...);
+    case 5: return F<5>::run(args...);
+    case 6: return F<6>::run(args...);
+    case 7: return F<7>::run(args...);
+    case 8: return F<8>::run(args...);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+static int64_t run_tpg_max(const wt_geometry* geo, int64_t B) {
+  return (B + geo->groups - 1) / geo->groups;
+}
+
+extern "C" int64_t wt_cond_run_scratch_bytes(const wt_geometry* geo, int64_t B, int64_t N) {
+  (void)N;
+  const int64_t wgs = geo->groups * geo->R, tpg = run_tpg_max(geo, B);
+  int64_t bytes = 256;                                    // error flags
+  bytes += geo->groups * 128;                             // barrier counters
+  bytes += 2 * wgs * tpg * geo->range_n * 4;              // fired segments
+  bytes += 2 * wgs * tpg * 4;                             // fired counts
+  return bytes;
+}
+
+template <int S>
+struct RunLaunch {
+  static hipError_t run(RunArgs& a, size_t lds, int block, hipStream_t stream, bool coop) {
+    const void* fn = reinterpret_cast<const void*>(&cond_run_kernel<S>);
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    dim3 grid((unsigned)(a.geo.groups * a.geo.R)), blk((unsigned)block);
+    void* params[] = {&a};
+    if (coop) return hipLaunchCooperativeKernel(fn, grid, blk, params, (unsigned)lds, stream);
+    hipLaunchKernelGGL(cond_run_kernel<S>, grid, blk, lds, stream, a);
+    return hipGetLastError();
+  }
+};
+
+extern "C" int wt_cond_run(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
+                           const wt_geometry* geo, const wt_run_io* io, void* scratch,
+                           wt_stream_t stream) {
+  if (!tab || !rec || !ff || !geo || !io || !scratch || !io->spikes || !io->v || !io->g)
+    return hipErrorInvalidValue;
+  if (tab->n_ref && !io->counter) return hipErrorInvalidValue;
+  if (tab->S < 1 || tab->S > WT_MAX_S || tab->K < 0 || tab->K > WT_MAX_K || tab->K_rec > tab->K)
+    return hipErrorInvalidValue;
+  if (geo->groups < 1 || geo->groups > kMaxGroups || geo->R < 1 || geo->R > 64 ||
+      geo->range_n < 1 || geo->R * geo->range_n < tab->N || geo->frac_bits < 0 ||
+      geo->frac_bits > 60)
+    return hipErrorInvalidValue;
+  const int64_t tpg = run_tpg_max(geo, io->B);
+  if (tpg > 64 || io->B < 1 || io->T < 0) return hipErrorInvalidValue;
+  if ((io->v_saved != nullptr) != (io->G_saved != nullptr)) return hipErrorInvalidValue;
+  if (io->track_v && (!io->track_I || !io->track_g)) return hipErrorInvalidValue;
+  if (rec->n_src > 0 && rec->n_src != tab->N) return hipErrorInvalidValue;
+  if (ff->n_src > 0 && ff->n_src != io->n_in) return hipErrorInvalidValue;
+  if (io->T == 0) return hipSuccess;
+
+  RunArgs a;
+  a.tab = *tab;
+  a.rec = *rec;
+  a.ff = *ff;
+  a.geo = *geo;
+  a.io = *io;
+  a.tpg_max = tpg;
+  char* base = static_cast<char*>(scratch);
+  a.err = reinterpret_cast<uint32_t*>(base);
+  a.barrier = reinterpret_cast<uint32_t*>(base + 256);
+  a.fired = reinterpret_cast<int32_t*>(base + 256 + geo->groups * 128);
+  a.fired_count = a.fired + 2 * geo->groups * geo->R * tpg * geo->range_n;
+
+  const size_t lds = (size_t)(tab->K > 0 ? tab->K : 1) * tpg * geo->range_n * sizeof(long long);
+  int dev = 0, max_lds = 0;
+  hipError_t qe = hipGetDevice(&dev);
+  if (qe == hipSuccess)
+    qe = hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+  if (qe != hipSuccess) return qe;
+  const size_t static_lds = 64 * 4 + 64 * 65 * 4 + 16;
+  if (lds + static_lds > (size_t)max_lds) return hipErrorInvalidValue;
+  const int64_t per_wg = tpg * geo->range_n;
+  int block = per_wg >= kRunBlock ? kRunBlock : (int)(((per_wg + 63) / 64) * 64);
+  if (block < 64) block = 64;
+  const bool coop = tab->K_rec > 0 && rec->n_src > 0 && geo->R > 1;
+  return dispatch_S<RunLaunch>(tab->S, a, lds, block, (hipStream_t)stream, coop);
+}
+
+extern "C" int wt_split_ranges(const int64_t* indptr, const int32_t* targets, int64_t n_src,
+                               int64_t R, int64_t range_n, int64_t* split, wt_stream_t stream) {
+  if (n_src < 0 || R < 1 || range_n < 1) return hipErrorInvalidValue;
+  const int64_t total = n_src * (R + 1);
+  if (total == 0) return hipSuccess;
+  if (!split || !indptr || !targets) return hipErrorInvalidValue;
+  const int block = 256;
+  hipLaunchKernelGGL(split_ranges_kernel, dim3((unsigned)((total + block - 1) / block)),
+                     dim3(block), 0, (hipStream_t)stream, indptr, targets, n_src, R,
+                     range_n, split);
+  return hipGetLastError();
+}
+
+template <int S>
+struct BackLaunch {
+  static hipError_t run(BackArgs& a, hipStream_t stream) {
+    const int64_t total = a.io.B * a.tab.N;
+    const int block = 256;
+    hipLaunchKernelGGL(cond_backward_kernel<S>, dim3((unsigned)((total + block - 1) / block)),
+                       dim3(block), 0, stream, a);
+    return hipGetLastError();
+  }
+};
+
+extern "C" int wt_cond_scan_backward(const wt_tables* tab, const wt_backward_io* io,
+                                     wt_stream_t stream) {
+  if (!tab || !io || !io->grad_spikes || !io->spikes || !io->v_saved || !io->G_saved)
+    return hipErrorInvalidValue;
+  if (tab->S < 1 || tab->S > WT_MAX_S || tab->K < 0 || tab->K > WT_MAX_K)
+    return hipErrorInvalidValue;
+  if ((io->grad_decay || io->grad_jump || io->grad_scale) && !io->A) return hipErrorInvalidValue;
+  if (io->grad_decay && !io->g_init) return hipErrorInvalidValue;
+  if (io->B * tab->N == 0 || io->T == 0) return hipSuccess;
+  BackArgs a;
+  a.tab = *tab;
+  a.io = *io;
+  return dispatch_S<BackLaunch>(tab->S, a, (hipStream_t)stream);
+}
+
+extern "C" int wt_edge_sources(const int64_t* indptr, int64_t n_src, int64_t* edge_src,
+                               wt_stream_t stream) {
+  if (!indptr || !edge_src || n_src < 0) return hipErrorInvalidValue;
+  if (n_src == 0) return hipSuccess;
+  const int block = 256;
+  hipLaunchKernelGGL(edge_source_kernel, dim3((unsigned)((n_src + block - 1) / block)),
+                     dim3(block), 0, (hipStream_t)stream, indptr, n_src, edge_src);
+  return hipGetLastError();
+}
+
+extern "C" int wt_weight_gradient(const wt_side* side, const int64_t* edge_src, int64_t n_edges,
+                                  const int64_t* ev_indptr, const int64_t* ev_bt,
+                                  const float* ev_val, const float* grad_A, int64_t B,
+                                  int64_t T, int64_t N, int64_t pathway_offset, float* grad_w,
+                                  wt_stream_t stream) {
+  if (!side || !edge_src || !ev_indptr || !ev_bt || !ev_val || !grad_A || !grad_w ||
+      pathway_offset < 0 || n_edges < 0)
+    return hipErrorInvalidValue;
+  if (n_edges == 0) return hipSuccess;
+  const int block = 256;
+  hipLaunchKernelGGL(weight_gradient_kernel, dim3((unsigned)((n_edges + block - 1) / block)),
+                     dim3(block), 0, (hipStream_t)stream, *side, edge_src, n_edges, ev_indptr,
+                     ev_bt, ev_val, grad_A, B * T, N, pathway_offset, grad_w);
+  return hipGetLastError();
+}
+
+extern "C" int wt_device_info(int64_t* n_cu, int64_t* max_lds_bytes) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  int cu = 0, lds = 0;
+  e = hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+  if (e != hipSuccess) return e;
+  if (n_cu) *n_cu = cu;
+  if (max_lds_bytes) *max_lds_bytes = lds;
+  return hipSuccess;
+}

@@ -1,0 +1,150 @@
+// wt_math.h — per-neuron conductance-LIF arithmetic for gfx950, in the reference's
+// operation order.
+//
+// The reference step is conductance/dynamics.py:103-143 (+ network.py:294-318): the
+// forward functions below evaluate it in float32 with the same association as torch's
+// CPU kernels (no fused multiply-add: this file is compiled with -ffp-contract=off),
+// so that spike decisions agree with the reference bit for bit unless a voltage lies
+// within rounding of threshold. The adjoint follows from differentiating those
+// equations (the autograd graph of dynamics.py, whose values the reference's
+// conductance/kernels.py:315-379 also reproduces).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wt {
+
+// A short row summed the way torch's CPU reduction associates it (checked against
+// torch for rows of up to five): four interleaved partial sums, then combined in order.
+template <int S>
+__host__ __device__ inline float row_sum(const float (&a)[S]) {
+  constexpr int L = S < 4 ? S : 4;
+  float acc[L];
+#pragma unroll
+  for (int i = 0; i < L; ++i) acc[i] = a[i];
+#pragma unroll
+  for (int i = L; i < S; ++i) acc[i % 4] = acc[i % 4] + a[i];
+  float out = acc[0];
+#pragma unroll
+  for (int i = 1; i < L; ++i) out = out + acc[i];
+  return out;
+}
+
+struct Leak {
+  float rate;  // 1 / tau_mem, from beta precisely (log1p: beta is close to 1)
+  float g_L;   // C_m * rate
+};
+
+__host__ __device__ inline Leak leak(float C_m, float beta, float dt) {
+  float rate = -log1pf(beta - 1.0f) / dt;
+  return {rate, C_m * rate};
+}
+
+// Synapse tables of one call, held by every thread (S entries each).
+template <int S>
+struct Synapses {
+  float E[S], clip[S], decay_r[S], decay_d[S], jump_r[S], jump_d[S];
+};
+
+// Spike and refractory part of a step (dynamics.py:103-107, network.py:294-318):
+// returns the spike; r is what holds the voltage at reset, held the refractory mask.
+__host__ __device__ inline float spike_step(float v, float theta, int32_t& counter,
+                                            int32_t n_ref, bool refractory, float& r,
+                                            float& held) {
+  float s = (v - theta) > 0.0f ? 1.0f : 0.0f;
+  if (refractory) {
+    held = counter > 0 ? 1.0f : 0.0f;
+    s = s * (1.0f - held);
+    r = fmaxf(s, held);
+    counter = s > 0.0f ? n_ref : (counter - 1 > 0 ? counter - 1 : 0);
+  } else {
+    held = 0.0f;
+    r = s;
+  }
+  return s;
+}
+
+// The exponential-Euler membrane step (dynamics.py:127-142). G (summed rise + decay
+// per synapse type, before clipping) and the currents are returned for saving and
+// tracking.
+template <int S>
+__host__ __device__ inline float membrane(float v, float r, const float (&gr)[S],
+                                          const float (&gd)[S], const Synapses<S>& syn,
+                                          float E_L, float C_m, float U_reset, Leak lk,
+                                          float dt, float (&G)[S], float (&I)[S],
+                                          float& I_leak) {
+  float Gc[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    G[s] = gr[s] + gd[s];
+    Gc[s] = fminf(fmaxf(G[s], 0.0f), syn.clip[s]);
+    I[s] = Gc[s] * (v - syn.E[s]);
+  }
+  I_leak = lk.g_L * (v - E_L);
+  float Gt = row_sum<S>(Gc);
+  float J = row_sum<S>(I) + I_leak;
+  float x = dt * lk.rate + dt * Gt / C_m;
+  float step = -expm1f(-x) / (lk.g_L + Gt);
+  return (v - step * J) * (1.0f - r) + U_reset * r;
+}
+
+// One step of the adjoint through the membrane update, given gx = dL/dv_next * (1 - r):
+// returns dL/dv (membrane part) and writes dL/dG_s (through the clip) to dG.
+// Differentiating v_next = v - phi(Gt) J(v, Gc) with phi = (1 - a) / (g_L + Gt),
+// a = exp(-x), x = dt (rate + Gt / C_m):
+//   d v_next / d v   = a                      (J' = g_L + Gt, 1 - phi (g_L + Gt) = a)
+//   d v_next / d Gc_s = -(phi_G J + phi (v - E_s)),  phi_G = (a dt / C_m - phi) / (g_L + Gt)
+// and the physiology terms below.
+struct MembraneAdjoint {
+  float dv;      // dL/dv entering the step (membrane part)
+  float phi, a, inv_g, J, Gt;
+};
+
+template <int S>
+__host__ __device__ inline MembraneAdjoint membrane_adjoint(
+    float gx, float v, const float (&G)[S], const Synapses<S>& syn, float E_L, float C_m,
+    Leak lk, float dt, float (&dG)[S], float (&Gc_out)[S]) {
+  float Gc[S], I[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    Gc[s] = fminf(fmaxf(G[s], 0.0f), syn.clip[s]);
+    I[s] = Gc[s] * (v - syn.E[s]);
+    Gc_out[s] = Gc[s];
+  }
+  float Gt = row_sum<S>(Gc);
+  float J = row_sum<S>(I) + lk.g_L * (v - E_L);
+  float x = dt * lk.rate + dt * Gt / C_m;
+  float em = expm1f(-x);
+  float a = 1.0f + em;
+  float inv_g = 1.0f / (lk.g_L + Gt);
+  float phi = -em * inv_g;
+  float phi_G = (a * dt / C_m - phi) * inv_g;
+  float k0 = -gx * (phi_G * J + phi * v);
+  float k1 = gx * phi;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    float d = k0 + k1 * syn.E[s];
+    // torch: clamp(min=0) passes the gradient where G >= 0; minimum(., clip) splits it
+    // evenly where G == clip.
+    float pass = G[s] < syn.clip[s] ? 1.0f : (G[s] == syn.clip[s] ? 0.5f : 0.0f);
+    dG[s] = G[s] >= 0.0f ? d * pass : 0.0f;
+  }
+  return {gx * a, phi, a, inv_g, J, Gt};
+}
+
+// Surrogate gradient of the spike at x = v - theta (surrogate_gradients.py:30-33).
+__host__ __device__ inline float surrogate(float x, float grad, float k) {
+  float d = k * fabsf(x) + 1.0f;
+  return grad / (d * d);
+}
+
+// Exact fixed-point accumulation of activations: multiples of 2^-frac.
+__device__ inline long long to_fixed(float w, float scale) {
+  return (long long)rintf(w * scale);
+}
+__device__ inline float from_fixed(long long q, float inv_scale) {
+  return (float)q * inv_scale;
+}
+
+}  // namespace wt

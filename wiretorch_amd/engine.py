@@ -1,5 +1,576 @@
-"""Placeholder, replaced by the HIP engine."""
+"""The HIP engine: ``simulate`` and its autograd function, over ``libwiretorch_amd.so``.
+
+``simulate(v, g, x, drive, p, *, refractory, ..., probabilities, track, track_batch_idx,
+retain) -> Run`` keeps the reference's contract (``conductance/engine.py:71-89``): the
+inputs are never modified (state is copied before the kernels update it in place), the
+returned ``Run`` holds spikes ``(B, T, N)``, the final ``v``, ``g`` as a ``(B, N, 2, S)``
+view, the refractory counters, probabilities and the tracked variables.
+
+What differs from the reference is underneath:
+
+* one persistent launch (``wt_cond_run``) runs all T steps of a chunk, recurrent or
+  feedforward — the feedforward drive is propagated from the input's nonzero entries
+  per step instead of being materialised as ``(K_ff, B, T, N)`` by matmuls
+  (``network_simulators/engine.py:123-145``);
+* connectivity is compressed by source (``connectome.Connectome``); dense pathways are
+  converted once (cached while their tensors are unchanged);
+* gradients (``_Run``, the counterpart of ``_FeedforwardScan`` / ``_RecurrentRun``,
+  ``conductance/engine.py:444-544``) come from ``wt_cond_scan_backward`` and the
+  event-driven ``wt_weight_gradient``.
+
+The engine runs only on a GPU with the library built; it raises otherwise. Not
+supported (raising ``NotImplementedError``): per-step gradient retention
+(``retain``), gradients through the recurrent spikes (``recurrent_gradients``),
+float16 storage, sampled spikes, presynaptic dynamics, Mg block, adaptation.
+"""
+
+from __future__ import annotations
+
+import math
+from collections import OrderedDict
+from dataclasses import dataclass, field
+
+import torch
+
+from wiretorch_amd import _lib
+from wiretorch_amd.connectome import Connectome, from_dense
+from wiretorch_amd.network import Drive, Physiology, Run
+
+#: Physiology the backward pass can differentiate, in ``Physiology`` names.
+PHYSIOLOGY = ("theta", "U_reset", "E_L", "C_m", "beta", "E_syn", "decay", "jump")
+MAX_FRAC_BITS = 40
+BLOCK = 1024
+MAX_GROUPS = 8
+#: When a list, every ``wt_cond_run`` launch appends a pair of events recorded on its
+#: stream just before and after it (``bench.py`` times the kernel with them).
+LAUNCH_EVENTS: list | None = None
 
 
-def simulate(*args, **kwargs):
-    raise RuntimeError("the HIP engine is not built")
+# =====================================================================
+# Connectivity as the kernels take it
+# =====================================================================
+
+
+@dataclass
+class _Side:
+    """A compressed input side on the device, with what the launches derive from it."""
+
+    conn: Connectome
+    pathway32: torch.Tensor
+    #: For a side built from dense pathways: each source's row within its pathway.
+    row_local: torch.Tensor | None = None
+    dense_shapes: tuple = ()
+    max_in_sum: float = 0.0
+    _split: dict = field(default_factory=dict)
+    _edge_src: torch.Tensor | None = None
+
+    @property
+    def n_src(self) -> int:
+        return self.conn.n_sources
+
+    def split(self, R: int, range_n: int, stream) -> torch.Tensor:
+        key = (R, range_n)
+        if key not in self._split:
+            c = self.conn
+            split = torch.zeros((max(c.n_sources, 1), R + 1), dtype=torch.int64, device=c.device)
+            _lib.check(
+                _lib.load().wt_split_ranges(c.indptr.data_ptr(), c.targets.data_ptr(),
+                                            c.n_sources, R, range_n, split.data_ptr(), stream),
+                "wt_split_ranges",
+            )  # fmt: skip
+            self._split[key] = split
+        return self._split[key]
+
+    def edge_src(self, stream) -> torch.Tensor:
+        if self._edge_src is None:
+            c = self.conn
+            out = torch.empty(c.n_edges, dtype=torch.int64, device=c.device)
+            _lib.check(
+                _lib.load().wt_edge_sources(c.indptr.data_ptr(), c.n_sources, out.data_ptr(), stream),
+                "wt_edge_sources",
+            )
+            self._edge_src = out
+        return self._edge_src
+
+    def abi(self, R: int, range_n: int, stream, weights: torch.Tensor | None = None) -> _lib.Side:
+        c = self.conn
+        w = c.weights if weights is None else weights
+        return _lib.Side(
+            c.indptr.data_ptr(), self.split(R, range_n, stream).data_ptr(),
+            c.targets.data_ptr(), w.data_ptr(), self.pathway32.data_ptr(), c.n_sources,
+        )  # fmt: skip
+
+
+def _empty_side(device) -> _Side:
+    z = torch.zeros(1, dtype=torch.int64, device=device)
+    conn = Connectome(0, 0, z, torch.zeros(1, dtype=torch.int32, device=device),
+                      torch.zeros(1, device=device), z, 0)
+    return _Side(conn, torch.zeros(1, dtype=torch.int32, device=device))
+
+
+def _max_in_sum(conn: Connectome) -> float:
+    if conn.n_edges == 0:
+        return 0.0
+    per_target = torch.zeros(conn.n_targets, dtype=torch.float64, device=conn.device)
+    per_target.index_add_(0, conn.targets.long(), conn.weights.detach().abs().double())
+    return float(per_target.max())
+
+
+def _from_connectome(conn: Connectome, device) -> _Side:
+    conn = conn.to(device)
+    t = conn.targets
+    if conn.n_edges:
+        ascending = bool(((t[1:] > t[:-1]) | _row_starts(conn)[1:]).all())
+        if not ascending or bool((t < 0).any()) or bool((t >= conn.n_targets).any()):
+            raise ValueError("Connectome targets must be in range and strictly ascending per source")
+    if conn.n_sources and (int(conn.pathway.max()) >= conn.n_pathways
+                           or conn.pathway.numel() != conn.n_sources):
+        raise ValueError("Connectome pathway ids must be < n_pathways (or -1)")
+    if int(conn.indptr[-1]) != conn.n_edges or conn.indptr.numel() != conn.n_sources + 1:
+        raise ValueError("Connectome indptr does not match its edges")
+    return _Side(conn, conn.pathway.to(torch.int32).contiguous(), max_in_sum=_max_in_sum(conn))
+
+
+def _row_starts(conn: Connectome) -> torch.Tensor:
+    starts = torch.zeros(conn.n_edges, dtype=torch.bool, device=conn.device)
+    first = conn.indptr[:-1][conn.indptr[:-1] < conn.n_edges]
+    starts[first] = True
+    return starts
+
+
+def _from_pathways(pathways, n_src: int, N: int, device) -> _Side:
+    W_all = torch.zeros((n_src, N), dtype=torch.float32, device=device)
+    pathway = torch.full((n_src,), -1, dtype=torch.int64, device=device)
+    row_local = torch.full((n_src,), -1, dtype=torch.int64, device=device)
+    shapes = []
+    for k, (rows, W) in enumerate(pathways):
+        rows = rows.to(device).long()
+        if bool((pathway[rows] >= 0).any()):
+            raise NotImplementedError("pathways sharing source rows (presynaptic dynamics)")
+        pathway[rows] = k
+        row_local[rows] = torch.arange(rows.numel(), device=device)
+        W_all[rows] = W.detach().to(device, torch.float32)
+        shapes.append(tuple(W.shape))
+    conn = from_dense(W_all, pathway, len(pathways))
+    side = _Side(conn, pathway.to(torch.int32), row_local=row_local,
+                 dense_shapes=tuple(shapes))
+    side.max_in_sum = _max_in_sum(conn)
+    return side
+
+
+_CACHE: OrderedDict = OrderedDict()
+_CACHE_SIZE = 8
+
+
+def _side_of(pathways, sparse, n_src: int, N: int, device) -> _Side:
+    """The compressed side of a drive, cached while its tensors are unchanged."""
+    if sparse is not None:
+        key = ("sparse", id(sparse), sparse.weights._version, sparse.weights.data_ptr())
+        keep = (sparse,)
+    elif pathways:
+        key = ("dense", n_src, N) + tuple(
+            (rows.data_ptr(), W.data_ptr(), W._version, tuple(W.shape)) for rows, W in pathways
+        )
+        keep = tuple(t for pair in pathways for t in pair)
+    else:
+        return _empty_side(device)
+    hit = _CACHE.get(key)
+    if hit is not None:
+        _CACHE.move_to_end(key)
+        return hit[0]
+    side = (_from_connectome(sparse, device) if sparse is not None
+            else _from_pathways(pathways, n_src, N, device))
+    _CACHE[key] = (side, keep)  # holding the tensors keeps their addresses unique
+    while len(_CACHE) > _CACHE_SIZE:
+        _CACHE.popitem(last=False)
+    return side
+
+
+# =====================================================================
+# One call
+# =====================================================================
+
+
+_DEVICE_INFO: dict = {}
+
+
+def _device_info(device) -> tuple[int, int]:
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if index not in _DEVICE_INFO:
+        n_cu, lds = _lib.I64(), _lib.I64()
+        with torch.cuda.device(index):
+            _lib.check(_lib.load().wt_device_info(n_cu, lds), "wt_device_info")
+        _DEVICE_INFO[index] = (int(n_cu.value), int(lds.value))
+    return _DEVICE_INFO[index]
+
+
+def geometry(B: int, N: int, K: int, n_cu: int, max_lds: int) -> tuple[int, int, int]:
+    """``(groups, R, range_n)``: trials round-robin over up to 8 groups (one per XCD);
+    each group's targets split over R workgroups, about one neuron-trial per thread,
+    within the LDS budget of the int64 accumulator ``K * trials * range_n``."""
+    groups = max(1, min(MAX_GROUPS, B))
+    tpg = -(-B // groups)
+    if tpg > 64:
+        raise ValueError(f"batch {B} is too large for one launch (at most 512 trials)")
+    limit = max(1, min(64, n_cu // groups))
+    R = max(1, min(limit, -(-N * tpg // BLOCK)))
+    budget = max_lds - 20 * 1024
+    while True:
+        range_n = -(-N // R)
+        if max(K, 1) * tpg * range_n * 8 <= budget or R >= limit:
+            break
+        R += 1
+    R = -(-N // range_n)
+    if max(K, 1) * tpg * range_n * 8 > budget:
+        raise ValueError("network too large for one launch's LDS accumulator")
+    return groups, R, range_n
+
+
+def _frac_bits(bound: float) -> int:
+    """Fractional bits of the fixed-point accumulator: exact while every per-target
+    sum stays below 2^61 / 2^frac."""
+    if bound <= 0:
+        return MAX_FRAC_BITS
+    return max(0, min(MAX_FRAC_BITS, 61 - math.ceil(math.log2(bound)) - 1))
+
+
+def _f32(t: torch.Tensor, device) -> torch.Tensor:
+    return t.detach().to(device=device, dtype=torch.float32).contiguous()
+
+
+@dataclass
+class _Plan:
+    """Shapes, tables and connectivity shared by the forward and backward launches."""
+
+    B: int
+    T: int
+    N: int
+    S: int
+    K_rec: int
+    K_ff: int
+    n_in: int
+    tables: dict
+    rec: _Side
+    ff: _Side
+    geo: tuple
+    frac_bits: int
+    refractory: bool
+    probabilities: bool
+    track: bool
+    track_b: int
+    stream: int
+    device: torch.device
+
+    @property
+    def K(self) -> int:
+        return self.K_rec + self.K_ff
+
+    def abi_tables(self, scale: torch.Tensor) -> _lib.Tables:
+        t = self.tables
+        return _lib.Tables(
+            t["theta"].data_ptr(), t["U_reset"].data_ptr(), t["E_L"].data_ptr(),
+            t["C_m"].data_ptr(), t["beta"].data_ptr(),
+            t["n_ref"].data_ptr() if t["n_ref"] is not None else None,
+            t["E_syn"].data_ptr(), t["g_clip"].data_ptr(), t["decay"].data_ptr(),
+            t["jump"].data_ptr(), t["made"].data_ptr(), scale.data_ptr(),
+            t["dt"].data_ptr(), t["surr"].data_ptr(), self.N, self.S, self.K, self.K_rec,
+        )  # fmt: skip
+
+
+def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_idx) -> _Plan:
+    device = x.device
+    B, T, n_in = x.shape
+    N = v.shape[1]
+    S = p.E_syn.shape[0]
+    if S > 8:
+        raise NotImplementedError(f"at most 8 synapse types, got {S}")
+    K_rec, K_ff = drive.K_rec, drive.K_ff
+    if K_rec + K_ff > 8:
+        raise NotImplementedError(f"at most 8 pathways, got {K_rec + K_ff}")
+    if drive.made.shape != (K_rec + K_ff, S) or drive.scale.shape != (K_rec + K_ff, N):
+        raise ValueError("drive.made / drive.scale do not match the pathways")
+    rec = _side_of(drive.recurrent, drive.sparse_recurrent, N, N, device)
+    ff = _side_of(drive.feedforward, drive.sparse_feedforward, n_in, N, device)
+    if rec.n_src and rec.conn.n_targets != N:
+        raise ValueError("recurrent connectome does not match the network size")
+    if ff.n_src and (ff.n_src != n_in or ff.conn.n_targets != N):
+        raise ValueError("feedforward connectome does not match the input and network")
+    n_cu, max_lds = _device_info(device)
+    groups, R, range_n = geometry(B, N, K_rec + K_ff, n_cu, max_lds)
+    bound = rec.max_in_sum
+    if ff.n_src and ff.conn.n_edges:
+        bound += ff.max_in_sum * float(x.detach().abs().max())
+    tables = {name: _f32(getattr(p, name), device) for name in
+              ("theta", "U_reset", "E_L", "C_m", "beta", "E_syn", "g_clip", "decay", "jump")}
+    tables["made"] = drive.made.to(device=device, dtype=torch.float32).contiguous()
+    tables["dt"] = _f32(p.dt, device)
+    tables["surr"] = _f32(p.surr_scale, device)
+    tables["n_ref"] = (None if p.n_ref is None
+                       else p.n_ref.to(device=device, dtype=torch.int32).contiguous())
+    return _Plan(
+        B=B, T=T, N=N, S=S, K_rec=K_rec, K_ff=K_ff, n_in=n_in, tables=tables, rec=rec,
+        ff=ff, geo=(groups, R, range_n), frac_bits=_frac_bits(bound),
+        refractory=p.n_ref is not None, probabilities=probabilities, track=track,
+        track_b=(-1 if track_batch_idx is None else int(track_batch_idx)) if track else 0,
+        stream=torch.cuda.current_stream(device).cuda_stream, device=device,
+    )  # fmt: skip
+
+
+def _launch(L: _Plan, x, scale, v, g, counter, spikes, prob, saved, tracked,
+            rec_weights=None, ff_weights=None) -> None:
+    groups, R, range_n = L.geo
+    geo = _lib.Geometry(groups, R, range_n, L.frac_bits)
+    lib = _lib.load()
+    scratch = torch.zeros(int(lib.wt_cond_run_scratch_bytes(geo, L.B, L.N)),
+                          dtype=torch.uint8, device=L.device)
+    v_saved, G_saved, held, A_saved = saved if saved is not None else (None,) * 4
+    tv, tI, tg = ((tracked["v"], tracked["I"], tracked["g"]) if tracked is not None
+                  else (None, None, None))
+    io = _lib.RunIO(
+        x.data_ptr(), L.B, L.T, L.n_in, v.data_ptr(), g.data_ptr(),
+        _lib.ptr(counter) if L.refractory else None, spikes.data_ptr(), _lib.ptr(prob),
+        _lib.ptr(v_saved), _lib.ptr(G_saved), _lib.ptr(held), _lib.ptr(A_saved),
+        _lib.ptr(tv), _lib.ptr(tI), _lib.ptr(tg), L.track_b,
+    )  # fmt: skip
+    rec = L.rec.abi(R, range_n, L.stream, rec_weights)
+    ff = L.ff.abi(R, range_n, L.stream, ff_weights)
+    tab = L.abi_tables(scale)
+    if LAUNCH_EVENTS is not None:
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+    _lib.check(lib.wt_cond_run(tab, rec, ff, geo, io, scratch.data_ptr(), L.stream), "wt_cond_run")
+    if LAUNCH_EVENTS is not None:
+        stop.record()
+        LAUNCH_EVENTS.append((start, stop))
+    flags = int(scratch[:4].view(torch.int32).item())
+    if flags:
+        raise RuntimeError(f"wt_cond_run: a workgroup barrier timed out (flags {flags:#x})")
+
+
+# =====================================================================
+# Autograd
+# =====================================================================
+
+
+class _Run(torch.autograd.Function):
+    """Spikes (and probabilities) of a chunk, differentiable in the kernel ``scale``,
+    the input ``x``, the pathway weights and the physiology (``PHYSIOLOGY``)."""
+
+    @staticmethod
+    def forward(ctx, L: _Plan, n_rec_w: int, scale, x, v, g, counter, *rest):
+        weights, physiology = rest[: len(rest) - len(PHYSIOLOGY)], rest[-len(PHYSIOLOGY):]
+        dev = L.device
+        spikes = torch.empty((L.B, L.T, L.N), device=dev)
+        prob = torch.empty_like(spikes) if L.probabilities else None
+        v_saved = torch.empty_like(spikes)
+        G_saved = torch.empty((L.B, L.T, L.N, L.S), device=dev)
+        held = torch.empty((L.B, L.T, L.N), dtype=torch.int8, device=dev) if L.refractory else None
+        A_saved = torch.empty((max(L.K, 1), L.B, L.T, L.N), device=dev)
+        want_decay = physiology[PHYSIOLOGY.index("decay")].requires_grad
+        g_init = g.clone() if want_decay else None
+        tracked = _tracked_buffers(L)
+        _launch(L, x.detach().float().contiguous(), scale.detach().float().contiguous(), v, g,
+                counter, spikes, prob, (v_saved, G_saved, held, A_saved), tracked,
+                *_sparse_weights(L, weights, n_rec_w))
+        ctx.L, ctx.n_rec_w, ctx.tracked = L, n_rec_w, tracked
+        ctx.save_for_backward(scale, x, spikes, v_saved, G_saved,
+                              held if held is not None else spikes.new_empty(0),
+                              A_saved, g_init if g_init is not None else spikes.new_empty(0),
+                              *weights)
+        ctx.mark_non_differentiable(v, g, counter)
+        return spikes, prob, v, g, counter
+
+    @staticmethod
+    def backward(ctx, grad_spikes, grad_prob, _v, _g, _c):
+        L, n_rec_w = ctx.L, ctx.n_rec_w
+        scale, x, spikes, v_saved, G_saved, held, A_saved, g_init, *weights = ctx.saved_tensors
+        needs = ctx.needs_input_grad
+        want_scale, want_x = needs[2], needs[3]
+        w_needs = needs[7: 7 + len(weights)]
+        p_needs = needs[7 + len(weights):]
+        if grad_spikes is None:
+            grad_spikes = torch.zeros_like(spikes)
+        want_A = want_x or any(w_needs)
+        dev = L.device
+        B, T, N, S, K = L.B, L.T, L.N, L.S, L.K
+        grad_A = torch.empty((max(K, 1), B, T, N), device=dev) if want_A else None
+        partial = torch.empty((max(K, 1), B, N), device=dev) if want_scale else None
+        shapes = [(B, N)] * 5 + [(B, S, N), (B, 2, S, N), (B, 2, S, N)]
+        phys = [torch.empty(sh, device=dev) if want else None for sh, want in zip(shapes, p_needs)]
+        io = _lib.BackwardIO(
+            grad_spikes.contiguous().data_ptr(),
+            _lib.ptr(grad_prob.contiguous()) if grad_prob is not None else None,
+            spikes.data_ptr(), v_saved.data_ptr(), G_saved.data_ptr(),
+            held.data_ptr() if L.refractory else None, A_saved.data_ptr(),
+            g_init.data_ptr() if g_init.numel() else None, B, T,
+            _lib.ptr(grad_A), _lib.ptr(partial), *[_lib.ptr(t) for t in phys],
+        )  # fmt: skip
+        _lib.check(_lib.load().wt_cond_scan_backward(L.abi_tables(scale.detach().float().contiguous()),
+                                                     io, L.stream), "wt_cond_scan_backward")
+        grad_scale = partial.sum(dim=1) if want_scale else None
+        dims = [0] * 5 + [(0, 2), (0, 3), (0, 3)]
+        grad_phys = [t.sum(d) if t is not None else None for t, d in zip(phys, dims)]
+        grad_w = [None] * len(weights)
+        if any(w_needs[:n_rec_w]):
+            grad_w[:n_rec_w] = _weight_grads(L, L.rec, spikes, grad_A, 0, weights[:n_rec_w],
+                                             w_needs[:n_rec_w])
+        if any(w_needs[n_rec_w:]):
+            grad_w[n_rec_w:] = _weight_grads(L, L.ff, x.detach().float(), grad_A, L.K_rec,
+                                             weights[n_rec_w:], w_needs[n_rec_w:])
+        grad_x = _input_grad(L, x, grad_A, weights[n_rec_w:]) if want_x else None
+        return (None, None, grad_scale, grad_x, None, None, None, *grad_w, *grad_phys)
+
+
+def _tracked_buffers(L: _Plan):
+    if not L.track:
+        return None
+    Bt = L.B if L.track_b < 0 else 1
+    dev = L.device
+    return {
+        "v": torch.empty((Bt, L.T, L.N), device=dev),
+        "I": torch.empty((Bt, L.T, L.N, L.S + 1), device=dev),
+        "g": torch.empty((Bt, L.T, L.N, 2, L.S), device=dev),
+    }
+
+
+def _sparse_weights(L: _Plan, weights, n_rec_w):
+    """Weight tensors the kernels read directly (a compressed side's ``weights``)."""
+    rec = ff = None
+    if L.rec.row_local is None and n_rec_w == 1:
+        rec = weights[0].detach().float().contiguous()
+    if L.ff.row_local is None and len(weights) - n_rec_w == 1:
+        ff = weights[n_rec_w].detach().float().contiguous()
+    return rec, ff
+
+
+def _events(activity: torch.Tensor):
+    """Per source, its (trial*T + step) events ascending and their values:
+    ``(indptr, bt, value)`` from ``activity`` ``(B, T, n_src)``."""
+    B, T, n = activity.shape
+    flat = activity.reshape(B * T, n)
+    bt, j = torch.nonzero(flat, as_tuple=True)
+    key = j * (B * T) + bt
+    order = torch.argsort(key)
+    j, bt = j[order], bt[order]
+    value = flat[bt, j].contiguous()
+    indptr = torch.zeros(n + 1, dtype=torch.int64, device=activity.device)
+    indptr[1:] = torch.cumsum(torch.bincount(j, minlength=n), 0)
+    return indptr, bt.contiguous(), value
+
+
+def _weight_grads(L: _Plan, side: _Side, activity, grad_A, k0, weights, needs):
+    """Gradients of a side's weight tensors from the event-driven support gradient."""
+    c = side.conn
+    indptr, bt, value = _events(activity)
+    grad_e = torch.empty(c.n_edges, device=L.device)
+    edge_src = side.edge_src(L.stream)
+    groups, R, range_n = L.geo
+    abi = side.abi(R, range_n, L.stream)
+    _lib.check(
+        _lib.load().wt_weight_gradient(abi, edge_src.data_ptr(), c.n_edges, indptr.data_ptr(),
+                                       bt.data_ptr(), value.data_ptr(), grad_A.data_ptr(), L.B,
+                                       L.T, L.N, k0, grad_e.data_ptr(), L.stream),
+        "wt_weight_gradient",
+    )  # fmt: skip
+    if side.row_local is None:  # compressed side: the gradient of its weights
+        return [grad_e if needs[0] else None]
+    out = []
+    k_of_edge = c.pathway[edge_src]
+    row_of_edge = side.row_local[edge_src]
+    for k, (shape, need) in enumerate(zip(side.dense_shapes, needs)):
+        if not need:
+            out.append(None)
+            continue
+        sel = k_of_edge == k
+        G = torch.zeros(shape, device=L.device)
+        G[row_of_edge[sel], c.targets[sel].long()] = grad_e[sel]
+        out.append(G)
+    return out
+
+
+def _input_grad(L: _Plan, x, grad_A, ff_weights):
+    """dL/dx of the feedforward input: each pathway's dL/da carried back through W^T."""
+    grad_x = torch.zeros_like(x, dtype=torch.float32)
+    side = L.ff
+    if side.row_local is None or not side.n_src:
+        raise NotImplementedError("input gradients through a compressed feedforward side")
+    pathway = side.conn.pathway
+    for k, W in enumerate(ff_weights):
+        rows = torch.nonzero(pathway == k).flatten()
+        order = torch.argsort(side.row_local[rows])
+        rows = rows[order]
+        grad_x[:, :, rows] += grad_A[L.K_rec + k] @ W.detach().float().T
+    return grad_x.to(x.dtype)
+
+
+# =====================================================================
+# Entry point
+# =====================================================================
+
+
+def simulate(
+    v, g, x, drive: Drive, p: Physiology, *, refractory=None, gating=None,
+    adaptation=None, probabilities=False, track=False, track_batch_idx=None, retain=None,
+) -> Run:  # fmt: skip
+    """Simulate ``x.shape[1]`` steps from ``(v, g)`` on the GPU; see the module docstring."""
+    if not x.is_cuda:
+        raise RuntimeError(f"the HIP engine runs on a GPU; the input is on {x.device}")
+    if retain is not None:
+        raise NotImplementedError("per-step gradient retention (track_gradients)")
+    if gating is not None or drive.gates or adaptation is not None or p.adapt is not None:
+        raise NotImplementedError("presynaptic dynamics and adaptation")
+    if p.mg_c is not None:
+        raise NotImplementedError("the NMDA Mg block")
+    if p.spike_mode != "deterministic":
+        raise NotImplementedError("sampled spikes")
+    if p.storage_dtype != torch.float32:
+        raise NotImplementedError("float16 storage")
+    device = x.device
+    L = _plan(v, x, drive, p, probabilities, track, track_batch_idx)
+    v = v.detach().to(device=device, dtype=torch.float32).contiguous().clone()
+    g_state = g.detach().permute(0, 2, 3, 1).to(device=device, dtype=torch.float32).contiguous()
+    if refractory is None:
+        refractory = torch.zeros(v.shape, dtype=torch.int32, device=device)
+    counter = refractory.to(device=device, dtype=torch.int32).contiguous().clone()
+
+    rec_w = ([drive.sparse_recurrent.weights] if drive.sparse_recurrent is not None
+             else [W for _, W in drive.recurrent])
+    ff_w = ([drive.sparse_feedforward.weights] if drive.sparse_feedforward is not None
+            else [W for _, W in drive.feedforward])
+    physiology = [getattr(p, name) for name in PHYSIOLOGY]
+    grad = torch.is_grad_enabled() and (
+        drive.scale.requires_grad or x.requires_grad
+        or any(W.requires_grad for W in rec_w + ff_w)
+        or any(t.requires_grad for t in physiology)
+    )  # fmt: skip
+    if grad and drive.recurrent_gradients and L.K_rec:
+        raise NotImplementedError("gradients through the recurrent spikes (recurrent_gradients)")
+    if grad:
+        spikes, prob, v, g_state, counter = _Run.apply(
+            L, len(rec_w), drive.scale, x, v, g_state, counter, *rec_w, *ff_w, *physiology
+        )
+        tracked = None
+        if track:  # the buffers live on the autograd context; rebuild from the last run
+            tracked = _last_tracked(spikes)
+    else:
+        spikes = torch.empty((L.B, L.T, L.N), device=device)
+        prob = torch.empty_like(spikes) if probabilities else None
+        tracked = _tracked_buffers(L)
+        with torch.no_grad():
+            rw, fw = _sparse_weights(L, rec_w + ff_w, len(rec_w))
+            _launch(L, x.detach().float().contiguous(),
+                    drive.scale.detach().float().contiguous(), v, g_state, counter, spikes,
+                    prob, None, tracked, rw, fw)
+    return Run(
+        output=spikes,
+        v=v,
+        syn=g_state.permute(0, 3, 1, 2),
+        probabilities=prob,
+        tracked=tracked,
+        refractory=counter,
+    )
+
+
+def _last_tracked(spikes):
+    node = spikes.grad_fn
+    return getattr(node, "tracked", None)
