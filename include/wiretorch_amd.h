@@ -67,7 +67,8 @@ typedef struct {
 } wt_side;
 
 /* Launch geometry of wt_cond_run: groups*R workgroups; group g owns the trials
- * b = g, g+groups, ...; workgroup slot r of a group owns targets [r*range_n, ...).
+ * b = g, g+groups, ...; workgroup slot r of a group owns targets [r*range_n, ...);
+ * range_n is a multiple of 32, and a workgroup owns at most 8192 (trial, neuron) items.
  * frac_bits: activations are accumulated exactly as int64 multiples of 2^-frac_bits. */
 typedef struct {
   int64_t groups, R, range_n, frac_bits;
@@ -112,6 +113,14 @@ int64_t wt_cond_run_scratch_bytes(const wt_geometry* geo, int64_t B, int64_t N);
 int wt_cond_run(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
                 const wt_geometry* geo, const wt_run_io* io, void* scratch,
                 wt_stream_t stream);
+
+/* wt_cond_run_timed — wt_cond_run with per-workgroup wall-clock ticks (100 MHz) of each
+ * phase of the step loop added to timing[wg * 5 + phase], phases: neuron update,
+ * publishing the fired bitmap, feedforward push, barrier wait, recurrent push. For
+ * profiling; no counterpart in the reference. timing: (groups * R * 5) u64. */
+int wt_cond_run_timed(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
+                      const wt_geometry* geo, const wt_run_io* io, void* scratch,
+                      uint64_t* timing, wt_stream_t stream);
 
 /* wt_cond_scan_backward — reverse-time adjoint of T steps whose activations A are
  * known (the recurrent activations treated as input).

@@ -164,3 +164,35 @@ def test_sparse_network_matches_oracle():
     assert s_ref[:, :200].sum() > 0
     differs = (s_gpu[:, :200] != s_ref[:, :200]).any(axis=(0, 2))
     assert not differs.any(), f"rasters differ from step {int(np.argmax(differs))}"
+
+
+@pytest.mark.slow
+def test_fly_scale_raster_matches_oracle():
+    """Configuration 2 itself (140k neurons, ~50M synapses, 8 trials): the GPU's
+    raster equals the oracle's over the first 200 steps (the oracle runs them on the
+    host, ~1 minute)."""
+    steps = 200
+    wl = synthetic.fly_scale(T=steps, device=DEV)
+    x = torch.from_numpy(wl.x).float()
+    v, g, c = synthetic.rest_state(8, wl.N, 2, DEV)
+    with torch.no_grad():
+        out = engine.simulate(v, g, x.to(DEV), wl.drive, wl.physiology, refractory=c)
+    s_gpu = out.spikes.cpu().numpy()
+    rec = wl.drive.sparse_recurrent.to("cpu")
+    ff = wl.drive.sparse_feedforward.to("cpu")
+    drive, p = synthetic.sparse_drive(rec, ff, wl.N, 0.1, "cpu")
+    v, g, c = synthetic.rest_state(8, wl.N, 2)
+    torch.set_num_threads(16)
+    try:
+        with torch.no_grad():
+            ref = oracle_engine.simulate(v, g, x, drive, p, refractory=c)
+    finally:
+        torch.set_num_threads(1)
+    s_ref = ref.spikes.numpy()
+    assert s_ref.sum() > 1000
+    differs = (s_gpu != s_ref).any(axis=(0, 2))
+    assert not differs.any(), (
+        f"rasters differ from step {int(np.argmax(differs))}: "
+        f"{int((s_gpu != s_ref).sum())} spikes differ; GPU {int(s_gpu.sum())}, oracle {int(s_ref.sum())}"
+    )
+    np.testing.assert_allclose(out.v.cpu().numpy(), ref.v.numpy(), rtol=1e-5, atol=1e-5 * 65)

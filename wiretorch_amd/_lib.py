@@ -59,6 +59,9 @@ SIGNATURES = {
     "wt_cond_run": (ctypes.c_int, [ctypes.POINTER(Tables), ctypes.POINTER(Side),
                                    ctypes.POINTER(Side), ctypes.POINTER(Geometry),
                                    ctypes.POINTER(RunIO), P, P]),
+    "wt_cond_run_timed": (ctypes.c_int, [ctypes.POINTER(Tables), ctypes.POINTER(Side),
+                                         ctypes.POINTER(Side), ctypes.POINTER(Geometry),
+                                         ctypes.POINTER(RunIO), P, P, P]),
     "wt_cond_scan_backward": (ctypes.c_int, [ctypes.POINTER(Tables),
                                              ctypes.POINTER(BackwardIO), P]),
     "wt_edge_sources": (ctypes.c_int, [P, I64, P, P]),

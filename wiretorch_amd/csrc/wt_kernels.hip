@@ -41,30 +41,37 @@ struct RunArgs {
   wt_geometry geo;
   wt_run_io io;
   // scratch
-  uint32_t* err;        // [0]: error flags
-  uint32_t* barrier;    // one counter per group, 128 bytes apart
-  int32_t* fired;       // [2][wgs][tpg_max][range_n]
-  int32_t* fired_count; // [2][wgs][tpg_max]
-  int64_t tpg_max;
+  uint32_t* err;       // [0]: error flags
+  uint32_t* barrier;   // one counter per group, 128 bytes apart
+  uint32_t* bitmap;    // [2][B][R * words]: which neurons fired, per trial
+  uint64_t* timing;    // [wgs][kPhases] wall-clock ticks per phase, or null
+  int64_t words;       // bitmap words per workgroup range (range_n / 32)
 };
 
-__device__ inline void store_agent(int32_t* p, int32_t v) {
+constexpr int kPhases = 5;  // update, publish, feedforward push, barrier wait, recurrent push
+
+__device__ inline void store_agent(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ inline int32_t load_agent(const int32_t* p) {
-  return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ inline uint32_t load_agent(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Group barrier: every thread's stores complete, then one arrival per workgroup on
-// the group's counter; the wait is bounded (2 s of wall clock) and gives up as soon as
-// any workgroup has flagged an error. Returns false on error.
-__device__ inline bool group_barrier(uint32_t* counter, uint32_t target, uint32_t* err,
-                                     uint32_t* s_flag) {
+// Split group barrier. arrive(): every thread's stores complete, then one arrival per
+// workgroup on the group's counter. wait(): bounded (2 s of wall clock), giving up as
+// soon as any workgroup has flagged an error. Work placed between the two overlaps
+// the other workgroups' progress.
+__device__ inline void barrier_arrive(uint32_t* counter) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ inline bool barrier_wait(uint32_t* counter, uint32_t target, uint32_t* err,
+                                    uint32_t* s_flag) {
   if (threadIdx.x == 0) {
     uint32_t bad = 0;
-    __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     uint64_t start = wall_clock64();
     uint32_t polls = 0;
     while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
@@ -97,36 +104,55 @@ __device__ inline void load_synapses(const wt_tables& tab, Synapses<S>& syn) {
   }
 }
 
-// Adds the synapses of `edges` [e0, e1) onto this workgroup's targets (local index
-// target - lo) of pathway k, trial slot q, to the LDS accumulator.
-__device__ inline void push_edges(long long* acc, const wt_side& side, int64_t e0,
-                                  int64_t e1, int64_t lo, int64_t slot_base, float value,
-                                  float fscale) {
-  if (value == 1.0f) {
-    for (int64_t e = e0; e < e1; ++e) {
-      int64_t t = side.targets[e] - lo;
-      atomicAdd(reinterpret_cast<unsigned long long*>(acc + slot_base + t),
-                (unsigned long long)to_fixed(side.weights[e], fscale));
+// Adds the synapses [e0, e1) of one source (all onto this workgroup's targets: local
+// index target - lo) times `value` to the accumulator row `row`. Loads are issued four
+// at a time ahead of their atomics.
+__device__ inline void push_edges(long long* row, const wt_side& side, int64_t e0, int64_t e1,
+                                  int64_t lo, float value, float fscale) {
+  int64_t e = e0;
+  for (; e + 4 <= e1; e += 4) {
+    int32_t t[4];
+    float w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      t[u] = side.targets[e + u];
+      w[u] = side.weights[e + u];
     }
-  } else {
-    for (int64_t e = e0; e < e1; ++e) {
-      int64_t t = side.targets[e] - lo;
-      atomicAdd(reinterpret_cast<unsigned long long*>(acc + slot_base + t),
-                (unsigned long long)to_fixed(value * side.weights[e], fscale));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float x = value == 1.0f ? w[u] : value * w[u];
+      atomicAdd(reinterpret_cast<unsigned long long*>(row + (t[u] - lo)),
+                (unsigned long long)to_fixed(x, fscale));
     }
+  }
+  for (; e < e1; ++e) {
+    const float x = value == 1.0f ? side.weights[e] : value * side.weights[e];
+    atomicAdd(reinterpret_cast<unsigned long long*>(row + (side.targets[e] - lo)),
+              (unsigned long long)to_fixed(x, fscale));
   }
 }
 
-template <int S>
+__device__ inline void tick(uint64_t* acc_t, uint64_t& last, int phase) {
+  if (acc_t && threadIdx.x == 0) {
+    const uint64_t now = wall_clock64();
+    acc_t[phase] += now - last;
+    last = now;
+  }
+}
+
+// The persistent forward. Each thread owns up to MAXI (trial, neuron) items — item
+// threadIdx.x + i * blockDim.x of its workgroup — whose state stays in registers for
+// the whole launch.
+template <int S, int MAXI>
 __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
-  extern __shared__ long long acc[];  // [K][tpg][range_n]
-  __shared__ int32_t s_fcnt[64];
-  __shared__ int32_t s_pre[64 * 65];  // per trial slot: prefix of the R fired counts
+  extern __shared__ long long acc[];  // [K][tpg][range_n], then the local fired bitmap
   __shared__ uint32_t s_flag;
+  __shared__ uint64_t s_time[kPhases];
 
   const wt_tables& tab = A.tab;
+  const wt_run_io& io = A.io;
   const int64_t groups = A.geo.groups, R = A.geo.R, range_n = A.geo.range_n;
-  const int64_t N = tab.N, K = tab.K, K_rec = tab.K_rec, B = A.io.B, T = A.io.T;
+  const int64_t N = tab.N, K = tab.K, K_rec = tab.K_rec, B = io.B, T = io.T;
   const int64_t wg = blockIdx.x;
   const int64_t g = wg % groups, r = wg / groups;
   const int64_t tpg = g < B ? (B - g + groups - 1) / groups : 0;
@@ -135,47 +161,60 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   const int64_t nr = lo < N ? (N - lo < range_n ? N - lo : range_n) : 0;
   const int64_t items = tpg * nr;
   const int64_t acc_len = K * tpg * range_n;
+  const int64_t words = A.words;  // bitmap words of one trial's range
+  uint32_t* s_bits = reinterpret_cast<uint32_t*>(acc + acc_len);  // [tpg][words]
   const bool refractory = tab.n_ref != nullptr;
   const bool recurrent = K_rec > 0 && A.rec.n_src > 0;
   const float dt = *tab.dt;
   const float fscale = ldexpf(1.0f, (int)A.geo.frac_bits);
   const float inv_fscale = ldexpf(1.0f, -(int)A.geo.frac_bits);
-  const wt_run_io& io = A.io;
   Synapses<S> syn;
   load_synapses<S>(tab, syn);
+  uint64_t* my_time = A.timing ? s_time : nullptr;
+  if (threadIdx.x < kPhases) s_time[threadIdx.x] = 0;
+  uint64_t last = wall_clock64();
 
   for (int64_t i = threadIdx.x; i < acc_len; i += blockDim.x) acc[i] = 0;
-  __syncthreads();
 
-  uint32_t* my_barrier = A.barrier + g * 32;
-  const int64_t fstride = A.tpg_max * range_n;  // one workgroup's fired segment
-  const int64_t wgs = groups * R;
-
-  for (int64_t t = 0; t <= T; ++t) {
-    const int buf = (int)(t & 1);
-    if (threadIdx.x < 64) s_fcnt[threadIdx.x] = 0;
-    __syncthreads();
-    int32_t* my_fired = A.fired + ((int64_t)buf * wgs + wg) * fstride;
-
-    // ---------------- (A) update the owned neurons ----------------
-    for (int64_t it = threadIdx.x; it < items; it += blockDim.x) {
-      const int64_t q = it / nr, ln = it - q * nr, n = lo + ln;
-      const int64_t b = g + q * groups;
-      const int64_t bn = b * N + n;
-      float v = io.v[bn];
-      float gr[S], gd[S];
+  // Registers: the owned items' state.
+  float v[MAXI], theta[MAXI], gr[MAXI][S], gd[MAXI][S];
+  int32_t counter[MAXI];
+#pragma unroll
+  for (int i = 0; i < MAXI; ++i) {
+    const int64_t it = threadIdx.x + (int64_t)i * blockDim.x;
+    if (it < items) {
+      const int64_t q = it / nr, n = lo + (it - q * nr), b = g + q * groups;
+      v[i] = io.v[b * N + n];
+      theta[i] = tab.theta[n];
+      counter[i] = refractory ? io.counter[b * N + n] : 0;
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        gr[s] = io.g[(b * 2 * S + s) * N + n];
-        gd[s] = io.g[(b * 2 * S + S + s) * N + n];
+        gr[i][s] = io.g[(b * 2 * S + s) * N + n];
+        gd[i][s] = io.g[(b * 2 * S + S + s) * N + n];
       }
+    }
+  }
+  uint32_t* my_barrier = A.barrier + g * 32;
+
+  for (int64_t t = 0; t <= T; ++t) {
+    const int64_t buf = t & 1;
+    for (int64_t w = threadIdx.x; w < tpg * words; w += blockDim.x) s_bits[w] = 0;
+    __syncthreads();
+
+    // ---------------- (A) update the owned neurons ----------------
+#pragma unroll
+    for (int i = 0; i < MAXI; ++i) {
+      const int64_t it = threadIdx.x + (int64_t)i * blockDim.x;
+      if (it >= items) continue;
+      const int64_t q = it / nr, ln = it - q * nr, n = lo + ln;
+      const int64_t b = g + q * groups;
       if (t > 0) {
         // g <- g * decay, then each pathway's activation times its kernel, in order
         // (dynamics.py:206-208; kernel = jump * scale * made, dynamics.py:95-100).
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-          gr[s] = gr[s] * syn.decay_r[s];
-          gd[s] = gd[s] * syn.decay_d[s];
+          gr[i][s] = gr[i][s] * syn.decay_r[s];
+          gd[i][s] = gd[i][s] * syn.decay_d[s];
         }
         for (int64_t k = 0; k < K; ++k) {
           long long* cell = acc + (k * tpg + q) * range_n + ln;
@@ -185,9 +224,10 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
           const float sc = tab.scale[k * N + n];
 #pragma unroll
           for (int s = 0; s < S; ++s) {
-            if (tab.made[k * S + s] != 0.0f) {
-              gr[s] = gr[s] + a * (syn.jump_r[s] * sc * tab.made[k * S + s]);
-              gd[s] = gd[s] + a * (syn.jump_d[s] * sc * tab.made[k * S + s]);
+            const float mk = tab.made[k * S + s];
+            if (mk != 0.0f) {
+              gr[i][s] = gr[i][s] + a * (syn.jump_r[s] * sc * mk);
+              gd[i][s] = gd[i][s] + a * (syn.jump_d[s] * sc * mk);
             }
           }
         }
@@ -196,29 +236,28 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
           float* out = io.track_g + ((bt * T + (t - 1)) * N + n) * 2 * S;
 #pragma unroll
           for (int s = 0; s < S; ++s) {
-            out[s] = gr[s];
-            out[S + s] = gd[s];
+            out[s] = gr[i][s];
+            out[S + s] = gd[i][s];
           }
         }
       }
       if (t < T) {
-        const float theta = tab.theta[n];
-        int32_t counter = refractory ? io.counter[bn] : 0;
         float r_hold, held;
-        const float s_out = spike_step(v, theta, counter, refractory ? tab.n_ref[n] : 0,
-                                       refractory, r_hold, held);
+        const float s_out = spike_step(v[i], theta[i], counter[i],
+                                       refractory ? tab.n_ref[n] : 0, refractory, r_hold, held);
         const int64_t out = (b * T + t) * N + n;
         io.spikes[out] = s_out;
         if (io.prob) {
-          float p = 1.0f / (1.0f + expf(-(*tab.surr * (v - theta))));
-          io.prob[out] = refractory ? p * (1.0f - held) : p;
+          const float pr = 1.0f / (1.0f + expf(-(*tab.surr * (v[i] - theta[i]))));
+          io.prob[out] = refractory ? pr * (1.0f - held) : pr;
         }
-        const Leak lk = leak(tab.C_m[n], tab.beta[n], dt);
+        const float C_m = tab.C_m[n];
+        const Leak lk = leak(C_m, tab.beta[n], dt);
         float G[S], I[S], I_leak;
-        const float v_next = membrane<S>(v, r_hold, gr, gd, syn, tab.E_L[n], tab.C_m[n],
+        const float v_next = membrane<S>(v[i], r_hold, gr[i], gd[i], syn, tab.E_L[n], C_m,
                                          tab.U_reset[n], lk, dt, G, I, I_leak);
         if (io.v_saved) {
-          io.v_saved[out] = v;
+          io.v_saved[out] = v[i];
 #pragma unroll
           for (int s = 0; s < S; ++s) io.G_saved[out * S + s] = G[s];
           if (refractory && io.held) io.held[out] = (int8_t)(held != 0.0f);
@@ -231,59 +270,27 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
           for (int s = 0; s < S; ++s) io.track_I[row * (S + 1) + s] = I[s];
           io.track_I[row * (S + 1) + S] = I_leak;
         }
-        if (recurrent && s_out != 0.0f && A.rec.pathway[n] >= 0) {
-          const int32_t pos = atomicAdd(&s_fcnt[q], 1);
-          store_agent(my_fired + q * range_n + pos, (int32_t)n);
-        }
-        v = v_next;
-        if (refractory) io.counter[bn] = counter;
-      }
-      io.v[bn] = v;
-#pragma unroll
-      for (int s = 0; s < S; ++s) {
-        io.g[(b * 2 * S + s) * N + n] = gr[s];
-        io.g[(b * 2 * S + S + s) * N + n] = gd[s];
+        if (recurrent && s_out != 0.0f)
+          atomicOr(&s_bits[q * words + (ln >> 5)], 1u << (ln & 31));
+        v[i] = v_next;
       }
     }
+    tick(my_time, last, 0);
     if (t == T) break;
 
-    // ---------------- publish the fired lists; group barrier ----------------
+    // ---------------- publish this step's spikes; arrive ----------------
     if (recurrent) {
       __syncthreads();
-      int32_t* my_count = A.fired_count + ((int64_t)buf * wgs + wg) * A.tpg_max;
-      if (threadIdx.x < tpg) store_agent(my_count + threadIdx.x, s_fcnt[threadIdx.x]);
-      if (!group_barrier(my_barrier, (uint32_t)((t + 1) * R), A.err, &s_flag)) return;
-      // prefix of the fired counts of the group's R workgroups, per trial slot
-      for (int64_t q = threadIdx.x; q < tpg; q += blockDim.x) {
-        int32_t run = 0;
-        for (int64_t rr = 0; rr < R; ++rr) {
-          s_pre[q * 65 + rr] = run;
-          run += load_agent(A.fired_count + ((int64_t)buf * wgs + g + rr * groups) * A.tpg_max + q);
-        }
-        s_pre[q * 65 + R] = run;
+      uint32_t* out_bits = A.bitmap + buf * B * R * words;
+      for (int64_t w = threadIdx.x; w < tpg * words; w += blockDim.x) {
+        const int64_t q = w / words, b = g + q * groups;
+        store_agent(out_bits + b * R * words + r * words + (w - q * words), s_bits[w]);
       }
+      barrier_arrive(my_barrier);
     }
-    __syncthreads();
+    tick(my_time, last, 1);
 
-    // ---------------- (P) push step t's events onto the owned targets ----------------
-    if (recurrent) {
-      for (int64_t q = 0; q < tpg; ++q) {
-        const int32_t total = s_pre[q * 65 + R];
-        for (int32_t f = threadIdx.x; f < total; f += blockDim.x) {
-          int32_t a = 0, z = (int32_t)R;  // find rr with pre[rr] <= f < pre[rr+1]
-          while (z - a > 1) {
-            int32_t m = (a + z) >> 1;
-            if (s_pre[q * 65 + m] <= f) a = m; else z = m;
-          }
-          const int64_t src_wg = g + (int64_t)a * groups;
-          const int32_t j = load_agent(A.fired + ((int64_t)buf * wgs + src_wg) * fstride +
-                                       q * range_n + (f - s_pre[q * 65 + a]));
-          const int32_t k = A.rec.pathway[j];
-          const int64_t* sp = A.rec.split + (int64_t)j * (R + 1) + r;
-          push_edges(acc, A.rec, sp[0], sp[1], lo, (k * tpg + q) * range_n, 1.0f, fscale);
-        }
-      }
-    }
+    // ---------------- (P) feedforward events of step t, between arrive and wait ----------
     if (A.ff.n_src > 0) {
       const int64_t n_in = io.n_in;
       for (int64_t q = 0; q < tpg; ++q) {
@@ -295,12 +302,55 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
           const int32_t k = A.ff.pathway[j];
           if (k < 0) continue;
           const int64_t* sp = A.ff.split + j * (R + 1) + r;
-          push_edges(acc, A.ff, sp[0], sp[1], lo, ((K_rec + k) * tpg + q) * range_n, xv, fscale);
+          push_edges(acc + ((K_rec + k) * tpg + q) * range_n, A.ff, sp[0], sp[1], lo, xv, fscale);
         }
       }
     }
+    tick(my_time, last, 2);
+
+    // ---------------- (P) recurrent events: wait, then walk the group's bitmap --------
+    if (recurrent) {
+      if (!barrier_wait(my_barrier, (uint32_t)((t + 1) * R), A.err, &s_flag)) return;
+      tick(my_time, last, 3);
+      const uint32_t* in_bits = A.bitmap + buf * B * R * words;
+      const int64_t total = R * words;
+      for (int64_t q = 0; q < tpg; ++q) {
+        const int64_t b = g + q * groups;
+        long long* row_base = acc + q * range_n;
+        for (int64_t w = threadIdx.x; w < total; w += blockDim.x) {
+          uint32_t bits = load_agent(in_bits + b * total + w);
+          while (bits) {
+            const int bit = __builtin_ctz(bits);
+            bits &= bits - 1;
+            const int64_t j = ((w / words) * range_n) + (w % words) * 32 + bit;
+            const int32_t k = A.rec.pathway[j];
+            if (k < 0) continue;
+            const int64_t* sp = A.rec.split + j * (R + 1) + r;
+            push_edges(row_base + k * tpg * range_n, A.rec, sp[0], sp[1], lo, 1.0f, fscale);
+          }
+        }
+      }
+      tick(my_time, last, 4);
+    }
     __syncthreads();
   }
+
+  // write the state back
+#pragma unroll
+  for (int i = 0; i < MAXI; ++i) {
+    const int64_t it = threadIdx.x + (int64_t)i * blockDim.x;
+    if (it < items) {
+      const int64_t q = it / nr, n = lo + (it - q * nr), b = g + q * groups;
+      io.v[b * N + n] = v[i];
+      if (refractory) io.counter[b * N + n] = counter[i];
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        io.g[(b * 2 * S + s) * N + n] = gr[i][s];
+        io.g[(b * 2 * S + S + s) * N + n] = gd[i][s];
+      }
+    }
+  }
+  if (A.timing && threadIdx.x < kPhases) A.timing[wg * kPhases + threadIdx.x] = s_time[threadIdx.x];
 }
 
 // ---------------------------------------------------------------------------------
@@ -524,42 +574,52 @@ static int64_t run_tpg_max(const wt_geometry* geo, int64_t B) {
 
 extern "C" int64_t wt_cond_run_scratch_bytes(const wt_geometry* geo, int64_t B, int64_t N) {
   (void)N;
-  const int64_t wgs = geo->groups * geo->R, tpg = run_tpg_max(geo, B);
+  const int64_t wgs = geo->groups * geo->R;
   int64_t bytes = 256;                                    // error flags
   bytes += geo->groups * 128;                             // barrier counters
-  bytes += 2 * wgs * tpg * geo->range_n * 4;              // fired segments
-  bytes += 2 * wgs * tpg * 4;                             // fired counts
+  bytes += 2 * B * geo->R * (geo->range_n / 32) * 4;      // fired bitmaps
+  bytes += wgs * kPhases * 8;                             // phase timing
   return bytes;
+}
+
+template <int S, int MAXI>
+static hipError_t launch_run(RunArgs& a, size_t lds, int block, hipStream_t stream, bool coop) {
+  const void* fn = reinterpret_cast<const void*>(&cond_run_kernel<S, MAXI>);
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  dim3 grid((unsigned)(a.geo.groups * a.geo.R)), blk((unsigned)block);
+  void* params[] = {&a};
+  if (coop) return hipLaunchCooperativeKernel(fn, grid, blk, params, (unsigned)lds, stream);
+  hipLaunchKernelGGL((cond_run_kernel<S, MAXI>), grid, blk, lds, stream, a);
+  return hipGetLastError();
 }
 
 template <int S>
 struct RunLaunch {
-  static hipError_t run(RunArgs& a, size_t lds, int block, hipStream_t stream, bool coop) {
-    const void* fn = reinterpret_cast<const void*>(&cond_run_kernel<S>);
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    dim3 grid((unsigned)(a.geo.groups * a.geo.R)), blk((unsigned)block);
-    void* params[] = {&a};
-    if (coop) return hipLaunchCooperativeKernel(fn, grid, blk, params, (unsigned)lds, stream);
-    hipLaunchKernelGGL(cond_run_kernel<S>, grid, blk, lds, stream, a);
-    return hipGetLastError();
+  static hipError_t run(RunArgs& a, size_t lds, int block, int64_t per_thread,
+                        hipStream_t stream, bool coop) {
+    if (per_thread <= 1) return launch_run<S, 1>(a, lds, block, stream, coop);
+    if (per_thread <= 2) return launch_run<S, 2>(a, lds, block, stream, coop);
+    if (per_thread <= 4) return launch_run<S, 4>(a, lds, block, stream, coop);
+    if (per_thread <= 8) return launch_run<S, 8>(a, lds, block, stream, coop);
+    return hipErrorInvalidValue;
   }
 };
 
-extern "C" int wt_cond_run(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
-                           const wt_geometry* geo, const wt_run_io* io, void* scratch,
-                           wt_stream_t stream) {
+static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
+                    const wt_geometry* geo, const wt_run_io* io, void* scratch,
+                    uint64_t* timing, wt_stream_t stream) {
   if (!tab || !rec || !ff || !geo || !io || !scratch || !io->spikes || !io->v || !io->g)
     return hipErrorInvalidValue;
   if (tab->n_ref && !io->counter) return hipErrorInvalidValue;
   if (tab->S < 1 || tab->S > WT_MAX_S || tab->K < 0 || tab->K > WT_MAX_K || tab->K_rec > tab->K)
     return hipErrorInvalidValue;
-  if (geo->groups < 1 || geo->groups > kMaxGroups || geo->R < 1 || geo->R > 64 ||
-      geo->range_n < 1 || geo->R * geo->range_n < tab->N || geo->frac_bits < 0 ||
-      geo->frac_bits > 60)
+  if (geo->groups < 1 || geo->groups > kMaxGroups || geo->R < 1 || geo->R > 256 ||
+      geo->range_n < 32 || geo->range_n % 32 != 0 || geo->R * geo->range_n < tab->N ||
+      geo->frac_bits < 0 || geo->frac_bits > 60)
     return hipErrorInvalidValue;
   const int64_t tpg = run_tpg_max(geo, io->B);
-  if (tpg > 64 || io->B < 1 || io->T < 0) return hipErrorInvalidValue;
+  if (io->B < 1 || io->T < 0) return hipErrorInvalidValue;
   if ((io->v_saved != nullptr) != (io->G_saved != nullptr)) return hipErrorInvalidValue;
   if (io->track_v && (!io->track_I || !io->track_g)) return hipErrorInvalidValue;
   if (rec->n_src > 0 && rec->n_src != tab->N) return hipErrorInvalidValue;
@@ -572,26 +632,39 @@ extern "C" int wt_cond_run(const wt_tables* tab, const wt_side* rec, const wt_si
   a.ff = *ff;
   a.geo = *geo;
   a.io = *io;
-  a.tpg_max = tpg;
+  a.words = geo->range_n / 32;
   char* base = static_cast<char*>(scratch);
   a.err = reinterpret_cast<uint32_t*>(base);
   a.barrier = reinterpret_cast<uint32_t*>(base + 256);
-  a.fired = reinterpret_cast<int32_t*>(base + 256 + geo->groups * 128);
-  a.fired_count = a.fired + 2 * geo->groups * geo->R * tpg * geo->range_n;
+  a.bitmap = reinterpret_cast<uint32_t*>(base + 256 + geo->groups * 128);
+  a.timing = timing;
 
-  const size_t lds = (size_t)(tab->K > 0 ? tab->K : 1) * tpg * geo->range_n * sizeof(long long);
+  const size_t lds = (size_t)(tab->K > 0 ? tab->K : 1) * tpg * geo->range_n * sizeof(long long) +
+                     (size_t)tpg * a.words * sizeof(uint32_t);
   int dev = 0, max_lds = 0;
   hipError_t qe = hipGetDevice(&dev);
   if (qe == hipSuccess)
     qe = hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   if (qe != hipSuccess) return qe;
-  const size_t static_lds = 64 * 4 + 64 * 65 * 4 + 16;
-  if (lds + static_lds > (size_t)max_lds) return hipErrorInvalidValue;
+  if (lds + 64 > (size_t)max_lds) return hipErrorInvalidValue;
   const int64_t per_wg = tpg * geo->range_n;
-  int block = per_wg >= kRunBlock ? kRunBlock : (int)(((per_wg + 63) / 64) * 64);
-  if (block < 64) block = 64;
+  const int block = per_wg >= kRunBlock ? kRunBlock : (int)(((per_wg + 63) / 64) * 64);
+  const int64_t per_thread = (per_wg + block - 1) / block;
   const bool coop = tab->K_rec > 0 && rec->n_src > 0 && geo->R > 1;
-  return dispatch_S<RunLaunch>(tab->S, a, lds, block, (hipStream_t)stream, coop);
+  return dispatch_S<RunLaunch>(tab->S, a, lds, block, per_thread, (hipStream_t)stream, coop);
+}
+
+extern "C" int wt_cond_run(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
+                           const wt_geometry* geo, const wt_run_io* io, void* scratch,
+                           wt_stream_t stream) {
+  return run_impl(tab, rec, ff, geo, io, scratch, nullptr, stream);
+}
+
+extern "C" int wt_cond_run_timed(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
+                                 const wt_geometry* geo, const wt_run_io* io, void* scratch,
+                                 uint64_t* timing, wt_stream_t stream) {
+  if (!timing) return hipErrorInvalidValue;
+  return run_impl(tab, rec, ff, geo, io, scratch, timing, stream);
 }
 
 extern "C" int wt_split_ranges(const int64_t* indptr, const int32_t* targets, int64_t n_src,

@@ -44,6 +44,9 @@ MAX_GROUPS = 8
 #: When a list, every ``wt_cond_run`` launch appends a pair of events recorded on its
 #: stream just before and after it (``bench.py`` times the kernel with them).
 LAUNCH_EVENTS: list | None = None
+#: When a list, launches run ``wt_cond_run_timed`` and append the per-workgroup phase
+#: ticks ``(groups * R, 5)`` (profiling only).
+PHASE_TIMING: list | None = None
 
 
 # =====================================================================
@@ -206,24 +209,28 @@ def _device_info(device) -> tuple[int, int]:
 
 def geometry(B: int, N: int, K: int, n_cu: int, max_lds: int) -> tuple[int, int, int]:
     """``(groups, R, range_n)``: trials round-robin over up to 8 groups (one per XCD);
-    each group's targets split over R workgroups, about one neuron-trial per thread,
-    within the LDS budget of the int64 accumulator ``K * trials * range_n``."""
+    each group's targets split over R workgroups (range_n a multiple of 32), about one
+    (trial, neuron) item per thread and at most 8 per thread (they live in registers),
+    within the LDS budget of the int64 accumulator ``K * trials * range_n`` and the
+    fired bitmap."""
     groups = max(1, min(MAX_GROUPS, B))
     tpg = -(-B // groups)
-    if tpg > 64:
-        raise ValueError(f"batch {B} is too large for one launch (at most 512 trials)")
-    limit = max(1, min(64, n_cu // groups))
+    limit = max(1, n_cu // groups)
+    budget = max_lds - 1024
+
+    def fits(R):
+        range_n = -(-(-(-N // R)) // 32) * 32
+        lds = max(K, 1) * tpg * range_n * 8 + tpg * (range_n // 32) * 4
+        return lds <= budget and tpg * range_n <= 8 * BLOCK, range_n
+
     R = max(1, min(limit, -(-N * tpg // BLOCK)))
-    budget = max_lds - 20 * 1024
-    while True:
-        range_n = -(-N // R)
-        if max(K, 1) * tpg * range_n * 8 <= budget or R >= limit:
-            break
+    ok, range_n = fits(R)
+    while not ok and R < limit:
         R += 1
-    R = -(-N // range_n)
-    if max(K, 1) * tpg * range_n * 8 > budget:
-        raise ValueError("network too large for one launch's LDS accumulator")
-    return groups, R, range_n
+        ok, range_n = fits(R)
+    if not ok:
+        raise ValueError(f"network too large for one launch (N {N}, batch {B}, {K} pathways)")
+    return groups, -(-N // range_n), range_n
 
 
 def _frac_bits(bound: float) -> int:
@@ -338,7 +345,14 @@ def _launch(L: _Plan, x, scale, v, g, counter, spikes, prob, saved, tracked,
     if LAUNCH_EVENTS is not None:
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
-    _lib.check(lib.wt_cond_run(tab, rec, ff, geo, io, scratch.data_ptr(), L.stream), "wt_cond_run")
+    if PHASE_TIMING is not None:
+        ticks = torch.zeros((groups * R, 5), dtype=torch.int64, device=L.device)
+        _lib.check(lib.wt_cond_run_timed(tab, rec, ff, geo, io, scratch.data_ptr(),
+                                         ticks.data_ptr(), L.stream), "wt_cond_run_timed")
+        PHASE_TIMING.append(ticks)
+    else:
+        _lib.check(lib.wt_cond_run(tab, rec, ff, geo, io, scratch.data_ptr(), L.stream),
+                   "wt_cond_run")
     if LAUNCH_EVENTS is not None:
         stop.record()
         LAUNCH_EVENTS.append((start, stop))

@@ -177,7 +177,7 @@ def power_law_degrees(rng, n, exponent, k_min, k_max):
 
 def fly_scale(N=140_000, n_types=8000, exponent=2.1, mean_degree=357, k_max=8000,
               count_mean=4.0, frac_e_types=0.7, frac_sensory=0.05, rate_hz=10.0, B=8,
-              T=2000, dt=0.1, seed=2, w_e=0.04, w_i=0.16, w_in=12.0, sf_sigma=0.5,
+              T=2000, dt=0.1, seed=2, w_e=1.0, w_i=5.0, w_in=30.0, sf_sigma=0.5,
               device="cpu", input_seed=0) -> Workload:
     """Configuration 2: a synthetic fly-scale conductance-LIF network.
 
@@ -188,7 +188,9 @@ def fly_scale(N=140_000, n_types=8000, exponent=2.1, mean_degree=357, k_max=8000
     scaling factor of its (source type, target type) pair — a lognormal(0, ``sf_sigma``)
     table of ``n_types``² entries, the quantity a model of this size would learn —
     times ``w_e`` / ``w_i`` by the source's receptor kind. A random 5% of neurons are
-    sensory, each driven by its own Poisson channel (weight ``w_in``)."""
+    sensory, each driven by its own Poisson channel (weight ``w_in``). The default
+    weights were chosen by a sweep on the GPU for a stable, irregular state at the
+    configuration's 10 Hz mean rate (9.3 Hz measured, 2% of neurons silent)."""
     rng = np.random.default_rng(seed)
     cell_type = rng.integers(0, n_types, N)
     type_is_e = rng.random(n_types) < frac_e_types
