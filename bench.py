@@ -48,6 +48,18 @@ def delivered_events(spikes, x, drive):
     return float(per_src @ out_rec + per_in @ out_ff)
 
 
+def measured_traffic():
+    """HBM bytes per launch of wt_cond_run on this workload, from the committed rocprofv3
+    FETCH_SIZE + WRITE_SIZE summary (calibrated against a copy of known size), or None."""
+    path = ROOT / "profiles" / "wt_cond_run_config2_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
 def cpu_baseline(wl, steps):
     """The oracle (the reference's PyTorch step restated, compressed propagation) on the
     first ``steps`` steps of the same workload, on this host's cores."""
@@ -82,7 +94,18 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--cpu-steps", type=int, default=int(os.environ.get("BENCH_CPU_STEPS", 100)))
     ap.add_argument("--T", type=int, default=2000)
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="only run one device-to-device copy of this many bytes (the "
+                         "reference kernel for calibrating rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
+    if args.copy_bytes:
+        src = torch.ones(args.copy_bytes // 4, device="cuda:0")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": args.copy_bytes}))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py runs on one GPU only: this build has no multi-GPU path "
               "(see DESIGN.md for how the hot path would shard)", file=sys.stderr)
@@ -150,7 +173,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": measured_traffic(),
             "kernel": "wt_cond_run",
             "kernel_ms": kernel_ms,
             "algorithmic_bytes_per_launch": bytes_per_launch,

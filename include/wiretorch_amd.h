@@ -50,6 +50,11 @@ typedef struct {
   const float* scale;    /* (K,N) */
   const float* dt;       /* 0-d */
   const float* surr;     /* 0-d */
+  /* The same per-neuron values deduplicated (used by wt_cond_run): n_types <= 256 rows
+   * of (theta, U_reset, E_L, C_m, beta, n_ref, scale[0..K-1]); type_of (N,) picks a row. */
+  const float* types;
+  const int32_t* type_of;
+  int64_t n_types;
   int64_t N, S, K, K_rec;
 } wt_tables;
 
@@ -89,8 +94,8 @@ int wt_split_ranges(const int64_t* indptr, const int32_t* targets, int64_t n_src
  *   State v, g, counter is updated in place. Outputs: spikes (required); prob,
  *   v_saved, G_saved, held, A_saved (K,B,T,N) and the tracked v/I/g of trial track_b
  *   (-1: all) may each be NULL.
- *   scratch: device workspace of wt_cond_run_scratch_bytes bytes, zeroed by the
- *   caller before each launch. */
+ *   scratch: device workspace of wt_cond_run_scratch_bytes bytes whose first
+ *   wt_cond_run_scratch_zeroed bytes the caller zeroes before each launch. */
 typedef struct {
   const float* x;
   int64_t B, T, n_in;
@@ -109,7 +114,9 @@ typedef struct {
   int64_t track_b;
 } wt_run_io;
 
-int64_t wt_cond_run_scratch_bytes(const wt_geometry* geo, int64_t B, int64_t N);
+int64_t wt_cond_run_scratch_bytes(const wt_geometry* geo, int64_t B, int64_t T);
+/* Leading bytes of the scratch that must be zero at each launch (the rest need not). */
+int64_t wt_cond_run_scratch_zeroed(const wt_geometry* geo);
 int wt_cond_run(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
                 const wt_geometry* geo, const wt_run_io* io, void* scratch,
                 wt_stream_t stream);

@@ -19,7 +19,8 @@ class Tables(ctypes.Structure):
     _fields_ = [
         ("theta", P), ("U_reset", P), ("E_L", P), ("C_m", P), ("beta", P), ("n_ref", P),
         ("E_syn", P), ("g_clip", P), ("decay", P), ("jump", P), ("made", P), ("scale", P),
-        ("dt", P), ("surr", P), ("N", I64), ("S", I64), ("K", I64), ("K_rec", I64),
+        ("dt", P), ("surr", P), ("types", P), ("type_of", P), ("n_types", I64),
+        ("N", I64), ("S", I64), ("K", I64), ("K_rec", I64),
     ]  # fmt: skip
 
 
@@ -56,6 +57,7 @@ class BackwardIO(ctypes.Structure):
 SIGNATURES = {
     "wt_split_ranges": (ctypes.c_int, [P, P, I64, I64, I64, P, P]),
     "wt_cond_run_scratch_bytes": (I64, [ctypes.POINTER(Geometry), I64, I64]),
+    "wt_cond_run_scratch_zeroed": (I64, [ctypes.POINTER(Geometry)]),
     "wt_cond_run": (ctypes.c_int, [ctypes.POINTER(Tables), ctypes.POINTER(Side),
                                    ctypes.POINTER(Side), ctypes.POINTER(Geometry),
                                    ctypes.POINTER(RunIO), P, P]),

@@ -11,11 +11,14 @@ from __future__ import annotations
 import os
 import subprocess
 import sys
+import time
 from pathlib import Path
 
 PACKAGE = Path(__file__).resolve().parent
 LIBRARY = PACKAGE / "libwiretorch_amd.so"
-SOURCES = [PACKAGE / "csrc" / "wt_kernels.hip"]
+CSRC = PACKAGE / "csrc"
+SOURCES = [CSRC / "wt_kernels.hip"] + [CSRC / f"wt_run_s{s}.hip" for s in range(1, 9)]
+OBJ_DIR = PACKAGE / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950",
@@ -24,22 +27,45 @@ FLAGS = [
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-fPIC",
-    "-shared",
 ]
 
 
-def build(verbose: bool = False) -> Path:
-    tmp = LIBRARY.with_suffix(".so.tmp")
-    cmd = [HIPCC, *FLAGS, *map(str, SOURCES), "-o", str(tmp)]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
+def _filter(stderr: str) -> str:
     noise = "is not a recognized feature for this target"
-    errors = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
+    return "\n".join(l for l in stderr.splitlines() if noise not in l)
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every source to an object (in parallel), then link the shared library."""
+    OBJ_DIR.mkdir(exist_ok=True)
+    jobs = jobs or min(len(SOURCES), os.cpu_count() or 1, 16)
+    procs = []
+    objects = []
+    for src in SOURCES:
+        obj = OBJ_DIR / (src.stem + ".o")
+        objects.append(obj)
+        cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        while len([p for p in procs if p[0].poll() is None]) >= jobs:
+            procs[0][0].wait() if procs[0][0].poll() is None else None
+            time.sleep(0.05)
+        procs.append((subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                                       text=True), src))
+    failed = []
+    for proc, src in procs:
+        out, err = proc.communicate()
+        if proc.returncode != 0:
+            failed.append(f"{src.name}:\n{_filter(err)}")
+        elif verbose and _filter(err).strip():
+            print(_filter(err), file=sys.stderr)
+    if failed:
+        raise RuntimeError("hipcc failed:\n" + "\n".join(failed))
+    tmp = LIBRARY.with_suffix(".so.tmp")
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{errors}")
-    if verbose and errors.strip():
-        print(errors, file=sys.stderr)
+        raise RuntimeError(f"link failed ({proc.returncode}):\n{_filter(proc.stderr)}")
     os.replace(tmp, LIBRARY)
     return LIBRARY
 

@@ -30,327 +30,33 @@
 #include "../../include/wiretorch_amd.h"
 #include "wt_math.h"
 
+#include "wt_run.h"
+
 namespace wt {
 
-constexpr int kRunBlock = 1024;
-constexpr int kMaxGroups = 64;
-
-struct RunArgs {
-  wt_tables tab;
-  wt_side rec, ff;
-  wt_geometry geo;
-  wt_run_io io;
-  // scratch
-  uint32_t* err;       // [0]: error flags
-  uint32_t* barrier;   // one counter per group, 128 bytes apart
-  uint32_t* bitmap;    // [2][B][R * words]: which neurons fired, per trial
-  uint64_t* timing;    // [wgs][kPhases] wall-clock ticks per phase, or null
-  int64_t words;       // bitmap words per workgroup range (range_n / 32)
-};
-
-constexpr int kPhases = 5;  // update, publish, feedforward push, barrier wait, recurrent push
-
-__device__ inline void store_agent(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ inline uint32_t load_agent(const uint32_t* p) {
-  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Split group barrier. arrive(): every thread's stores complete, then one arrival per
-// workgroup on the group's counter. wait(): bounded (2 s of wall clock), giving up as
-// soon as any workgroup has flagged an error. Work placed between the two overlaps
-// the other workgroups' progress.
-__device__ inline void barrier_arrive(uint32_t* counter) {
-  __builtin_amdgcn_s_waitcnt(0);
+// The nonzero inputs of each (trial, step) row of x: one workgroup per row; at most
+// kInCap listed (count above kInCap: the row is scanned in place by the run kernel).
+__global__ __launch_bounds__(256) void compact_input_kernel(const float* x, int64_t rows,
+                                                            int64_t n_in, int32_t* count,
+                                                            int32_t* idx, float* val) {
+  __shared__ int32_t s_n;
+  const int64_t row = blockIdx.x;
+  if (row >= rows) return;
+  if (threadIdx.x == 0) s_n = 0;
   __syncthreads();
-  if (threadIdx.x == 0)
-    __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ inline bool barrier_wait(uint32_t* counter, uint32_t target, uint32_t* err,
-                                    uint32_t* s_flag) {
-  if (threadIdx.x == 0) {
-    uint32_t bad = 0;
-    uint64_t start = wall_clock64();
-    uint32_t polls = 0;
-    while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      __builtin_amdgcn_s_sleep(1);
-      if ((++polls & 63u) == 0) {
-        if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) { bad = 1; break; }
-        if (wall_clock64() - start > 200000000ull) {  // 2 s at the 100 MHz wall clock
-          __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          bad = 1;
-          break;
-        }
+  const float* xr = x + row * n_in;
+  for (int64_t j = threadIdx.x; j < n_in; j += blockDim.x) {
+    const float xv = xr[j];
+    if (xv != 0.0f) {
+      const int32_t pos = atomicAdd(&s_n, 1);
+      if (pos < kInCap) {
+        idx[row * kInCap + pos] = (int32_t)j;
+        val[row * kInCap + pos] = xv;
       }
     }
-    *s_flag = bad;
   }
   __syncthreads();
-  return *s_flag == 0;
-}
-
-template <int S>
-__device__ inline void load_synapses(const wt_tables& tab, Synapses<S>& syn) {
-#pragma unroll
-  for (int s = 0; s < S; ++s) {
-    syn.E[s] = tab.E_syn[s];
-    syn.clip[s] = tab.g_clip[s];
-    syn.decay_r[s] = tab.decay[s];
-    syn.decay_d[s] = tab.decay[S + s];
-    syn.jump_r[s] = tab.jump[s];
-    syn.jump_d[s] = tab.jump[S + s];
-  }
-}
-
-// Adds the synapses [e0, e1) of one source (all onto this workgroup's targets: local
-// index target - lo) times `value` to the accumulator row `row`. Loads are issued four
-// at a time ahead of their atomics.
-__device__ inline void push_edges(long long* row, const wt_side& side, int64_t e0, int64_t e1,
-                                  int64_t lo, float value, float fscale) {
-  int64_t e = e0;
-  for (; e + 4 <= e1; e += 4) {
-    int32_t t[4];
-    float w[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      t[u] = side.targets[e + u];
-      w[u] = side.weights[e + u];
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float x = value == 1.0f ? w[u] : value * w[u];
-      atomicAdd(reinterpret_cast<unsigned long long*>(row + (t[u] - lo)),
-                (unsigned long long)to_fixed(x, fscale));
-    }
-  }
-  for (; e < e1; ++e) {
-    const float x = value == 1.0f ? side.weights[e] : value * side.weights[e];
-    atomicAdd(reinterpret_cast<unsigned long long*>(row + (side.targets[e] - lo)),
-              (unsigned long long)to_fixed(x, fscale));
-  }
-}
-
-__device__ inline void tick(uint64_t* acc_t, uint64_t& last, int phase) {
-  if (acc_t && threadIdx.x == 0) {
-    const uint64_t now = wall_clock64();
-    acc_t[phase] += now - last;
-    last = now;
-  }
-}
-
-// The persistent forward. Each thread owns up to MAXI (trial, neuron) items — item
-// threadIdx.x + i * blockDim.x of its workgroup — whose state stays in registers for
-// the whole launch.
-template <int S, int MAXI>
-__global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
-  extern __shared__ long long acc[];  // [K][tpg][range_n], then the local fired bitmap
-  __shared__ uint32_t s_flag;
-  __shared__ uint64_t s_time[kPhases];
-
-  const wt_tables& tab = A.tab;
-  const wt_run_io& io = A.io;
-  const int64_t groups = A.geo.groups, R = A.geo.R, range_n = A.geo.range_n;
-  const int64_t N = tab.N, K = tab.K, K_rec = tab.K_rec, B = io.B, T = io.T;
-  const int64_t wg = blockIdx.x;
-  const int64_t g = wg % groups, r = wg / groups;
-  const int64_t tpg = g < B ? (B - g + groups - 1) / groups : 0;
-  if (tpg == 0) return;  // no trial in this group: it takes part in nothing
-  const int64_t lo = r * range_n;
-  const int64_t nr = lo < N ? (N - lo < range_n ? N - lo : range_n) : 0;
-  const int64_t items = tpg * nr;
-  const int64_t acc_len = K * tpg * range_n;
-  const int64_t words = A.words;  // bitmap words of one trial's range
-  uint32_t* s_bits = reinterpret_cast<uint32_t*>(acc + acc_len);  // [tpg][words]
-  const bool refractory = tab.n_ref != nullptr;
-  const bool recurrent = K_rec > 0 && A.rec.n_src > 0;
-  const float dt = *tab.dt;
-  const float fscale = ldexpf(1.0f, (int)A.geo.frac_bits);
-  const float inv_fscale = ldexpf(1.0f, -(int)A.geo.frac_bits);
-  Synapses<S> syn;
-  load_synapses<S>(tab, syn);
-  uint64_t* my_time = A.timing ? s_time : nullptr;
-  if (threadIdx.x < kPhases) s_time[threadIdx.x] = 0;
-  uint64_t last = wall_clock64();
-
-  for (int64_t i = threadIdx.x; i < acc_len; i += blockDim.x) acc[i] = 0;
-
-  // Registers: the owned items' state.
-  float v[MAXI], theta[MAXI], gr[MAXI][S], gd[MAXI][S];
-  int32_t counter[MAXI];
-#pragma unroll
-  for (int i = 0; i < MAXI; ++i) {
-    const int64_t it = threadIdx.x + (int64_t)i * blockDim.x;
-    if (it < items) {
-      const int64_t q = it / nr, n = lo + (it - q * nr), b = g + q * groups;
-      v[i] = io.v[b * N + n];
-      theta[i] = tab.theta[n];
-      counter[i] = refractory ? io.counter[b * N + n] : 0;
-#pragma unroll
-      for (int s = 0; s < S; ++s) {
-        gr[i][s] = io.g[(b * 2 * S + s) * N + n];
-        gd[i][s] = io.g[(b * 2 * S + S + s) * N + n];
-      }
-    }
-  }
-  uint32_t* my_barrier = A.barrier + g * 32;
-
-  for (int64_t t = 0; t <= T; ++t) {
-    const int64_t buf = t & 1;
-    for (int64_t w = threadIdx.x; w < tpg * words; w += blockDim.x) s_bits[w] = 0;
-    __syncthreads();
-
-    // ---------------- (A) update the owned neurons ----------------
-#pragma unroll
-    for (int i = 0; i < MAXI; ++i) {
-      const int64_t it = threadIdx.x + (int64_t)i * blockDim.x;
-      if (it >= items) continue;
-      const int64_t q = it / nr, ln = it - q * nr, n = lo + ln;
-      const int64_t b = g + q * groups;
-      if (t > 0) {
-        // g <- g * decay, then each pathway's activation times its kernel, in order
-        // (dynamics.py:206-208; kernel = jump * scale * made, dynamics.py:95-100).
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-          gr[i][s] = gr[i][s] * syn.decay_r[s];
-          gd[i][s] = gd[i][s] * syn.decay_d[s];
-        }
-        for (int64_t k = 0; k < K; ++k) {
-          long long* cell = acc + (k * tpg + q) * range_n + ln;
-          const float a = from_fixed(*cell, inv_fscale);
-          *cell = 0;
-          if (io.A_saved) io.A_saved[((k * B + b) * T + (t - 1)) * N + n] = a;
-          const float sc = tab.scale[k * N + n];
-#pragma unroll
-          for (int s = 0; s < S; ++s) {
-            const float mk = tab.made[k * S + s];
-            if (mk != 0.0f) {
-              gr[i][s] = gr[i][s] + a * (syn.jump_r[s] * sc * mk);
-              gd[i][s] = gd[i][s] + a * (syn.jump_d[s] * sc * mk);
-            }
-          }
-        }
-        if (io.track_g && (io.track_b < 0 || io.track_b == b)) {
-          const int64_t bt = io.track_b < 0 ? b : 0;
-          float* out = io.track_g + ((bt * T + (t - 1)) * N + n) * 2 * S;
-#pragma unroll
-          for (int s = 0; s < S; ++s) {
-            out[s] = gr[i][s];
-            out[S + s] = gd[i][s];
-          }
-        }
-      }
-      if (t < T) {
-        float r_hold, held;
-        const float s_out = spike_step(v[i], theta[i], counter[i],
-                                       refractory ? tab.n_ref[n] : 0, refractory, r_hold, held);
-        const int64_t out = (b * T + t) * N + n;
-        io.spikes[out] = s_out;
-        if (io.prob) {
-          const float pr = 1.0f / (1.0f + expf(-(*tab.surr * (v[i] - theta[i]))));
-          io.prob[out] = refractory ? pr * (1.0f - held) : pr;
-        }
-        const float C_m = tab.C_m[n];
-        const Leak lk = leak(C_m, tab.beta[n], dt);
-        float G[S], I[S], I_leak;
-        const float v_next = membrane<S>(v[i], r_hold, gr[i], gd[i], syn, tab.E_L[n], C_m,
-                                         tab.U_reset[n], lk, dt, G, I, I_leak);
-        if (io.v_saved) {
-          io.v_saved[out] = v[i];
-#pragma unroll
-          for (int s = 0; s < S; ++s) io.G_saved[out * S + s] = G[s];
-          if (refractory && io.held) io.held[out] = (int8_t)(held != 0.0f);
-        }
-        if (io.track_v && (io.track_b < 0 || io.track_b == b)) {
-          const int64_t bt = io.track_b < 0 ? b : 0;
-          const int64_t row = (bt * T + t) * N + n;
-          io.track_v[row] = v_next;
-#pragma unroll
-          for (int s = 0; s < S; ++s) io.track_I[row * (S + 1) + s] = I[s];
-          io.track_I[row * (S + 1) + S] = I_leak;
-        }
-        if (recurrent && s_out != 0.0f)
-          atomicOr(&s_bits[q * words + (ln >> 5)], 1u << (ln & 31));
-        v[i] = v_next;
-      }
-    }
-    tick(my_time, last, 0);
-    if (t == T) break;
-
-    // ---------------- publish this step's spikes; arrive ----------------
-    if (recurrent) {
-      __syncthreads();
-      uint32_t* out_bits = A.bitmap + buf * B * R * words;
-      for (int64_t w = threadIdx.x; w < tpg * words; w += blockDim.x) {
-        const int64_t q = w / words, b = g + q * groups;
-        store_agent(out_bits + b * R * words + r * words + (w - q * words), s_bits[w]);
-      }
-      barrier_arrive(my_barrier);
-    }
-    tick(my_time, last, 1);
-
-    // ---------------- (P) feedforward events of step t, between arrive and wait ----------
-    if (A.ff.n_src > 0) {
-      const int64_t n_in = io.n_in;
-      for (int64_t q = 0; q < tpg; ++q) {
-        const int64_t b = g + q * groups;
-        const float* xrow = io.x + (b * T + t) * n_in;
-        for (int64_t j = threadIdx.x; j < n_in; j += blockDim.x) {
-          const float xv = xrow[j];
-          if (xv == 0.0f) continue;
-          const int32_t k = A.ff.pathway[j];
-          if (k < 0) continue;
-          const int64_t* sp = A.ff.split + j * (R + 1) + r;
-          push_edges(acc + ((K_rec + k) * tpg + q) * range_n, A.ff, sp[0], sp[1], lo, xv, fscale);
-        }
-      }
-    }
-    tick(my_time, last, 2);
-
-    // ---------------- (P) recurrent events: wait, then walk the group's bitmap --------
-    if (recurrent) {
-      if (!barrier_wait(my_barrier, (uint32_t)((t + 1) * R), A.err, &s_flag)) return;
-      tick(my_time, last, 3);
-      const uint32_t* in_bits = A.bitmap + buf * B * R * words;
-      const int64_t total = R * words;
-      for (int64_t q = 0; q < tpg; ++q) {
-        const int64_t b = g + q * groups;
-        long long* row_base = acc + q * range_n;
-        for (int64_t w = threadIdx.x; w < total; w += blockDim.x) {
-          uint32_t bits = load_agent(in_bits + b * total + w);
-          while (bits) {
-            const int bit = __builtin_ctz(bits);
-            bits &= bits - 1;
-            const int64_t j = ((w / words) * range_n) + (w % words) * 32 + bit;
-            const int32_t k = A.rec.pathway[j];
-            if (k < 0) continue;
-            const int64_t* sp = A.rec.split + j * (R + 1) + r;
-            push_edges(row_base + k * tpg * range_n, A.rec, sp[0], sp[1], lo, 1.0f, fscale);
-          }
-        }
-      }
-      tick(my_time, last, 4);
-    }
-    __syncthreads();
-  }
-
-  // write the state back
-#pragma unroll
-  for (int i = 0; i < MAXI; ++i) {
-    const int64_t it = threadIdx.x + (int64_t)i * blockDim.x;
-    if (it < items) {
-      const int64_t q = it / nr, n = lo + (it - q * nr), b = g + q * groups;
-      io.v[b * N + n] = v[i];
-      if (refractory) io.counter[b * N + n] = counter[i];
-#pragma unroll
-      for (int s = 0; s < S; ++s) {
-        io.g[(b * 2 * S + s) * N + n] = gr[i][s];
-        io.g[(b * 2 * S + S + s) * N + n] = gd[i][s];
-      }
-    }
-  }
-  if (A.timing && threadIdx.x < kPhases) A.timing[wg * kPhases + threadIdx.x] = s_time[threadIdx.x];
+  if (threadIdx.x == 0) count[row] = s_n;
 }
 
 // ---------------------------------------------------------------------------------
@@ -553,6 +259,16 @@ __global__ void edge_source_kernel(const int64_t* indptr, int64_t n_src, int64_t
 // ===================================================================================
 using namespace wt;
 
+// RunLaunch<S>::run is compiled in wt_run_s<S>.hip.
+extern template struct wt::RunLaunch<1>;
+extern template struct wt::RunLaunch<2>;
+extern template struct wt::RunLaunch<3>;
+extern template struct wt::RunLaunch<4>;
+extern template struct wt::RunLaunch<5>;
+extern template struct wt::RunLaunch<6>;
+extern template struct wt::RunLaunch<7>;
+extern template struct wt::RunLaunch<8>;
+
 template <template <int> class F, typename... Args>
 static hipError_t dispatch_S(int64_t S, Args&&... args) {
   switch (S) {
@@ -572,39 +288,22 @@ static int64_t run_tpg_max(const wt_geometry* geo, int64_t B) {
   return (B + geo->groups - 1) / geo->groups;
 }
 
-extern "C" int64_t wt_cond_run_scratch_bytes(const wt_geometry* geo, int64_t B, int64_t N) {
-  (void)N;
-  const int64_t wgs = geo->groups * geo->R;
-  int64_t bytes = 256;                                    // error flags
-  bytes += geo->groups * 128;                             // barrier counters
+// Scratch: [0, zeroed) must be zero at launch (error flags, barrier counters); the rest
+// (fired bitmaps, the input lists) is written before it is read.
+static int64_t scratch_zeroed(const wt_geometry* geo) { return 256 + geo->groups * 128; }
+
+extern "C" int64_t wt_cond_run_scratch_bytes(const wt_geometry* geo, int64_t B, int64_t T) {
+  int64_t bytes = scratch_zeroed(geo);
   bytes += 2 * B * geo->R * (geo->range_n / 32) * 4;      // fired bitmaps
-  bytes += wgs * kPhases * 8;                             // phase timing
+  bytes = (bytes + 255) / 256 * 256;
+  bytes += B * T * 4;                                     // input counts
+  bytes += B * T * kInCap * 8;                            // input indices and values
   return bytes;
 }
 
-template <int S, int MAXI>
-static hipError_t launch_run(RunArgs& a, size_t lds, int block, hipStream_t stream, bool coop) {
-  const void* fn = reinterpret_cast<const void*>(&cond_run_kernel<S, MAXI>);
-  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (e != hipSuccess) return e;
-  dim3 grid((unsigned)(a.geo.groups * a.geo.R)), blk((unsigned)block);
-  void* params[] = {&a};
-  if (coop) return hipLaunchCooperativeKernel(fn, grid, blk, params, (unsigned)lds, stream);
-  hipLaunchKernelGGL((cond_run_kernel<S, MAXI>), grid, blk, lds, stream, a);
-  return hipGetLastError();
+extern "C" int64_t wt_cond_run_scratch_zeroed(const wt_geometry* geo) {
+  return scratch_zeroed(geo);
 }
-
-template <int S>
-struct RunLaunch {
-  static hipError_t run(RunArgs& a, size_t lds, int block, int64_t per_thread,
-                        hipStream_t stream, bool coop) {
-    if (per_thread <= 1) return launch_run<S, 1>(a, lds, block, stream, coop);
-    if (per_thread <= 2) return launch_run<S, 2>(a, lds, block, stream, coop);
-    if (per_thread <= 4) return launch_run<S, 4>(a, lds, block, stream, coop);
-    if (per_thread <= 8) return launch_run<S, 8>(a, lds, block, stream, coop);
-    return hipErrorInvalidValue;
-  }
-};
 
 static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
                     const wt_geometry* geo, const wt_run_io* io, void* scratch,
@@ -636,17 +335,38 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
   char* base = static_cast<char*>(scratch);
   a.err = reinterpret_cast<uint32_t*>(base);
   a.barrier = reinterpret_cast<uint32_t*>(base + 256);
-  a.bitmap = reinterpret_cast<uint32_t*>(base + 256 + geo->groups * 128);
+  a.bitmap = reinterpret_cast<uint32_t*>(base + scratch_zeroed(geo));
+  int64_t off = scratch_zeroed(geo) + 2 * io->B * geo->R * a.words * 4;
+  off = (off + 255) / 256 * 256;
+  int32_t* in_count = reinterpret_cast<int32_t*>(base + off);
+  off += io->B * io->T * 4;
+  int32_t* in_idx = reinterpret_cast<int32_t*>(base + off);
+  float* in_val = reinterpret_cast<float*>(base + off + io->B * io->T * kInCap * 4);
+  a.in_count = in_count;
+  a.in_idx = in_idx;
+  a.in_val = in_val;
   a.timing = timing;
+  if (!tab->types || !tab->type_of || tab->n_types < 1) return hipErrorInvalidValue;
+  if (tab->n_types > kMaxLdsTypes) return hipErrorInvalidValue;
+  a.table_in_lds = 1;
 
   const size_t lds = (size_t)(tab->K > 0 ? tab->K : 1) * tpg * geo->range_n * sizeof(long long) +
-                     (size_t)tpg * a.words * sizeof(uint32_t);
+                     (size_t)tpg * a.words * sizeof(uint32_t) +
+                     (size_t)tab->n_types * (kTypeCols + tab->K + 2) * 4;
   int dev = 0, max_lds = 0;
   hipError_t qe = hipGetDevice(&dev);
   if (qe == hipSuccess)
     qe = hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   if (qe != hipSuccess) return qe;
-  if (lds + 64 > (size_t)max_lds) return hipErrorInvalidValue;
+  const size_t static_lds = kRunBlock * (8 + 4 + 4 + 4 + 1) + 17 * 4 + 64;
+  if (lds + static_lds > (size_t)max_lds) return hipErrorInvalidValue;
+  if (ff->n_src > 0 && io->x) {
+    const int64_t rows = io->B * io->T;
+    hipLaunchKernelGGL(compact_input_kernel, dim3((unsigned)rows), dim3(256), 0,
+                       (hipStream_t)stream, io->x, rows, io->n_in, in_count, in_idx, in_val);
+    hipError_t ce = hipGetLastError();
+    if (ce != hipSuccess) return ce;
+  }
   const int64_t per_wg = tpg * geo->range_n;
   const int block = per_wg >= kRunBlock ? kRunBlock : (int)(((per_wg + 63) / 64) * 64);
   const int64_t per_thread = (per_wg + block - 1) / block;

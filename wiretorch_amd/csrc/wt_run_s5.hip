@@ -1,0 +1,4 @@
+// The persistent forward kernel for S = 5 synapse types (see wt_run.h).
+#include "wt_run.h"
+
+template struct wt::RunLaunch<5>;

@@ -41,6 +41,7 @@ PHYSIOLOGY = ("theta", "U_reset", "E_L", "C_m", "beta", "E_syn", "decay", "jump"
 MAX_FRAC_BITS = 40
 BLOCK = 1024
 MAX_GROUPS = 8
+MAX_TYPES = 256
 #: When a list, every ``wt_cond_run`` launch appends a pair of events recorded on its
 #: stream just before and after it (``bench.py`` times the kernel with them).
 LAUNCH_EVENTS: list | None = None
@@ -216,7 +217,7 @@ def geometry(B: int, N: int, K: int, n_cu: int, max_lds: int) -> tuple[int, int,
     groups = max(1, min(MAX_GROUPS, B))
     tpg = -(-B // groups)
     limit = max(1, n_cu // groups)
-    budget = max_lds - 1024
+    budget = max_lds - 24 * 1024 - 256 * (8 + K) * 4  # event list, type table
 
     def fits(R):
         range_n = -(-(-(-N // R)) // 32) * 32
@@ -239,6 +240,24 @@ def _frac_bits(bound: float) -> int:
     if bound <= 0:
         return MAX_FRAC_BITS
     return max(0, min(MAX_FRAC_BITS, 61 - math.ceil(math.log2(bound)) - 1))
+
+
+def _type_table(tables: dict, scale: torch.Tensor, device):
+    """The per-neuron values the forward reads — theta, U_reset, E_L, C_m, beta, n_ref
+    and each pathway's kernel scale — as rows of distinct values and each neuron's row:
+    networks built from cell types have a handful, which the kernel keeps in LDS."""
+    N = tables["theta"].shape[0]
+    n_ref = (tables["n_ref"].float() if tables["n_ref"] is not None
+             else torch.zeros(N, device=device))
+    cols = [tables[n] for n in ("theta", "U_reset", "E_L", "C_m", "beta")] + [n_ref]
+    rows = torch.cat([torch.stack(cols, dim=1), _f32(scale, device).T], dim=1)
+    types, type_of = torch.unique(rows, dim=0, return_inverse=True)
+    if types.shape[0] > MAX_TYPES:
+        raise NotImplementedError(
+            f"{types.shape[0]} distinct per-neuron parameter rows (at most {MAX_TYPES}: "
+            "physiology and kernel scales are expected to follow cell types)"
+        )
+    return types.contiguous(), type_of.to(torch.int32).contiguous()
 
 
 def _f32(t: torch.Tensor, device) -> torch.Tensor:
@@ -280,7 +299,8 @@ class _Plan:
             t["n_ref"].data_ptr() if t["n_ref"] is not None else None,
             t["E_syn"].data_ptr(), t["g_clip"].data_ptr(), t["decay"].data_ptr(),
             t["jump"].data_ptr(), t["made"].data_ptr(), scale.data_ptr(),
-            t["dt"].data_ptr(), t["surr"].data_ptr(), self.N, self.S, self.K, self.K_rec,
+            t["dt"].data_ptr(), t["surr"].data_ptr(), t["types"].data_ptr(),
+            t["type_of"].data_ptr(), int(t["types"].shape[0]), self.N, self.S, self.K, self.K_rec,
         )  # fmt: skip
 
 
@@ -314,6 +334,7 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
     tables["surr"] = _f32(p.surr_scale, device)
     tables["n_ref"] = (None if p.n_ref is None
                        else p.n_ref.to(device=device, dtype=torch.int32).contiguous())
+    tables["types"], tables["type_of"] = _type_table(tables, drive.scale, device)
     return _Plan(
         B=B, T=T, N=N, S=S, K_rec=K_rec, K_ff=K_ff, n_in=n_in, tables=tables, rec=rec,
         ff=ff, geo=(groups, R, range_n), frac_bits=_frac_bits(bound),
@@ -328,8 +349,9 @@ def _launch(L: _Plan, x, scale, v, g, counter, spikes, prob, saved, tracked,
     groups, R, range_n = L.geo
     geo = _lib.Geometry(groups, R, range_n, L.frac_bits)
     lib = _lib.load()
-    scratch = torch.zeros(int(lib.wt_cond_run_scratch_bytes(geo, L.B, L.N)),
+    scratch = torch.empty(int(lib.wt_cond_run_scratch_bytes(geo, L.B, L.T)),
                           dtype=torch.uint8, device=L.device)
+    scratch[: int(lib.wt_cond_run_scratch_zeroed(geo))].zero_()
     v_saved, G_saved, held, A_saved = saved if saved is not None else (None,) * 4
     tv, tI, tg = ((tracked["v"], tracked["I"], tracked["g"]) if tracked is not None
                   else (None, None, None))
@@ -541,11 +563,16 @@ def simulate(
         raise NotImplementedError("float16 storage")
     device = x.device
     L = _plan(v, x, drive, p, probabilities, track, track_batch_idx)
-    v = v.detach().to(device=device, dtype=torch.float32).contiguous().clone()
-    g_state = g.detach().permute(0, 2, 3, 1).to(device=device, dtype=torch.float32).contiguous()
+    # The kernel updates the state in place: always work on copies, so the caller's
+    # tensors keep their values (a permuted view may already be contiguous storage).
+    v = v.detach().to(device=device, dtype=torch.float32).clone(
+        memory_format=torch.contiguous_format)
+    g_state = g.detach().to(device=device, dtype=torch.float32).permute(0, 2, 3, 1).clone(
+        memory_format=torch.contiguous_format)
     if refractory is None:
         refractory = torch.zeros(v.shape, dtype=torch.int32, device=device)
-    counter = refractory.to(device=device, dtype=torch.int32).contiguous().clone()
+    counter = refractory.to(device=device, dtype=torch.int32).clone(
+        memory_format=torch.contiguous_format)
 
     rec_w = ([drive.sparse_recurrent.weights] if drive.sparse_recurrent is not None
              else [W for _, W in drive.recurrent])
