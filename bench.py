@@ -92,7 +92,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--cpu-steps", type=int, default=int(os.environ.get("BENCH_CPU_STEPS", 100)))
+    ap.add_argument("--cpu-steps", type=int, default=int(os.environ.get("BENCH_CPU_STEPS", 400)))
     ap.add_argument("--T", type=int, default=2000)
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run one device-to-device copy of this many bytes (the "
@@ -108,7 +108,7 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py runs on one GPU only: this build has no multi-GPU path "
-              "(see DESIGN.md for how the hot path would shard)", file=sys.stderr)
+              "(the hot path runs on a single GPU)", file=sys.stderr)
         sys.exit(2)
     dev = torch.device("cuda:0")
     t_build = time.perf_counter()
