@@ -77,6 +77,9 @@ class _Side:
         if key not in self._split:
             c = self.conn
             split = torch.zeros((max(c.n_sources, 1), R + 1), dtype=torch.int64, device=c.device)
+            if c.n_edges == 0:  # every range of every source is empty: the zeros stand
+                self._split[key] = split
+                return split
             _lib.check(
                 _lib.load().wt_split_ranges(c.indptr.data_ptr(), c.targets.data_ptr(),
                                             c.n_sources, R, range_n, split.data_ptr(), stream),
@@ -89,6 +92,9 @@ class _Side:
         if self._edge_src is None:
             c = self.conn
             out = torch.empty(c.n_edges, dtype=torch.int64, device=c.device)
+            if c.n_edges == 0:
+                self._edge_src = out
+                return out
             _lib.check(
                 _lib.load().wt_edge_sources(c.indptr.data_ptr(), c.n_sources, out.data_ptr(), stream),
                 "wt_edge_sources",
