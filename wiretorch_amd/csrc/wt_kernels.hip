@@ -293,9 +293,14 @@ static int64_t run_tpg_max(const wt_geometry* geo, int64_t B) {
 // (fired bitmaps, the input lists) is written before it is read.
 static int64_t scratch_zeroed(const wt_geometry* geo) { return 256 + geo->groups * 128; }
 
+// Fired bitmaps: two buffers of [groups][tpg_max][R * words] words.
+static int64_t bitmap_words(const wt_geometry* geo, int64_t B) {
+  return geo->groups * run_tpg_max(geo, B) * geo->R * (geo->range_n / 32);
+}
+
 extern "C" int64_t wt_cond_run_scratch_bytes(const wt_geometry* geo, int64_t B, int64_t T) {
   int64_t bytes = scratch_zeroed(geo);
-  bytes += 2 * B * geo->R * (geo->range_n / 32) * 4;      // fired bitmaps
+  bytes += 2 * bitmap_words(geo, B) * 4;                  // fired bitmaps
   bytes = (bytes + 255) / 256 * 256;
   bytes += B * T * 4;                                     // input counts
   bytes += B * T * kInCap * 8;                            // input indices and values
@@ -337,7 +342,8 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
   a.err = reinterpret_cast<uint32_t*>(base);
   a.barrier = reinterpret_cast<uint32_t*>(base + 256);
   a.bitmap = reinterpret_cast<uint32_t*>(base + scratch_zeroed(geo));
-  int64_t off = scratch_zeroed(geo) + 2 * io->B * geo->R * a.words * 4;
+  a.tpg_max = tpg;
+  int64_t off = scratch_zeroed(geo) + 2 * bitmap_words(geo, io->B) * 4;
   off = (off + 255) / 256 * 256;
   int32_t* in_count = reinterpret_cast<int32_t*>(base + off);
   off += io->B * io->T * 4;
@@ -349,17 +355,19 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
   a.timing = timing;
   if (!tab->types || !tab->type_of || tab->n_types < 1) return hipErrorInvalidValue;
   if (tab->n_types > kMaxLdsTypes) return hipErrorInvalidValue;
-  a.table_in_lds = 1;
+  // descriptors pack the target within the range in 16 bits, the trial in 8
+  if (geo->range_n > 65535 || tpg > 255) return hipErrorInvalidValue;
 
-  const size_t lds = (size_t)(tab->K > 0 ? tab->K : 1) * tpg * geo->range_n * sizeof(long long) +
-                     (size_t)tpg * a.words * sizeof(uint32_t) +
-                     (size_t)tab->n_types * (kTypeCols + tab->K + 2) * 4;
+  const int64_t acc_len = (tab->K > 0 ? tab->K : 1) * tpg * geo->range_n;
+  const size_t lds = (size_t)run_types_offset(acc_len, tpg * a.words) +
+                     (size_t)tab->n_types * kRow * 4;
   int dev = 0, max_lds = 0;
   hipError_t qe = hipGetDevice(&dev);
   if (qe == hipSuccess)
     qe = hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   if (qe != hipSuccess) return qe;
-  const size_t static_lds = kRunBlock * (8 + 4 + 4 + 4 + 1) + 17 * 4 + 64;
+  const size_t static_lds = kRunBlock * (8 + 4 + 4 + 4 + 1) + sizeof(BlockScan::storage_type) +
+                            kPhases * 8 + 64;
   if (lds + static_lds > (size_t)max_lds) return hipErrorInvalidValue;
   if (ff->n_src > 0 && io->x) {
     const int64_t rows = io->B * io->T;
@@ -368,11 +376,9 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
     hipError_t ce = hipGetLastError();
     if (ce != hipSuccess) return ce;
   }
-  const int64_t per_wg = tpg * geo->range_n;
-  const int block = per_wg >= kRunBlock ? kRunBlock : (int)(((per_wg + 63) / 64) * 64);
-  const int64_t per_thread = (per_wg + block - 1) / block;
+  const int64_t per_thread = (tpg * geo->range_n + kRunBlock - 1) / kRunBlock;
   const bool coop = tab->K_rec > 0 && rec->n_src > 0 && geo->R > 1;
-  return dispatch_S<RunLaunch>(tab->S, a, lds, block, per_thread, (hipStream_t)stream, coop);
+  return dispatch_S<RunLaunch>(tab->S, a, lds, per_thread, (hipStream_t)stream, coop);
 }
 
 extern "C" int wt_cond_run(const wt_tables* tab, const wt_side* rec, const wt_side* ff,

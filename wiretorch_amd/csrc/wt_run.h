@@ -1,7 +1,21 @@
 // wt_run.h — the persistent forward kernel of wt_cond_run (see wt_kernels.hip) and its
 // launcher, instantiated per synapse count S in wt_run_s<S>.hip (compiled in parallel).
+//
+// Registers and LDS, per workgroup of 1024 threads:
+//   * each thread owns up to MAXI (trial, neuron) items; their v, conductances and
+//     refractory counters stay in VGPRs for the whole launch, with one packed
+//     descriptor each (target within the range, trial within the group, type row);
+//   * LDS holds the int64 activation accumulators [K][tpg][range_n], the workgroup's
+//     own fired bits of the next step, the parameter table (one 64-byte row per distinct
+//     neuron type) and the step's event list.
+// A step: wait for the group's bitmap of this step; preload it into registers; update
+// every owned neuron (inject the previous step's activations, spike, membrane,
+// refractory) and decide its next spike into the LDS bits; publish them to the group
+// and arrive at the group barrier; list this step's input and recurrent events; add
+// their synapses onto the workgroup's targets into the accumulators.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <rocprim/block/block_scan.hpp>
 #include <stdint.h>
 
 #include "../../include/wiretorch_amd.h"
@@ -20,19 +34,57 @@ struct RunArgs {
   // scratch
   uint32_t* err;        // [0]: error flags
   uint32_t* barrier;    // one counter per group, 128 bytes apart
-  uint32_t* bitmap;     // [2][B][R * words]: which neurons fired, per trial
+  uint32_t* bitmap;     // [2][groups][tpg_max][R * words]: which neurons fired
   const int32_t* in_count;  // [B*T]: nonzero inputs of each (trial, step), or > kInCap
   const int32_t* in_idx;    // [B*T][kInCap]
   const float* in_val;      // [B*T][kInCap]
   uint64_t* timing;     // [wgs][kPhases] wall-clock ticks per phase, or null
   int64_t words;        // bitmap words per workgroup range (range_n / 32)
-  int64_t table_in_lds; // the per-type table fits the LDS copy
+  int64_t tpg_max;      // trials of the largest group
 };
 
-constexpr int kPhases = 5;  // update, publish, feedforward events, barrier wait, recurrent push
+// update, publish + arrive, input events, barrier wait, recurrent events + push
+constexpr int kPhases = 5;
 constexpr int kInCap = 64;  // inputs listed per (trial, step); denser rows are scanned
 constexpr int kMaxLdsTypes = 256;
-constexpr int kTypeCols = 6;  // theta, U_reset, E_L, C_m, beta, n_ref; then scale[K]
+constexpr int kTypeCols = 6;  // global table: theta, U_reset, E_L, C_m, beta, n_ref; scale[K]
+// LDS table row (floats): theta, U_reset, E_L, C_m, n_ref, rate, g_L, -, scale[0..7]
+constexpr int kRow = 16;
+constexpr uint32_t kNoItem = 0xffffffffu;
+
+// Byte offset of the type table in the dynamic LDS: after the accumulators and the
+// workgroup's bits, rounded up to 16 bytes (float4 reads).
+__host__ __device__ inline int64_t run_types_offset(int64_t acc_len, int64_t bit_words) {
+  return (acc_len * 8 + bit_words * 4 + 15) / 16 * 16;
+}
+
+using BlockScan = rocprim::block_scan<int32_t, kRunBlock,
+                                      rocprim::block_scan_algorithm::using_warp_scan>;
+
+// The kernel's arguments, re-read from the kernarg segment (scalar loads) wherever a
+// phase needs them, instead of being held in scalar registers across the whole loop.
+typedef const __attribute__((address_space(4))) RunArgs* ArgPtr;
+__device__ inline ArgPtr kargs() {
+  ArgPtr p = (ArgPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(p));
+  return p;
+}
+
+// A value the compiler cannot see through: what is derived from an item's descriptor
+// is recomputed each step instead of hoisted out of the time loop (which would keep
+// every item's addresses live in registers for the whole launch).
+__device__ inline uint32_t opaque(uint32_t x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// A load through the global address space. Pointers held in structures reach the
+// kernel as generic pointers; generic (flat) loads also count against the LDS wait
+// counter, which serialises them with the LDS work around them.
+template <class T>
+__device__ inline T gload(const T* p) {
+  return *(const __attribute__((address_space(1))) T*)p;
+}
 
 __device__ inline void store_agent(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -93,11 +145,12 @@ __device__ inline void add_fixed(long long* cell, float x, float fscale) {
 }
 
 // Serial fallback for an event that did not fit the work list.
-__device__ inline void push_edges(long long* row, const wt_side& side, int64_t e0, int64_t e1,
-                                  int64_t lo, float value, float fscale) {
+__device__ inline void push_edges(long long* row, const int32_t* targets, const float* weights,
+                                  int64_t e0, int64_t e1, int64_t lo, float value,
+                                  float fscale) {
   for (int64_t e = e0; e < e1; ++e) {
-    const float w = side.weights[e];
-    add_fixed(row + (side.targets[e] - lo), value == 1.0f ? w : value * w, fscale);
+    const float w = gload(weights + e);
+    add_fixed(row + (gload(targets + e) - lo), value == 1.0f ? w : value * w, fscale);
   }
 }
 
@@ -109,17 +162,9 @@ __device__ inline void tick(uint64_t* acc_t, uint64_t& last, int phase) {
   }
 }
 
-// An item index the compiler cannot see through: recomputed each step instead of
-// hoisted out of the time loop (which would keep every item's derived indices live in
-// registers for the whole launch).
-__device__ inline uint32_t opaque(uint32_t x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
-
 // The workgroup's list of this step's events: a source whose synapses onto the
-// workgroup's targets are edges [e0, e0 + count) of `side` (0 recurrent, 1 input), to be
-// added times `value` to the accumulator row at `row`.
+// workgroup's targets are edges [e0, e0 + count) of side `side` (0 recurrent, 1 input),
+// to be added times `value` to the accumulator row at `row` (relative to the range).
 struct EventList {
   int64_t* e0;
   int32_t* count;  // becomes the exclusive prefix of the counts
@@ -127,92 +172,74 @@ struct EventList {
   float* value;
   uint8_t* side;
   int32_t* n;      // entries appended (may exceed the capacity: the rest ran serially)
-  int32_t* wave_sum;
-  int cap;
 };
 
-__device__ inline void append_event(const EventList& L, long long* acc, const wt_side& side,
-                                    int side_id, int64_t e0, int64_t e1, int64_t row,
-                                    int64_t lo, float value, float fscale) {
+__device__ inline void append_event(const EventList& L, long long* acc, const int32_t* targets,
+                                    const float* weights, int side_id, int64_t e0, int64_t e1,
+                                    int64_t row, int64_t lo, float value, float fscale) {
   if (e1 <= e0) return;
   const int pos = atomicAdd(L.n, 1);
-  if (pos < L.cap) {
+  if (pos < kRunBlock) {
     L.e0[pos] = e0;
     L.count[pos] = (int32_t)(e1 - e0);
     L.row[pos] = (int32_t)(row - lo);
     L.value[pos] = value;
     L.side[pos] = (uint8_t)side_id;
   } else {
-    push_edges(acc + row, side, e0, e1, lo, value, fscale);
+    push_edges(acc + row, targets, weights, e0, e1, lo, value, fscale);
   }
-}
-
-// Exclusive prefix of L.count[0 .. m) in place; returns the total. Two levels in LDS:
-// 64 threads sum contiguous chunks, one thread scans the 64 chunk sums, the 64 threads
-// rewrite their chunks.
-__device__ inline int32_t scan_counts(const EventList& L, int m) {
-  const int tid = threadIdx.x;
-  const int chunk = (m + 63) / 64;
-  if (tid < 64) {
-    int32_t sum = 0;
-    const int end = (tid + 1) * chunk < m ? (tid + 1) * chunk : m;
-    for (int i = tid * chunk; i < end; ++i) sum += L.count[i];
-    L.wave_sum[tid] = sum;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int32_t run = 0;
-    for (int w = 0; w < 64; ++w) {
-      const int32_t v = L.wave_sum[w];
-      L.wave_sum[w] = run;
-      run += v;
-    }
-    L.wave_sum[64] = run;
-  }
-  __syncthreads();
-  if (tid < 64) {
-    int32_t run = L.wave_sum[tid];
-    const int end = (tid + 1) * chunk < m ? (tid + 1) * chunk : m;
-    for (int i = tid * chunk; i < end; ++i) {
-      const int32_t c = L.count[i];
-      L.count[i] = run;
-      run += c;
-    }
-  }
-  __syncthreads();
-  return L.wave_sum[64];
 }
 
 // Every listed synapse, spread evenly over the workgroup (four per thread per round,
-// loads issued before the atomics), added to the accumulator.
+// loads issued before the atomics), added to the accumulator. L.count holds the
+// exclusive prefix of the entries' edge counts.
 __device__ inline void run_events(const EventList& L, int m, int32_t total, long long* acc,
-                                  const wt_side& rec, const wt_side& ff, int64_t lo,
-                                  float fscale) {
+                                  int64_t lo, float fscale) {
+  ArgPtr P = kargs();
+  const int32_t* const rec_tg = P->rec.targets;
+  const int32_t* const ff_tg = P->ff.targets;
+  const float* const rec_w = P->rec.weights;
+  const float* const ff_w = P->ff.weights;
   const int stride = blockDim.x;
   for (int32_t base = threadIdx.x; base < total; base += 4 * stride) {
-    int32_t tgt[4], rows[4];
-    float x[4];
+    // three passes, so that all eight loads are in flight together: locate each edge's
+    // entry (LDS), load the edges (HBM), add them (LDS atomics)
+    int64_t e[4];
+    int32_t rows[4];
+    float val[4];
+    bool input[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int32_t f = base + u * stride;
+      e[u] = 0;
+      rows[u] = 0;
+      val[u] = 0.0f;
+      input[u] = false;
       if (f < total) {
         int a = 0, z = m;  // entry a with prefix[a] <= f < prefix[a + 1]
         while (z - a > 1) {
           const int mid = (a + z) >> 1;
           if (L.count[mid] <= f) a = mid; else z = mid;
         }
-        const wt_side& side = L.side[a] ? ff : rec;
-        const int64_t e = L.e0[a] + (f - L.count[a]);
-        tgt[u] = side.targets[e];
-        const float w = side.weights[e];
-        const float v = L.value[a];
-        x[u] = v == 1.0f ? w : v * w;
+        e[u] = L.e0[a] + (f - L.count[a]);
+        input[u] = L.side[a] != 0;
+        val[u] = L.value[a];
         rows[u] = L.row[a];  // may be negative: rows are relative to the range start
+      }
+    }
+    int32_t tgt[4];
+    float w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (base + u * stride < total) {
+        tgt[u] = gload((input[u] ? ff_tg : rec_tg) + e[u]);
+        w[u] = gload((input[u] ? ff_w : rec_w) + e[u]);
       }
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u)
-      if (base + u * stride < total) add_fixed(acc + rows[u] + tgt[u], x[u], fscale);
+      if (base + u * stride < total)
+        add_fixed(acc + rows[u] + tgt[u], val[u] == 1.0f ? w[u] : val[u] * w[u], fscale);
   }
 }
 
@@ -221,7 +248,7 @@ __device__ inline void run_events(const EventList& L, int m, int32_t total, long
 // the whole launch.
 template <int S, int MAXI, bool EXTRA>
 __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
-  extern __shared__ long long acc[];  // [K][tpg][range_n], the fired bitmap, the type table
+  extern __shared__ __align__(16) long long acc[];  // [K][tpg][range_n], own bits, types
   __shared__ uint32_t s_flag;
   __shared__ uint64_t s_time[kPhases];
   __shared__ int64_t s_e0[kRunBlock];
@@ -230,347 +257,385 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   __shared__ float s_value[kRunBlock];
   __shared__ uint8_t s_side[kRunBlock];
   __shared__ int32_t s_nev;
-  __shared__ int32_t s_wave[65];
+  __shared__ typename BlockScan::storage_type s_scan;
 
-  const wt_tables& tab = A.tab;
-  const wt_run_io& io = A.io;
   const int64_t groups = A.geo.groups, R = A.geo.R, range_n = A.geo.range_n;
-  const int64_t N = tab.N, K = tab.K, K_rec = tab.K_rec, B = io.B, T = io.T;
-  // Optional outputs exist only in the EXTRA variant (the lean one writes spikes only).
-  float* const o_prob = EXTRA ? io.prob : nullptr;
-  float* const o_v_saved = EXTRA ? io.v_saved : nullptr;
-  float* const o_G_saved = EXTRA ? io.G_saved : nullptr;
-  int8_t* const o_held = EXTRA ? io.held : nullptr;
-  float* const o_A_saved = EXTRA ? io.A_saved : nullptr;
-  float* const o_track_v = EXTRA ? io.track_v : nullptr;
-  float* const o_track_I = EXTRA ? io.track_I : nullptr;
-  float* const o_track_g = EXTRA ? io.track_g : nullptr;
+  const int64_t N = A.tab.N, K = A.tab.K, B = A.io.B, T = A.io.T;
   const int64_t wg = blockIdx.x;
   const int64_t g = wg % groups, r = wg / groups;
   const int64_t tpg = g < B ? (B - g + groups - 1) / groups : 0;
   if (tpg == 0) return;  // no trial in this group: it takes part in nothing
   const int64_t lo = r * range_n;
   const int64_t nr = lo < N ? (N - lo < range_n ? N - lo : range_n) : 0;
-  const int64_t items = tpg * nr;
-  const int64_t acc_len = K * tpg * range_n;
+  const uint32_t items = (uint32_t)(tpg * nr);
   const int64_t words = A.words;
-  const uint32_t nr32 = (uint32_t)(nr > 0 ? nr : 1), items32 = (uint32_t)items;
+  const int64_t total_words = R * words;        // one trial's bitmap
+  const int64_t group_words = tpg * total_words;
+  const uint32_t acc_stride = (uint32_t)(tpg * range_n);  // one pathway's accumulators
+  const int64_t acc_len = (K > 0 ? K : 1) * (int64_t)acc_stride;
   uint32_t* s_bits = reinterpret_cast<uint32_t*>(acc + acc_len);  // [tpg][words]
-  const int64_t cols = kTypeCols + K;      // columns of a type row (global table)
-  const int64_t lcols = cols + 2;          // LDS rows add rate and g_L
-  float* s_types = reinterpret_cast<float*>(s_bits + tpg * words);
-  const bool refractory = tab.n_ref != nullptr;
-  const bool recurrent = K_rec > 0 && A.rec.n_src > 0;
-  const float dt = *tab.dt;
+  float* s_types = reinterpret_cast<float*>(                       // 16-byte aligned rows
+      reinterpret_cast<char*>(acc) + run_types_offset(acc_len, tpg * words));
+  const bool refractory = A.tab.n_ref != nullptr;
+  const bool recurrent = A.tab.K_rec > 0 && A.rec.n_src > 0;
+  // Every read of a published bitmap happens in the preload: the workgroup may then
+  // arrive at the barrier as soon as its own bits are out.
+  const bool early_arrive = group_words <= (int64_t)MAXI * blockDim.x;
+  const float dt = *A.tab.dt;
   const float fscale = ldexpf(1.0f, (int)A.geo.frac_bits);
   const float inv_fscale = ldexpf(1.0f, -(int)A.geo.frac_bits);
-  const EventList EL{s_e0, s_count, s_row, s_value, s_side, &s_nev, s_wave, (int)blockDim.x};
+  const EventList EL{s_e0, s_count, s_row, s_value, s_side, &s_nev};
   Synapses<S> syn;
-  load_synapses<S>(tab, syn);
+  load_synapses<S>(A.tab, syn);
+  uint64_t made = 0;  // bit k * S + s: pathway k drives synapse type s
+  for (int64_t k = 0; k < K; ++k)
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+      if (A.tab.made[k * S + s] != 0.0f) made |= 1ull << (k * S + s);
   uint64_t* my_time = A.timing ? s_time : nullptr;
   if (threadIdx.x < kPhases) s_time[threadIdx.x] = 0;
   uint64_t last = wall_clock64();
 
   for (int64_t i = threadIdx.x; i < acc_len; i += blockDim.x) acc[i] = 0;
   {
-    for (int64_t ty = threadIdx.x; ty < tab.n_types; ty += blockDim.x) {
-      const float* src = tab.types + ty * cols;
-      float* dst = s_types + ty * lcols;
-      for (int64_t c = 0; c < cols; ++c) dst[c] = src[c];
+    const int64_t cols = kTypeCols + K;
+    for (int64_t ty = threadIdx.x; ty < A.tab.n_types; ty += blockDim.x) {
+      const float* src = A.tab.types + ty * cols;
+      float* dst = s_types + ty * kRow;
       const Leak lk = leak(src[3], src[4], dt);
-      dst[cols] = lk.rate;
-      dst[cols + 1] = lk.g_L;
+      dst[0] = src[0];
+      dst[1] = src[1];
+      dst[2] = src[2];
+      dst[3] = src[3];
+      dst[4] = src[5];
+      dst[5] = lk.rate;
+      dst[6] = lk.g_L;
+      dst[7] = 0.0f;
+      for (int64_t k = 0; k < 8; ++k) dst[8 + k] = k < K ? src[kTypeCols + k] : 0.0f;
     }
   }
 
-  // Registers: the owned items' state.
+  // Registers: the owned items' state and descriptors (target within the range in bits
+  // 0-15, trial within the group in 16-23, row of the type table in 24-31).
   float v[MAXI], gr[MAXI][S], gd[MAXI][S];
   int32_t counter[MAXI];
-  uint32_t type_pack[(MAXI + 3) / 4];  // each item's row of the type table, one byte each
+  uint32_t desc[MAXI];
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) {
     const uint32_t it = threadIdx.x + (uint32_t)i * blockDim.x;
-    if (i % 4 == 0) type_pack[i / 4] = 0;
-    if (it < items32) {
-      const uint32_t q = it / nr32;
-      const int64_t n = lo + (it - q * nr32), b = g + (int64_t)q * groups;
-      v[i] = io.v[b * N + n];
-      counter[i] = refractory ? io.counter[b * N + n] : 0;
-      type_pack[i / 4] |= ((uint32_t)tab.type_of[n] & 0xffu) << (8 * (i % 4));
+    desc[i] = kNoItem;
+    v[i] = 0.0f;
+    counter[i] = 0;
+#pragma unroll
+    for (int s = 0; s < S; ++s) gr[i][s] = gd[i][s] = 0.0f;
+    if (it < items) {
+      const uint32_t q = it / (uint32_t)nr, ln = it - q * (uint32_t)nr;
+      const int64_t n = lo + ln, b = g + (int64_t)q * groups;
+      desc[i] = ln | (q << 16) | (((uint32_t)A.tab.type_of[n] & 0xffu) << 24);
+      v[i] = A.io.v[b * N + n];
+      counter[i] = refractory ? A.io.counter[b * N + n] : 0;
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        gr[i][s] = io.g[(b * 2 * S + s) * N + n];
-        gd[i][s] = io.g[(b * 2 * S + S + s) * N + n];
+        gr[i][s] = A.io.g[(b * 2 * S + s) * N + n];
+        gd[i][s] = A.io.g[(b * 2 * S + S + s) * N + n];
       }
     }
   }
-  uint32_t* my_barrier = A.barrier + g * 32;
-  uint32_t phase = 0;  // barriers passed
+  uint32_t* const my_barrier = A.barrier + g * 32;
+  uint32_t* const group_bits = A.bitmap + g * A.tpg_max * total_words;  // buffer 0
+  const int64_t buffer_words = groups * A.tpg_max * total_words;
+  uint32_t phase = 0;  // barrier arrivals of this workgroup
   // Per item, as bit masks: the spike s_t of the step about to be integrated, and
   // whether the neuron is held (refractory) during it.
   uint32_t masks = 0;  // bit i: item i spikes at the current step; bit 8 + i: it is held
-  const int64_t total_words = R * words;  // one trial's bitmap
 
   // Spikes of step 0, from the entering state.
   for (int64_t w = threadIdx.x; w < tpg * words; w += blockDim.x) s_bits[w] = 0;
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) {
-    const uint32_t it = opaque(threadIdx.x + (uint32_t)i * blockDim.x);
-    if (it >= items32) continue;
-    const uint32_t q = it / nr32, ln = it - q * nr32;
-    const int64_t n = lo + ln, b = g + (int64_t)q * groups;
-    const int64_t ty0 = (type_pack[i / 4] >> (8 * (i % 4))) & 0xffu;
-    const float theta = s_types[ty0 * lcols];
+    const uint32_t d = desc[i];
+    if (d == kNoItem) continue;
+    const uint32_t ln = d & 0xffffu, q = (d >> 16) & 0xffu;
+    const float* row = s_types + (d >> 24) * kRow;
+    const float theta = row[0];
     float r_hold, held;
-    const float s0 = spike_step(v[i], theta, counter[i], (int32_t)s_types[ty0 * lcols + 5],
-                                refractory, r_hold, held);
+    const float s0 = spike_step(v[i], theta, counter[i], (int32_t)row[4], refractory,
+                                r_hold, held);
     if (s0 != 0.0f) {
       masks |= 1u << i;
       if (recurrent) atomicOr(&s_bits[q * words + (ln >> 5)], 1u << (ln & 31));
     }
     if (held != 0.0f) masks |= 256u << i;
-    if (o_prob) {
-      const float pr = 1.0f / (1.0f + expf(-(*tab.surr * (v[i] - theta))));
-      o_prob[b * T * N + n] = refractory ? pr * (1.0f - held) : pr;
+    if (EXTRA && A.io.prob) {
+      const int64_t n = lo + ln, b = g + (int64_t)q * groups;
+      const float pr = 1.0f / (1.0f + expf(-(*A.tab.surr * (v[i] - theta))));
+      A.io.prob[b * T * N + n] = refractory ? pr * (1.0f - held) : pr;
     }
   }
   if (recurrent) {
     __syncthreads();
     for (int64_t w = threadIdx.x; w < tpg * words; w += blockDim.x) {
-      const int64_t q = w / words, b = g + q * groups;
-      store_agent(A.bitmap + b * total_words + r * words + (w - q * words), s_bits[w]);
+      const int64_t q = w / words;
+      store_agent(group_bits + q * total_words + r * words + (w - q * words), s_bits[w]);
     }
     barrier_arrive(my_barrier);
-    if (!barrier_wait(my_barrier, (uint32_t)(++phase * R), A.err, &s_flag)) return;
+    ++phase;
   }
 
-  constexpr int kPre = MAXI;  // bitmap words preloaded per thread (one per item at R = 32)
   for (int64_t t = 0; t < T; ++t) {
-    const int64_t cur = t & 1, nxt = (t + 1) & 1;
     const bool more = t + 1 < T;
-    // ---- preload this step's fired bitmap (published one phase ago) ----
-    uint32_t pre[kPre];
-    const uint32_t* in_bits = A.bitmap + cur * B * total_words;
+    const uint32_t* in_bits = group_bits + (t & 1) * buffer_words;
+    // ---- the group's fired bits of step t: complete once every workgroup arrived ----
+    if (recurrent) {
+      if (!barrier_wait(my_barrier, phase * (uint32_t)R, A.err, &s_flag)) return;
+    }
+    tick(my_time, last, 3);
+    uint32_t pre[MAXI];
 #pragma unroll
-    for (int u = 0; u < kPre; ++u) {
+    for (int u = 0; u < MAXI; ++u) {
       const int64_t w = threadIdx.x + (int64_t)u * blockDim.x;
-      pre[u] = (recurrent && w < tpg * total_words)
-                   ? load_agent(in_bits + (g + (w / total_words) * groups) * total_words + w % total_words)
-                   : 0u;
+      pre[u] = (recurrent && w < group_words) ? load_agent(in_bits + w) : 0u;
     }
     for (int64_t w = threadIdx.x; w < tpg * words; w += blockDim.x) s_bits[w] = 0;
     if (threadIdx.x == 0) s_nev = 0;
     __syncthreads();
 
     // ---------------- (A) integrate step t for the owned neurons ----------------
-    uint32_t masks_next = 0;
+    {
+      float* const spikes = A.io.spikes;
+      // element (b, t, n) of a (B, T, N) array: step_base + q * trial_stride + ln
+      const int64_t step_base = (g * T + t) * N + lo;
+      const uint64_t trial_stride = (uint64_t)(groups * T * N);
+      uint32_t masks_next = 0;
 #pragma unroll
-    for (int i = 0; i < MAXI; ++i) {
-      const uint32_t it = opaque(threadIdx.x + (uint32_t)i * blockDim.x);
-      if (it >= items32) continue;
-      const uint32_t q = it / nr32, ln = it - q * nr32;
-      const int64_t n = lo + ln;
-      const int64_t b = g + (int64_t)q * groups;
-      // opaque: the row's values are re-read from LDS each step, not held in registers
-      const int64_t ty = opaque((type_pack[i / 4] >> (8 * (i % 4))) & 0xffu);
-      auto P = [&](int64_t c) -> float { return s_types[ty * lcols + c]; };
-      if (t > 0) {
-        // g <- g * decay, then each pathway's activation times its kernel, in order
-        // (dynamics.py:206-208; kernel = jump * scale * made, dynamics.py:95-100).
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-          gr[i][s] = gr[i][s] * syn.decay_r[s];
-          gd[i][s] = gd[i][s] * syn.decay_d[s];
-        }
-        for (int64_t k = 0; k < K; ++k) {
-          long long* cell = acc + (k * tpg + (int64_t)q) * range_n + ln;
-          const float a = from_fixed(*cell, inv_fscale);
-          *cell = 0;
-          if (o_A_saved) o_A_saved[((k * B + b) * T + (t - 1)) * N + n] = a;
-          const float sc = P(kTypeCols + k);
+      for (int i = 0; i < MAXI; ++i) {
+        const uint32_t d = opaque(desc[i]);
+        if (d == kNoItem) continue;
+        const uint32_t ln = d & 0xffffu, q = (d >> 16) & 0xffu;
+        const float* row = s_types + (d >> 24) * kRow;
+        const int64_t out = step_base + (int64_t)((uint64_t)q * trial_stride) + ln;
+        const int64_t b = EXTRA ? g + (int64_t)q * groups : 0;
+        const int64_t n = lo + ln;
+        if (t > 0) {
+          // g <- g * decay, then each pathway's activation times its kernel, in order
+          // (dynamics.py:206-208; kernel = jump * scale * made, dynamics.py:95-100).
 #pragma unroll
           for (int s = 0; s < S; ++s) {
-            const float mk = tab.made[k * S + s];
-            if (mk != 0.0f) {
-              gr[i][s] = gr[i][s] + a * (syn.jump_r[s] * sc * mk);
-              gd[i][s] = gd[i][s] + a * (syn.jump_d[s] * sc * mk);
+            gr[i][s] = gr[i][s] * syn.decay_r[s];
+            gd[i][s] = gd[i][s] * syn.decay_d[s];
+          }
+          long long* cell = acc + __umul24(q, (uint32_t)range_n) + ln;
+          for (int64_t k = 0; k < K; ++k, cell += acc_stride) {
+            const float a = from_fixed(*cell, inv_fscale);
+            *cell = 0;
+            if (EXTRA && A.io.A_saved) A.io.A_saved[((k * B + b) * T + (t - 1)) * N + n] = a;
+            const float sc = row[8 + k];
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+              if ((made >> (k * S + s)) & 1u) {
+                gr[i][s] = gr[i][s] + a * (syn.jump_r[s] * sc);
+                gd[i][s] = gd[i][s] + a * (syn.jump_d[s] * sc);
+              }
+            }
+          }
+          if (EXTRA && A.io.track_g && (A.io.track_b < 0 || A.io.track_b == b)) {
+            const int64_t bt = A.io.track_b < 0 ? b : 0;
+            float* o = A.io.track_g + ((bt * T + (t - 1)) * N + n) * 2 * S;
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+              o[s] = gr[i][s];
+              o[S + s] = gd[i][s];
             }
           }
         }
-        if (o_track_g && (io.track_b < 0 || io.track_b == b)) {
-          const int64_t bt = io.track_b < 0 ? b : 0;
-          float* out = o_track_g + ((bt * T + (t - 1)) * N + n) * 2 * S;
+        const float4 p0 = *reinterpret_cast<const float4*>(row);      // theta U_reset E_L C_m
+        const float4 p1 = *reinterpret_cast<const float4*>(row + 4);  // n_ref rate g_L -
+        const float s_t = (float)((masks >> i) & 1u);
+        const float held_t = (float)((masks >> (8 + i)) & 1u);
+        const float r_hold = refractory ? fmaxf(s_t, held_t) : s_t;
+        spikes[out] = s_t;
+        float G[S], I[S], I_leak;
+        const float v_next = membrane<S>(v[i], r_hold, gr[i], gd[i], syn, p0.z, p0.w, p0.y,
+                                         Leak{p1.y, p1.z}, dt, G, I, I_leak);
+        if (EXTRA && A.io.v_saved) {
+          A.io.v_saved[out] = v[i];
 #pragma unroll
-          for (int s = 0; s < S; ++s) {
-            out[s] = gr[i][s];
-            out[S + s] = gd[i][s];
+          for (int s = 0; s < S; ++s) A.io.G_saved[out * S + s] = G[s];
+          if (refractory && A.io.held) A.io.held[out] = (int8_t)(held_t != 0.0f);
+        }
+        if (EXTRA && A.io.track_v && (A.io.track_b < 0 || A.io.track_b == b)) {
+          const int64_t bt = A.io.track_b < 0 ? b : 0;
+          const int64_t trow = (bt * T + t) * N + n;
+          A.io.track_v[trow] = v_next;
+#pragma unroll
+          for (int s = 0; s < S; ++s) A.io.track_I[trow * (S + 1) + s] = I[s];
+          A.io.track_I[trow * (S + 1) + S] = I_leak;
+        }
+        v[i] = v_next;
+        if (more) {  // the spike of step t+1 depends on v_{t+1} only: decide it now
+          float r_next, held;
+          const float s_next = spike_step(v_next, p0.x, counter[i], (int32_t)p1.x, refractory,
+                                          r_next, held);
+          if (s_next != 0.0f) {
+            masks_next |= 1u << i;
+            if (recurrent) atomicOr(&s_bits[q * words + (ln >> 5)], 1u << (ln & 31));
+          }
+          if (held != 0.0f) masks_next |= 256u << i;
+          if (EXTRA && A.io.prob) {
+            const float pr = 1.0f / (1.0f + expf(-(*A.tab.surr * (v_next - p0.x))));
+            A.io.prob[out + N] = refractory ? pr * (1.0f - held) : pr;
           }
         }
+        // items one after another: interleaving them only raises register pressure (the
+        // workgroup's 16 waves hide the latency)
+        __builtin_amdgcn_sched_barrier(0);
       }
-      const float s_t = (float)((masks >> i) & 1u);
-      const float held_t = (float)((masks >> (8 + i)) & 1u);
-      const float r_hold = refractory ? fmaxf(s_t, held_t) : s_t;
-      const int64_t out = (b * T + t) * N + n;
-      io.spikes[out] = s_t;
-      float G[S], I[S], I_leak;
-      const float v_next = membrane<S>(v[i], r_hold, gr[i], gd[i], syn, P(2), P(3), P(1),
-                                       Leak{P(cols), P(cols + 1)}, dt, G, I, I_leak);
-      if (o_v_saved) {
-        o_v_saved[out] = v[i];
-#pragma unroll
-        for (int s = 0; s < S; ++s) o_G_saved[out * S + s] = G[s];
-        if (refractory && o_held) o_held[out] = (int8_t)(held_t != 0.0f);
-      }
-      if (o_track_v && (io.track_b < 0 || io.track_b == b)) {
-        const int64_t bt = io.track_b < 0 ? b : 0;
-        const int64_t row = (bt * T + t) * N + n;
-        o_track_v[row] = v_next;
-#pragma unroll
-        for (int s = 0; s < S; ++s) o_track_I[row * (S + 1) + s] = I[s];
-        o_track_I[row * (S + 1) + S] = I_leak;
-      }
-      v[i] = v_next;
-      if (more) {  // the spike of step t+1 depends on v_{t+1} only: decide it now
-        const float theta = P(0);
-        float r_next, held;
-        const float s_next = spike_step(v_next, theta, counter[i], (int32_t)P(5), refractory,
-                                        r_next, held);
-        if (s_next != 0.0f) {
-          masks_next |= 1u << i;
-          if (recurrent) atomicOr(&s_bits[q * words + (ln >> 5)], 1u << (ln & 31));
-        }
-        if (held != 0.0f) masks_next |= 256u << i;
-        if (o_prob) {
-          const float pr = 1.0f / (1.0f + expf(-(*tab.surr * (v_next - theta))));
-          o_prob[out + N] = refractory ? pr * (1.0f - held) : pr;
-        }
-      }
-      // items one after another: interleaving them only raises register pressure (the
-      // workgroup's 16 waves hide the latency)
-      __builtin_amdgcn_sched_barrier(0);
+      masks = masks_next;
     }
-    masks = masks_next;
     tick(my_time, last, 0);
-    __syncthreads();  // the accumulator is read and cleared: events may be added now
+    __syncthreads();  // the accumulator is read and cleared; the next bits are complete
 
-    // ---------------- publish step t+1's spikes (completion overlaps the push) -----
-    if (recurrent && more) {
-      uint32_t* out_bits = A.bitmap + nxt * B * total_words;
+    // ---------------- publish step t+1's spikes ----------------
+    const bool publish = recurrent && more;
+    if (publish) {
+      uint32_t* out_bits = group_bits + ((t + 1) & 1) * buffer_words;
       for (int64_t w = threadIdx.x; w < tpg * words; w += blockDim.x) {
-        const int64_t q = w / words, b = g + q * groups;
-        store_agent(out_bits + b * total_words + r * words + (w - q * words), s_bits[w]);
+        const int64_t q = w / words;
+        store_agent(out_bits + q * total_words + r * words + (w - q * words), s_bits[w]);
       }
     }
-    tick(my_time, last, 1);
 
-    // ---------------- events of step t: inputs, then the preloaded bitmap ----------
-    if (A.ff.n_src > 0) {
-      const int64_t n_in = io.n_in;
-      for (int64_t q = 0; q < tpg; ++q) {
-        const int64_t b = g + q * groups, bt = b * T + t;
-        const int32_t c = A.in_count[bt];
-        const int64_t row_base = (K_rec * tpg + q) * range_n;
-        if (c <= kInCap) {
-          for (int32_t e = threadIdx.x; e < c; e += blockDim.x) {
-            const int32_t j = A.in_idx[bt * kInCap + e];
-            const int32_t k = A.ff.pathway[j];
-            if (k < 0) continue;
-            const int64_t* sp = A.ff.split + (int64_t)j * (R + 1) + r;
-            append_event(EL, acc, A.ff, 1, sp[0], sp[1], row_base + k * tpg * range_n, lo,
-                         A.in_val[bt * kInCap + e], fscale);
-          }
-        } else {
-          const float* xrow = io.x + bt * n_in;
-          for (int64_t j = threadIdx.x; j < n_in; j += blockDim.x) {
-            const float xv = xrow[j];
-            if (xv == 0.0f) continue;
-            const int32_t k = A.ff.pathway[j];
-            if (k < 0) continue;
-            const int64_t* sp = A.ff.split + j * (R + 1) + r;
-            append_event(EL, acc, A.ff, 1, sp[0], sp[1], row_base + k * tpg * range_n, lo,
-                         xv, fscale);
+    // ---------------- events of step t: inputs ----------------
+    {
+      ArgPtr P = kargs();
+      const int64_t n_ff = P->ff.n_src;
+      if (n_ff > 0) {
+        const int64_t* ff_split = P->ff.split;
+        const int32_t* ff_path = P->ff.pathway;
+        const int32_t* ff_tg = P->ff.targets;
+        const float* ff_w = P->ff.weights;
+        const int32_t* in_count = P->in_count;
+        const int64_t n_in = P->io.n_in, K_rec = P->tab.K_rec;
+        for (int64_t q = 0; q < tpg; ++q) {
+          const int64_t b = g + q * groups, bt = b * T + t;
+          const int32_t c = gload(in_count + bt);
+          const int64_t row_base = (K_rec * tpg + q) * range_n;
+          if (c <= kInCap) {
+            for (int32_t e = threadIdx.x; e < c; e += blockDim.x) {
+              const int32_t j = gload(P->in_idx + bt * kInCap + e);
+              const int32_t k = gload(ff_path + j);
+              if (k < 0) continue;
+              const int64_t* sp = ff_split + (int64_t)j * (R + 1) + r;
+              append_event(EL, acc, ff_tg, ff_w, 1, gload(sp), gload(sp + 1),
+                           row_base + k * acc_stride, lo, gload(P->in_val + bt * kInCap + e),
+                           fscale);
+            }
+          } else {
+            const float* xrow = P->io.x + bt * n_in;
+            for (int64_t j = threadIdx.x; j < n_in; j += blockDim.x) {
+              const float xv = gload(xrow + j);
+              if (xv == 0.0f) continue;
+              const int32_t k = gload(ff_path + j);
+              if (k < 0) continue;
+              const int64_t* sp = ff_split + j * (R + 1) + r;
+              append_event(EL, acc, ff_tg, ff_w, 1, gload(sp), gload(sp + 1),
+                           row_base + k * acc_stride, lo, xv, fscale);
+            }
           }
         }
       }
     }
     tick(my_time, last, 2);
+    if (publish && early_arrive) {
+      barrier_arrive(my_barrier);
+      ++phase;
+    }
+    tick(my_time, last, 1);
+
+    // ---------------- events of step t: the fired bits ----------------
     if (recurrent) {
-      const int64_t n_words = tpg * total_words;
-      for (int64_t w = threadIdx.x, u = 0; w < n_words; w += blockDim.x, ++u) {
+      ArgPtr P = kargs();
+      const int64_t* rec_split = P->rec.split;
+      const int32_t* rec_path = P->rec.pathway;
+      const int32_t* rec_tg = P->rec.targets;
+      const float* rec_w = P->rec.weights;
+      for (int64_t w = threadIdx.x, u = 0; w < group_words; w += blockDim.x, ++u) {
         uint32_t bits = 0;
 #pragma unroll
-        for (int v_ = 0; v_ < kPre; ++v_)
+        for (int v_ = 0; v_ < MAXI; ++v_)
           if (u == v_) bits = pre[v_];
-        if (u >= kPre)
-          bits = load_agent(in_bits + (g + (w / total_words) * groups) * total_words + w % total_words);
-        const int64_t q = w / total_words, wl = w % total_words;
+        if (u >= MAXI) bits = load_agent(in_bits + w);
+        if (!bits) continue;
+        const int64_t q = w / total_words, wl = w - q * total_words;
+        const int64_t j0 = (wl / words) * range_n + (wl % words) * 32;
         while (bits) {
           const int bit = __builtin_ctz(bits);
           bits &= bits - 1;
-          const int64_t j = (wl / words) * range_n + (wl % words) * 32 + bit;
-          const int64_t* sp = A.rec.split + j * (R + 1) + r;
-          const int64_t e0 = sp[0], e1 = sp[1];
-          const int32_t k = A.rec.pathway[j];
+          const int64_t j = j0 + bit;
+          const int64_t* sp = rec_split + j * (R + 1) + r;
+          const int64_t e0 = gload(sp), e1 = gload(sp + 1);
+          const int32_t k = gload(rec_path + j);
           if (k < 0) continue;
-          append_event(EL, acc, A.rec, 0, e0, e1, (k * tpg + q) * range_n, lo, 1.0f, fscale);
+          append_event(EL, acc, rec_tg, rec_w, 0, e0, e1, k * acc_stride + q * range_n, lo,
+                       1.0f, fscale);
         }
       }
     }
-    __syncthreads();
-    {
-      const int m = s_nev < EL.cap ? s_nev : EL.cap;
-      if (m > 0) {
-        const int32_t total = scan_counts(EL, m);
-        run_events(EL, m, total, acc, A.rec, A.ff, lo, fscale);
-      }
-    }
-    tick(my_time, last, 4);
-
-    // ---------------- barrier: step t+1's bitmap is complete ----------------
-    if (recurrent && more) {
+    if (publish && !early_arrive) {
       barrier_arrive(my_barrier);
-      if (!barrier_wait(my_barrier, (uint32_t)(++phase * R), A.err, &s_flag)) return;
+      ++phase;
     } else {
       __syncthreads();
     }
-    tick(my_time, last, 3);
+    {
+      const int m = s_nev < kRunBlock ? s_nev : kRunBlock;
+      if (m > 0) {  // m is uniform: every thread takes part in the scan
+        const int tid = threadIdx.x;
+        int32_t c = tid < m ? s_count[tid] : 0, total;
+        BlockScan().exclusive_scan(c, c, 0, total, s_scan);
+        if (tid < m) s_count[tid] = c;
+        __syncthreads();
+        run_events(EL, m, total, acc, lo, fscale);
+      }
+    }
+    __syncthreads();  // the accumulator is complete for the next update
+    tick(my_time, last, 4);
   }
 
   // The activations of the last step enter the conductances that leave the chunk.
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) {
-    const uint32_t it = opaque(threadIdx.x + (uint32_t)i * blockDim.x);
-    if (it >= items32 || T == 0) continue;
-    const uint32_t q = it / nr32, ln = it - q * nr32;
+    const uint32_t d = desc[i];
+    if (d == kNoItem || T == 0) continue;
+    const uint32_t ln = d & 0xffffu, q = (d >> 16) & 0xffu;
+    const float* row = s_types + (d >> 24) * kRow;
     const int64_t n = lo + ln, b = g + (int64_t)q * groups;
-    const int64_t ty = (type_pack[i / 4] >> (8 * (i % 4))) & 0xffu;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       gr[i][s] = gr[i][s] * syn.decay_r[s];
       gd[i][s] = gd[i][s] * syn.decay_d[s];
     }
-    for (int64_t k = 0; k < K; ++k) {
-      long long* cell = acc + (k * tpg + (int64_t)q) * range_n + ln;
+    const long long* cell = acc + q * range_n + ln;
+    for (int64_t k = 0; k < K; ++k, cell += acc_stride) {
       const float a = from_fixed(*cell, inv_fscale);
-      if (o_A_saved) o_A_saved[((k * B + b) * T + (T - 1)) * N + n] = a;
-      const float sc = s_types[ty * lcols + kTypeCols + k];
+      if (EXTRA && A.io.A_saved) A.io.A_saved[((k * B + b) * T + (T - 1)) * N + n] = a;
+      const float sc = row[8 + k];
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        const float mk = tab.made[k * S + s];
-        if (mk != 0.0f) {
-          gr[i][s] = gr[i][s] + a * (syn.jump_r[s] * sc * mk);
-          gd[i][s] = gd[i][s] + a * (syn.jump_d[s] * sc * mk);
+        if ((made >> (k * S + s)) & 1u) {
+          gr[i][s] = gr[i][s] + a * (syn.jump_r[s] * sc);
+          gd[i][s] = gd[i][s] + a * (syn.jump_d[s] * sc);
         }
       }
     }
-    if (o_track_g && (io.track_b < 0 || io.track_b == b)) {
-      const int64_t bt = io.track_b < 0 ? b : 0;
-      float* out = o_track_g + ((bt * T + (T - 1)) * N + n) * 2 * S;
+    if (EXTRA && A.io.track_g && (A.io.track_b < 0 || A.io.track_b == b)) {
+      const int64_t bt = A.io.track_b < 0 ? b : 0;
+      float* o = A.io.track_g + ((bt * T + (T - 1)) * N + n) * 2 * S;
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        out[s] = gr[i][s];
-        out[S + s] = gd[i][s];
+        o[s] = gr[i][s];
+        o[S + s] = gd[i][s];
       }
     }
   }
@@ -578,30 +643,29 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   // write the state back
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) {
-    const uint32_t it = threadIdx.x + (uint32_t)i * blockDim.x;
-    if (it < items32) {
-      const uint32_t q = it / nr32;
-      const int64_t n = lo + (it - q * nr32), b = g + (int64_t)q * groups;
-      io.v[b * N + n] = v[i];
-      if (refractory) io.counter[b * N + n] = counter[i];
+    const uint32_t d = desc[i];
+    if (d == kNoItem) continue;
+    const uint32_t ln = d & 0xffffu, q = (d >> 16) & 0xffu;
+    const int64_t n = lo + ln, b = g + (int64_t)q * groups;
+    A.io.v[b * N + n] = v[i];
+    if (refractory) A.io.counter[b * N + n] = counter[i];
 #pragma unroll
-      for (int s = 0; s < S; ++s) {
-        io.g[(b * 2 * S + s) * N + n] = gr[i][s];
-        io.g[(b * 2 * S + S + s) * N + n] = gd[i][s];
-      }
+    for (int s = 0; s < S; ++s) {
+      A.io.g[(b * 2 * S + s) * N + n] = gr[i][s];
+      A.io.g[(b * 2 * S + S + s) * N + n] = gd[i][s];
     }
   }
   if (A.timing && threadIdx.x < kPhases) A.timing[wg * kPhases + threadIdx.x] = s_time[threadIdx.x];
 }
 
 template <int S, int MAXI>
-inline hipError_t launch_run(RunArgs& a, size_t lds, int block, hipStream_t stream, bool coop) {
+inline hipError_t launch_run(RunArgs& a, size_t lds, hipStream_t stream, bool coop) {
   const bool extra = a.io.prob || a.io.v_saved || a.io.A_saved || a.io.track_v || a.io.track_g;
   const void* fn = extra ? reinterpret_cast<const void*>(&cond_run_kernel<S, MAXI, true>)
                          : reinterpret_cast<const void*>(&cond_run_kernel<S, MAXI, false>);
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
-  dim3 grid((unsigned)(a.geo.groups * a.geo.R)), blk((unsigned)block);
+  dim3 grid((unsigned)(a.geo.groups * a.geo.R)), blk((unsigned)kRunBlock);
   void* params[] = {&a};
   if (coop) return hipLaunchCooperativeKernel(fn, grid, blk, params, (unsigned)lds, stream);
   if (extra)
@@ -613,27 +677,25 @@ inline hipError_t launch_run(RunArgs& a, size_t lds, int block, hipStream_t stre
 
 template <int S>
 struct RunLaunch {  // run() is instantiated in wt_run_s<S>.hip
-  static hipError_t run(RunArgs& a, size_t lds, int block, int64_t per_thread,
-                        hipStream_t stream, bool coop);
+  static hipError_t run(RunArgs& a, size_t lds, int64_t per_thread, hipStream_t stream,
+                        bool coop);
 };
 
 template <int S>
-hipError_t RunLaunch<S>::run(RunArgs& a, size_t lds, int block, int64_t per_thread,
-                             hipStream_t stream, bool coop) {
-  {
-    switch (per_thread) {
-      case 0:
-      case 1: return launch_run<S, 1>(a, lds, block, stream, coop);
-      case 2: return launch_run<S, 2>(a, lds, block, stream, coop);
-      case 3: return launch_run<S, 3>(a, lds, block, stream, coop);
-      case 4: return launch_run<S, 4>(a, lds, block, stream, coop);
-      case 5: return launch_run<S, 5>(a, lds, block, stream, coop);
-      case 6: return launch_run<S, 6>(a, lds, block, stream, coop);
-      case 7:
-      case 8: return launch_run<S, 8>(a, lds, block, stream, coop);
-    }
-    return hipErrorInvalidValue;
+hipError_t RunLaunch<S>::run(RunArgs& a, size_t lds, int64_t per_thread, hipStream_t stream,
+                             bool coop) {
+  switch (per_thread) {
+    case 0:
+    case 1: return launch_run<S, 1>(a, lds, stream, coop);
+    case 2: return launch_run<S, 2>(a, lds, stream, coop);
+    case 3: return launch_run<S, 3>(a, lds, stream, coop);
+    case 4: return launch_run<S, 4>(a, lds, stream, coop);
+    case 5: return launch_run<S, 5>(a, lds, stream, coop);
+    case 6: return launch_run<S, 6>(a, lds, stream, coop);
+    case 7:
+    case 8: return launch_run<S, 8>(a, lds, stream, coop);
   }
-};
+  return hipErrorInvalidValue;
+}
 
 }  // namespace wt

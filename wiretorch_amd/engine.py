@@ -223,7 +223,7 @@ def geometry(B: int, N: int, K: int, n_cu: int, max_lds: int) -> tuple[int, int,
     groups = max(1, min(MAX_GROUPS, B))
     tpg = -(-B // groups)
     limit = max(1, n_cu // groups)
-    budget = max_lds - 24 * 1024 - 256 * (8 + K) * 4  # event list, type table
+    budget = max_lds - 24 * 1024 - MAX_TYPES * 64 - 16  # event list, type table
 
     def fits(R):
         range_n = -(-(-(-N // R)) // 32) * 32
@@ -241,11 +241,12 @@ def geometry(B: int, N: int, K: int, n_cu: int, max_lds: int) -> tuple[int, int,
 
 
 def _frac_bits(bound: float) -> int:
-    """Fractional bits of the fixed-point accumulator: exact while every per-target
-    sum stays below 2^61 / 2^frac."""
+    """Fractional bits of the fixed-point accumulator: every per-target sum stays below
+    2^51 / 2^frac, so the int64 accumulators stay below 2^53 (with each product's
+    rounding) and convert to float exactly once."""
     if bound <= 0:
         return MAX_FRAC_BITS
-    return max(0, min(MAX_FRAC_BITS, 61 - math.ceil(math.log2(bound)) - 1))
+    return max(0, min(MAX_FRAC_BITS, 51 - math.ceil(math.log2(bound))))
 
 
 def _type_table(tables: dict, scale: torch.Tensor, device):
