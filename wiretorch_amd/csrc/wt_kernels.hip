@@ -357,6 +357,8 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
   if (tab->n_types > kMaxLdsTypes) return hipErrorInvalidValue;
   // descriptors pack the target within the range in 16 bits, the trial in 8
   if (geo->range_n > 65535 || tpg > 255) return hipErrorInvalidValue;
+  // the fired list packs a source in 24 bits
+  if (tab->N >= (1 << 24)) return hipErrorInvalidValue;
 
   const int64_t acc_len = (tab->K > 0 ? tab->K : 1) * tpg * geo->range_n;
   const size_t lds = (size_t)run_types_offset(acc_len, tpg * a.words) +
@@ -366,8 +368,8 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
   if (qe == hipSuccess)
     qe = hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   if (qe != hipSuccess) return qe;
-  const size_t static_lds = kRunBlock * (8 + 4 + 4 + 4 + 1) + sizeof(BlockScan::storage_type) +
-                            kPhases * 8 + 64;
+  const size_t static_lds = kRunBlock * (8 + 4 + 4 + 4 + 1 + 4) +
+                            sizeof(BlockScan::storage_type) + kPhases * 8 + 64;
   if (lds + static_lds > (size_t)max_lds) return hipErrorInvalidValue;
   if (ff->n_src > 0 && io->x) {
     const int64_t rows = io->B * io->T;

@@ -43,7 +43,9 @@ struct RunArgs {
   int64_t tpg_max;      // trials of the largest group
 };
 
-// update, publish + arrive, input events, barrier wait, recurrent events + push
+// Phases timed by wt_cond_run_timed (thread 0's view): its own update, the wait for the
+// rest of the workgroup's update, publication + event compaction + arrival, the barrier
+// wait, range lookups + scan + synapse push.
 constexpr int kPhases = 5;
 constexpr int kInCap = 64;  // inputs listed per (trial, step); denser rows are scanned
 constexpr int kMaxLdsTypes = 256;
@@ -257,6 +259,8 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   __shared__ float s_value[kRunBlock];
   __shared__ uint8_t s_side[kRunBlock];
   __shared__ int32_t s_nev;
+  __shared__ int32_t s_nfired;
+  __shared__ uint32_t s_fired[kRunBlock];  // this step's fired sources: j | trial << 24
   __shared__ typename BlockScan::storage_type s_scan;
 
   const int64_t groups = A.geo.groups, R = A.geo.R, range_n = A.geo.range_n;
@@ -278,9 +282,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       reinterpret_cast<char*>(acc) + run_types_offset(acc_len, tpg * words));
   const bool refractory = A.tab.n_ref != nullptr;
   const bool recurrent = A.tab.K_rec > 0 && A.rec.n_src > 0;
-  // Every read of a published bitmap happens in the preload: the workgroup may then
-  // arrive at the barrier as soon as its own bits are out.
-  const bool early_arrive = group_words <= (int64_t)MAXI * blockDim.x;
+  const bool has_ff = A.ff.n_src > 0;
   const float dt = *A.tab.dt;
   const float fscale = ldexpf(1.0f, (int)A.geo.frac_bits);
   const float inv_fscale = ldexpf(1.0f, -(int)A.geo.frac_bits);
@@ -397,8 +399,23 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       const int64_t w = threadIdx.x + (int64_t)u * blockDim.x;
       pre[u] = (recurrent && w < group_words) ? load_agent(in_bits + w) : 0u;
     }
+    // This step's listed inputs, fetched now and used after the update: thread
+    // (q, e) = (tid / kInCap, tid % kInCap) holds input e of trial q's row.
+    int32_t in_c = 0, in_j = 0;
+    float in_v = 0.0f;
+    if (has_ff && threadIdx.x < (uint32_t)(tpg * kInCap)) {
+      ArgPtr P = kargs();
+      const int64_t bt = (g + (int64_t)(threadIdx.x / kInCap) * groups) * T + t;
+      const int64_t slot = bt * kInCap + threadIdx.x % kInCap;
+      in_c = gload(P->in_count + bt);
+      in_j = gload(P->in_idx + slot);
+      in_v = gload(P->in_val + slot);
+    }
     for (int64_t w = threadIdx.x; w < tpg * words; w += blockDim.x) s_bits[w] = 0;
-    if (threadIdx.x == 0) s_nev = 0;
+    if (threadIdx.x == 0) {
+      s_nev = 0;
+      s_nfired = 0;
+    }
     __syncthreads();
 
     // ---------------- (A) integrate step t for the owned neurons ----------------
@@ -495,6 +512,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     }
     tick(my_time, last, 0);
     __syncthreads();  // the accumulator is read and cleared; the next bits are complete
+    tick(my_time, last, 1);
 
     // ---------------- publish step t+1's spikes ----------------
     const bool publish = recurrent && more;
@@ -506,88 +524,106 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       }
     }
 
-    // ---------------- events of step t: inputs ----------------
+    // ---------------- events of step t ----------------
+    // (1) The fired bits are compacted into s_fired (source | trial << 24); sources past
+    // its capacity, and inputs of rows with more than kInCap of them, are listed here by
+    // the thread that finds them. Every read of this step's bitmap happens before the
+    // arrival at the barrier.
     {
       ArgPtr P = kargs();
-      const int64_t n_ff = P->ff.n_src;
-      if (n_ff > 0) {
-        const int64_t* ff_split = P->ff.split;
-        const int32_t* ff_path = P->ff.pathway;
-        const int32_t* ff_tg = P->ff.targets;
-        const float* ff_w = P->ff.weights;
-        const int32_t* in_count = P->in_count;
+      const int64_t* rec_split = P->rec.split;
+      const int32_t* rec_path = P->rec.pathway;
+      auto fired = [&](uint32_t w, uint32_t bits) {
+        const uint32_t q = w / (uint32_t)total_words, wl = w - q * (uint32_t)total_words;
+        const uint32_t j0 =
+            (wl / (uint32_t)words) * (uint32_t)range_n + (wl % (uint32_t)words) * 32;
+        int pos = atomicAdd(&s_nfired, __builtin_popcount(bits));
+        while (bits) {
+          const uint32_t j = j0 + __builtin_ctz(bits);
+          bits &= bits - 1;
+          if (pos < kRunBlock) {
+            s_fired[pos] = j | (q << 24);
+          } else {
+            const int32_t k = gload(rec_path + j);
+            const int64_t* sp = rec_split + (int64_t)j * (R + 1) + r;
+            if (k >= 0)
+              append_event(EL, acc, P->rec.targets, P->rec.weights, 0, gload(sp),
+                           gload(sp + 1), k * acc_stride + (int64_t)q * range_n, lo, 1.0f,
+                           fscale);
+          }
+          ++pos;
+        }
+      };
+      if (recurrent) {
+#pragma unroll
+        for (int u = 0; u < MAXI; ++u)
+          if (pre[u]) fired(threadIdx.x + (uint32_t)u * blockDim.x, pre[u]);
+        // words beyond the preload (only when the bitmap outgrows the registers)
+        for (int64_t w = threadIdx.x + (int64_t)MAXI * blockDim.x; w < group_words;
+             w += blockDim.x) {
+          const uint32_t bits = load_agent(in_bits + w);
+          if (bits) fired((uint32_t)w, bits);
+        }
+      }
+      if (has_ff) {
         const int64_t n_in = P->io.n_in, K_rec = P->tab.K_rec;
         for (int64_t q = 0; q < tpg; ++q) {
-          const int64_t b = g + q * groups, bt = b * T + t;
-          const int32_t c = gload(in_count + bt);
+          const int64_t bt = (g + q * groups) * T + t;
+          if (gload(P->in_count + bt) <= kInCap) continue;  // uniform
+          const float* xrow = P->io.x + bt * n_in;
           const int64_t row_base = (K_rec * tpg + q) * range_n;
-          if (c <= kInCap) {
-            for (int32_t e = threadIdx.x; e < c; e += blockDim.x) {
-              const int32_t j = gload(P->in_idx + bt * kInCap + e);
-              const int32_t k = gload(ff_path + j);
-              if (k < 0) continue;
-              const int64_t* sp = ff_split + (int64_t)j * (R + 1) + r;
-              append_event(EL, acc, ff_tg, ff_w, 1, gload(sp), gload(sp + 1),
-                           row_base + k * acc_stride, lo, gload(P->in_val + bt * kInCap + e),
-                           fscale);
-            }
-          } else {
-            const float* xrow = P->io.x + bt * n_in;
-            for (int64_t j = threadIdx.x; j < n_in; j += blockDim.x) {
-              const float xv = gload(xrow + j);
-              if (xv == 0.0f) continue;
-              const int32_t k = gload(ff_path + j);
-              if (k < 0) continue;
-              const int64_t* sp = ff_split + j * (R + 1) + r;
-              append_event(EL, acc, ff_tg, ff_w, 1, gload(sp), gload(sp + 1),
-                           row_base + k * acc_stride, lo, xv, fscale);
-            }
+          for (int64_t j = threadIdx.x; j < n_in; j += blockDim.x) {
+            const float xv = gload(xrow + j);
+            if (xv == 0.0f) continue;
+            const int32_t k = gload(P->ff.pathway + j);
+            if (k < 0) continue;
+            const int64_t* sp = P->ff.split + j * (R + 1) + r;
+            append_event(EL, acc, P->ff.targets, P->ff.weights, 1, gload(sp), gload(sp + 1),
+                         row_base + k * acc_stride, lo, xv, fscale);
           }
         }
       }
     }
-    tick(my_time, last, 2);
-    if (publish && early_arrive) {
-      barrier_arrive(my_barrier);
-      ++phase;
-    }
-    tick(my_time, last, 1);
-
-    // ---------------- events of step t: the fired bits ----------------
-    if (recurrent) {
-      ArgPtr P = kargs();
-      const int64_t* rec_split = P->rec.split;
-      const int32_t* rec_path = P->rec.pathway;
-      const int32_t* rec_tg = P->rec.targets;
-      const float* rec_w = P->rec.weights;
-      for (int64_t w = threadIdx.x, u = 0; w < group_words; w += blockDim.x, ++u) {
-        uint32_t bits = 0;
-#pragma unroll
-        for (int v_ = 0; v_ < MAXI; ++v_)
-          if (u == v_) bits = pre[v_];
-        if (u >= MAXI) bits = load_agent(in_bits + w);
-        if (!bits) continue;
-        const int64_t q = w / total_words, wl = w - q * total_words;
-        const int64_t j0 = (wl / words) * range_n + (wl % words) * 32;
-        while (bits) {
-          const int bit = __builtin_ctz(bits);
-          bits &= bits - 1;
-          const int64_t j = j0 + bit;
-          const int64_t* sp = rec_split + j * (R + 1) + r;
-          const int64_t e0 = gload(sp), e1 = gload(sp + 1);
-          const int32_t k = gload(rec_path + j);
-          if (k < 0) continue;
-          append_event(EL, acc, rec_tg, rec_w, 0, e0, e1, k * acc_stride + q * range_n, lo,
-                       1.0f, fscale);
-        }
-      }
-    }
-    if (publish && !early_arrive) {
+    if (publish) {
       barrier_arrive(my_barrier);
       ++phase;
     } else {
       __syncthreads();
     }
+    tick(my_time, last, 2);
+    // (2) One thread per listed fired source and per prefetched input: every range
+    // lookup in flight together, then the events appended.
+    {
+      ArgPtr P = kargs();
+      const int n_list = s_nfired < kRunBlock ? s_nfired : kRunBlock;
+      const bool has_rec = (int)threadIdx.x < n_list;
+      const bool has_in = (int)(threadIdx.x % kInCap) < in_c && in_c <= kInCap;
+      int64_t re0 = 0, re1 = 0, ie0 = 0, ie1 = 0;
+      int32_t rk = -1, ik = -1;
+      uint32_t rj = 0;
+      if (has_rec) {
+        rj = s_fired[threadIdx.x];
+        const int64_t* sp = P->rec.split + (int64_t)(rj & 0xffffffu) * (R + 1) + r;
+        re0 = gload(sp);
+        re1 = gload(sp + 1);
+        rk = gload(P->rec.pathway + (rj & 0xffffffu));
+      }
+      if (has_in) {
+        const int64_t* sp = P->ff.split + (int64_t)in_j * (R + 1) + r;
+        ie0 = gload(sp);
+        ie1 = gload(sp + 1);
+        ik = gload(P->ff.pathway + in_j);
+      }
+      if (rk >= 0)
+        append_event(EL, acc, P->rec.targets, P->rec.weights, 0, re0, re1,
+                     rk * acc_stride + (int64_t)(rj >> 24) * range_n, lo, 1.0f, fscale);
+      if (ik >= 0)
+        append_event(EL, acc, P->ff.targets, P->ff.weights, 1, ie0, ie1,
+                     (P->tab.K_rec * tpg + (int64_t)(threadIdx.x / kInCap)) * range_n +
+                         ik * acc_stride,
+                     lo, in_v, fscale);
+    }
+    __syncthreads();
     {
       const int m = s_nev < kRunBlock ? s_nev : kRunBlock;
       if (m > 0) {  // m is uniform: every thread takes part in the scan

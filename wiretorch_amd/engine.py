@@ -223,7 +223,7 @@ def geometry(B: int, N: int, K: int, n_cu: int, max_lds: int) -> tuple[int, int,
     groups = max(1, min(MAX_GROUPS, B))
     tpg = -(-B // groups)
     limit = max(1, n_cu // groups)
-    budget = max_lds - 24 * 1024 - MAX_TYPES * 64 - 16  # event list, type table
+    budget = max_lds - 28 * 1024 - MAX_TYPES * 64 - 16  # event lists, type table
 
     def fits(R):
         range_n = -(-(-(-N // R)) // 32) * 32
