@@ -360,16 +360,17 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
   // the fired list packs a source in 24 bits
   if (tab->N >= (1 << 24)) return hipErrorInvalidValue;
 
+  if (tpg * geo->range_n > kMaxItemsPerWg) return hipErrorInvalidValue;
   const int64_t acc_len = (tab->K > 0 ? tab->K : 1) * tpg * geo->range_n;
-  const size_t lds = (size_t)run_types_offset(acc_len, tpg * a.words) +
-                     (size_t)tab->n_types * kRow * 4;
+  const size_t lds = (size_t)acc_len * sizeof(double);
   int dev = 0, max_lds = 0;
   hipError_t qe = hipGetDevice(&dev);
   if (qe == hipSuccess)
     qe = hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   if (qe != hipSuccess) return qe;
   const size_t static_lds = kRunBlock * (8 + 4 + 4 + 4 + 1 + 4) +
-                            sizeof(BlockScan::storage_type) + kPhases * 8 + 64;
+                            sizeof(BlockScan::storage_type) + (kPhases + 1) * 8 + 64 +
+                            kMaxLdsTypes * kRow * 4 + kMaxOwnWords * 4;
   if (lds + static_lds > (size_t)max_lds) return hipErrorInvalidValue;
   if (ff->n_src > 0 && io->x) {
     const int64_t rows = io->B * io->T;

@@ -139,16 +139,4 @@ __host__ __device__ inline float surrogate(float x, float grad, float k) {
   return grad / (d * d);
 }
 
-// Exact fixed-point accumulation of activations: multiples of 2^-frac.
-__device__ inline long long to_fixed(float w, float scale) {
-  return (long long)rintf(w * scale);
-}
-// q -> float32, correctly rounded, for |q| < 2^53 (the host keeps every accumulator
-// below that): the two halves convert exactly to double and their sum is exact, so the
-// only rounding is the final one to float (the scale is a power of two).
-__device__ inline float from_fixed(long long q, float inv_scale) {
-  const double d = (double)(int32_t)(q >> 32) * 4294967296.0 + (double)(uint32_t)q;
-  return (float)d * inv_scale;
-}
-
 }  // namespace wt

@@ -18,6 +18,8 @@
 #include <rocprim/block/block_scan.hpp>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/wiretorch_amd.h"
 #include "wt_math.h"
 
@@ -52,13 +54,8 @@ constexpr int kMaxLdsTypes = 256;
 constexpr int kTypeCols = 6;  // global table: theta, U_reset, E_L, C_m, beta, n_ref; scale[K]
 // LDS table row (floats): theta, U_reset, E_L, C_m, n_ref, rate, g_L, -, scale[0..7]
 constexpr int kRow = 16;
-constexpr uint32_t kNoItem = 0xffffffffu;
-
-// Byte offset of the type table in the dynamic LDS: after the accumulators and the
-// workgroup's bits, rounded up to 16 bytes (float4 reads).
-__host__ __device__ inline int64_t run_types_offset(int64_t acc_len, int64_t bit_words) {
-  return (acc_len * 8 + bit_words * 4 + 15) / 16 * 16;
-}
+constexpr int kMaxItemsPerWg = 8 * kRunBlock;        // trials x range per workgroup
+constexpr int kMaxOwnWords = kMaxItemsPerWg / 32;    // the workgroup's own fired bits
 
 using BlockScan = rocprim::block_scan<int32_t, kRunBlock,
                                       rocprim::block_scan_algorithm::using_warp_scan>;
@@ -77,6 +74,11 @@ __device__ inline ArgPtr kargs() {
 // every item's addresses live in registers for the whole launch).
 __device__ inline uint32_t opaque(uint32_t x) {
   asm volatile("" : "+v"(x));
+  return x;
+}
+// The same for a wave-uniform value (kept in a scalar register).
+__device__ inline uint32_t opaque_s(uint32_t x) {
+  asm volatile("" : "+s"(x));
   return x;
 }
 
@@ -142,25 +144,34 @@ __device__ inline void load_synapses(const wt_tables& tab, Synapses<S>& syn) {
   }
 }
 
-__device__ inline void add_fixed(long long* cell, float x, float fscale) {
-  atomicAdd(reinterpret_cast<unsigned long long*>(cell), (unsigned long long)to_fixed(x, fscale));
+// Exact accumulation of activations. Each product is rounded to a multiple of 2^-f and
+// added in float64: the host keeps every accumulator below 2^(53-f) in magnitude, so
+// every partial sum is exact, the order of the atomic adds does not matter, and the
+// conversion to float32 at the end is the only other rounding.
+struct Fixed {
+  float scale;  // 2^f
+  double inv;   // 2^-f
+};
+__device__ inline void add_fixed(double* cell, float x, Fixed fx) {
+  atomicAdd(cell, (double)rintf(x * fx.scale) * fx.inv);
 }
 
 // Serial fallback for an event that did not fit the work list.
-__device__ inline void push_edges(long long* row, const int32_t* targets, const float* weights,
-                                  int64_t e0, int64_t e1, int64_t lo, float value,
-                                  float fscale) {
+__device__ inline void push_edges(double* row, const int32_t* targets, const float* weights,
+                                  int64_t e0, int64_t e1, int64_t lo, float value, Fixed fx) {
   for (int64_t e = e0; e < e1; ++e) {
     const float w = gload(weights + e);
-    add_fixed(row + (gload(targets + e) - lo), value == 1.0f ? w : value * w, fscale);
+    add_fixed(row + (gload(targets + e) - lo), value == 1.0f ? w : value * w, fx);
   }
 }
 
-__device__ inline void tick(uint64_t* acc_t, uint64_t& last, int phase) {
-  if (acc_t && threadIdx.x == 0) {
+// Phase timer (wt_cond_run_timed): s_time[0 .. kPhases) accumulate wall-clock ticks,
+// s_time[kPhases] holds the last reading.
+__device__ inline void tick(uint64_t* s_time, int phase) {
+  if (threadIdx.x == 0 && kargs()->timing) {
     const uint64_t now = wall_clock64();
-    acc_t[phase] += now - last;
-    last = now;
+    s_time[phase] += now - s_time[kPhases];
+    s_time[kPhases] = now;
   }
 }
 
@@ -176,9 +187,9 @@ struct EventList {
   int32_t* n;      // entries appended (may exceed the capacity: the rest ran serially)
 };
 
-__device__ inline void append_event(const EventList& L, long long* acc, const int32_t* targets,
+__device__ inline void append_event(const EventList& L, double* acc, const int32_t* targets,
                                     const float* weights, int side_id, int64_t e0, int64_t e1,
-                                    int64_t row, int64_t lo, float value, float fscale) {
+                                    int64_t row, int64_t lo, float value, Fixed fx) {
   if (e1 <= e0) return;
   const int pos = atomicAdd(L.n, 1);
   if (pos < kRunBlock) {
@@ -188,15 +199,15 @@ __device__ inline void append_event(const EventList& L, long long* acc, const in
     L.value[pos] = value;
     L.side[pos] = (uint8_t)side_id;
   } else {
-    push_edges(acc + row, targets, weights, e0, e1, lo, value, fscale);
+    push_edges(acc + row, targets, weights, e0, e1, lo, value, fx);
   }
 }
 
 // Every listed synapse, spread evenly over the workgroup (four per thread per round,
 // loads issued before the atomics), added to the accumulator. L.count holds the
 // exclusive prefix of the entries' edge counts.
-__device__ inline void run_events(const EventList& L, int m, int32_t total, long long* acc,
-                                  int64_t lo, float fscale) {
+__device__ inline void run_events(const EventList& L, int m, int32_t total, double* acc,
+                                  int64_t lo, Fixed fx) {
   ArgPtr P = kargs();
   const int32_t* const rec_tg = P->rec.targets;
   const int32_t* const ff_tg = P->ff.targets;
@@ -241,18 +252,20 @@ __device__ inline void run_events(const EventList& L, int m, int32_t total, long
 #pragma unroll
     for (int u = 0; u < 4; ++u)
       if (base + u * stride < total)
-        add_fixed(acc + rows[u] + tgt[u], val[u] == 1.0f ? w[u] : val[u] * w[u], fscale);
+        add_fixed(acc + rows[u] + tgt[u], val[u] == 1.0f ? w[u] : val[u] * w[u], fx);
   }
 }
 
 // The persistent forward. Each thread owns up to MAXI (trial, neuron) items — item
 // threadIdx.x + i * blockDim.x of its workgroup — whose state stays in registers for
 // the whole launch.
-template <int S, int MAXI, bool EXTRA>
+template <int S, int MAXI, bool EXTRA, bool REFR>
 __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
-  extern __shared__ __align__(16) long long acc[];  // [K][tpg][range_n], own bits, types
+  extern __shared__ __align__(16) double acc[];  // [K][tpg][range_n]
+  __shared__ __align__(16) float s_types[kMaxLdsTypes * kRow];
+  __shared__ uint32_t s_bits[kMaxOwnWords];  // [tpg][words]: the next step's own spikes
   __shared__ uint32_t s_flag;
-  __shared__ uint64_t s_time[kPhases];
+  __shared__ uint64_t s_time[kPhases + 1];
   __shared__ int64_t s_e0[kRunBlock];
   __shared__ int32_t s_count[kRunBlock];
   __shared__ int32_t s_row[kRunBlock];
@@ -263,29 +276,29 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   __shared__ uint32_t s_fired[kRunBlock];  // this step's fired sources: j | trial << 24
   __shared__ typename BlockScan::storage_type s_scan;
 
-  const int64_t groups = A.geo.groups, R = A.geo.R, range_n = A.geo.range_n;
-  const int64_t N = A.tab.N, K = A.tab.K, B = A.io.B, T = A.io.T;
-  const int64_t wg = blockIdx.x;
-  const int64_t g = wg % groups, r = wg / groups;
-  const int64_t tpg = g < B ? (B - g + groups - 1) / groups : 0;
+  // Sizes in 32 bits (the host checks that they fit); offsets into (B, T, N) arrays
+  // are formed in 64 bits.
+  const int32_t groups = (int32_t)A.geo.groups, R = (int32_t)A.geo.R;
+  const int32_t range_n = (int32_t)A.geo.range_n;
+  const int32_t N = (int32_t)A.tab.N, K = (int32_t)A.tab.K, B = (int32_t)A.io.B;
+  const int32_t T = (int32_t)A.io.T;
+  const int32_t wg = blockIdx.x;
+  const int32_t g = wg % groups, r = wg / groups;
+  const int32_t tpg = g < B ? (B - g + groups - 1) / groups : 0;
   if (tpg == 0) return;  // no trial in this group: it takes part in nothing
-  const int64_t lo = r * range_n;
-  const int64_t nr = lo < N ? (N - lo < range_n ? N - lo : range_n) : 0;
+  const int32_t lo = r * range_n;
+  const int32_t nr = lo < N ? (N - lo < range_n ? N - lo : range_n) : 0;
   const uint32_t items = (uint32_t)(tpg * nr);
-  const int64_t words = A.words;
-  const int64_t total_words = R * words;        // one trial's bitmap
-  const int64_t group_words = tpg * total_words;
+  const int32_t words = (int32_t)A.words;
+  const int32_t total_words = R * words;        // one trial's bitmap
+  const int32_t group_words = tpg * total_words;
   const uint32_t acc_stride = (uint32_t)(tpg * range_n);  // one pathway's accumulators
-  const int64_t acc_len = (K > 0 ? K : 1) * (int64_t)acc_stride;
-  uint32_t* s_bits = reinterpret_cast<uint32_t*>(acc + acc_len);  // [tpg][words]
-  float* s_types = reinterpret_cast<float*>(                       // 16-byte aligned rows
-      reinterpret_cast<char*>(acc) + run_types_offset(acc_len, tpg * words));
-  const bool refractory = A.tab.n_ref != nullptr;
+  const int32_t acc_len = (K > 0 ? K : 1) * (int32_t)acc_stride;
+  constexpr bool refractory = REFR;  // the network has refractory periods
   const bool recurrent = A.tab.K_rec > 0 && A.rec.n_src > 0;
   const bool has_ff = A.ff.n_src > 0;
   const float dt = *A.tab.dt;
-  const float fscale = ldexpf(1.0f, (int)A.geo.frac_bits);
-  const float inv_fscale = ldexpf(1.0f, -(int)A.geo.frac_bits);
+  const Fixed fx{ldexpf(1.0f, (int)A.geo.frac_bits), ldexp(1.0, -(int)A.geo.frac_bits)};
   const EventList EL{s_e0, s_count, s_row, s_value, s_side, &s_nev};
   Synapses<S> syn;
   load_synapses<S>(A.tab, syn);
@@ -294,11 +307,10 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
 #pragma unroll
     for (int s = 0; s < S; ++s)
       if (A.tab.made[k * S + s] != 0.0f) made |= 1ull << (k * S + s);
-  uint64_t* my_time = A.timing ? s_time : nullptr;
   if (threadIdx.x < kPhases) s_time[threadIdx.x] = 0;
-  uint64_t last = wall_clock64();
+  if (threadIdx.x == 0) s_time[kPhases] = wall_clock64();
 
-  for (int64_t i = threadIdx.x; i < acc_len; i += blockDim.x) acc[i] = 0;
+  for (int64_t i = threadIdx.x; i < acc_len; i += blockDim.x) acc[i] = 0.0;
   {
     const int64_t cols = kTypeCols + K;
     for (int64_t ty = threadIdx.x; ty < A.tab.n_types; ty += blockDim.x) {
@@ -318,14 +330,16 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   }
 
   // Registers: the owned items' state and descriptors (target within the range in bits
-  // 0-15, trial within the group in 16-23, row of the type table in 24-31).
+  // 0-15, trial within the group in 16-23, row of the type table in 24-31). A thread's
+  // item i is item threadIdx.x + i * kRunBlock of the workgroup; past the last item the
+  // descriptor is 0 and the state zeros, so every lane may compute (only writes check).
   float v[MAXI], gr[MAXI][S], gd[MAXI][S];
   int32_t counter[MAXI];
   uint32_t desc[MAXI];
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) {
-    const uint32_t it = threadIdx.x + (uint32_t)i * blockDim.x;
-    desc[i] = kNoItem;
+    const uint32_t it = threadIdx.x + (uint32_t)i * kRunBlock;
+    desc[i] = 0;
     v[i] = 0.0f;
     counter[i] = 0;
 #pragma unroll
@@ -357,7 +371,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) {
     const uint32_t d = desc[i];
-    if (d == kNoItem) continue;
+    if (threadIdx.x + (uint32_t)i * kRunBlock >= items) continue;
     const uint32_t ln = d & 0xffffu, q = (d >> 16) & 0xffu;
     const float* row = s_types + (d >> 24) * kRow;
     const float theta = row[0];
@@ -385,14 +399,14 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     ++phase;
   }
 
-  for (int64_t t = 0; t < T; ++t) {
+  for (int32_t t = 0; t < T; ++t) {
     const bool more = t + 1 < T;
     const uint32_t* in_bits = group_bits + (t & 1) * buffer_words;
     // ---- the group's fired bits of step t: complete once every workgroup arrived ----
     if (recurrent) {
       if (!barrier_wait(my_barrier, phase * (uint32_t)R, A.err, &s_flag)) return;
     }
-    tick(my_time, last, 3);
+    tick(s_time, 3);
     uint32_t pre[MAXI];
 #pragma unroll
     for (int u = 0; u < MAXI; ++u) {
@@ -419,22 +433,28 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     __syncthreads();
 
     // ---------------- (A) integrate step t for the owned neurons ----------------
-    {
+    // (step 0 has no previous activations to inject: its own instance of the loop)
+    auto update = [&](auto inject_tag) {
+      constexpr bool kInject = decltype(inject_tag)::value;
       float* const spikes = A.io.spikes;
       // element (b, t, n) of a (B, T, N) array: step_base + q * trial_stride + ln
-      const int64_t step_base = (g * T + t) * N + lo;
-      const uint64_t trial_stride = (uint64_t)(groups * T * N);
+      const int64_t step_base = ((int64_t)g * T + t) * N + lo;
+      const uint64_t trial_stride = (uint64_t)groups * T * N;
       uint32_t masks_next = 0;
+      const uint32_t wave_base = opaque_s(__builtin_amdgcn_readfirstlane(threadIdx.x) & ~63u);
 #pragma unroll
       for (int i = 0; i < MAXI; ++i) {
+        // a wave skips item i only when none of its lanes holds one (a uniform branch:
+        // the state is then updated in place on every path)
+        if (wave_base + (uint32_t)i * kRunBlock >= items) continue;
+        const bool valid = opaque(threadIdx.x + (uint32_t)i * kRunBlock) < items;
         const uint32_t d = opaque(desc[i]);
-        if (d == kNoItem) continue;
         const uint32_t ln = d & 0xffffu, q = (d >> 16) & 0xffu;
         const float* row = s_types + (d >> 24) * kRow;
         const int64_t out = step_base + (int64_t)((uint64_t)q * trial_stride) + ln;
         const int64_t b = EXTRA ? g + (int64_t)q * groups : 0;
         const int64_t n = lo + ln;
-        if (t > 0) {
+        if constexpr (kInject) {
           // g <- g * decay, then each pathway's activation times its kernel, in order
           // (dynamics.py:206-208; kernel = jump * scale * made, dynamics.py:95-100).
 #pragma unroll
@@ -442,11 +462,11 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
             gr[i][s] = gr[i][s] * syn.decay_r[s];
             gd[i][s] = gd[i][s] * syn.decay_d[s];
           }
-          long long* cell = acc + __umul24(q, (uint32_t)range_n) + ln;
+          double* cell = acc + __umul24(q, (uint32_t)range_n) + ln;
           for (int64_t k = 0; k < K; ++k, cell += acc_stride) {
-            const float a = from_fixed(*cell, inv_fscale);
-            *cell = 0;
-            if (EXTRA && A.io.A_saved) A.io.A_saved[((k * B + b) * T + (t - 1)) * N + n] = a;
+            const float a = (float)*cell;
+            if (valid) *cell = 0.0;
+            if (EXTRA && valid && A.io.A_saved) A.io.A_saved[((k * B + b) * T + (t - 1)) * N + n] = a;
             const float sc = row[8 + k];
 #pragma unroll
             for (int s = 0; s < S; ++s) {
@@ -456,7 +476,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
               }
             }
           }
-          if (EXTRA && A.io.track_g && (A.io.track_b < 0 || A.io.track_b == b)) {
+          if (EXTRA && valid && A.io.track_g && (A.io.track_b < 0 || A.io.track_b == b)) {
             const int64_t bt = A.io.track_b < 0 ? b : 0;
             float* o = A.io.track_g + ((bt * T + (t - 1)) * N + n) * 2 * S;
 #pragma unroll
@@ -471,17 +491,17 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
         const float s_t = (float)((masks >> i) & 1u);
         const float held_t = (float)((masks >> (8 + i)) & 1u);
         const float r_hold = refractory ? fmaxf(s_t, held_t) : s_t;
-        spikes[out] = s_t;
+        if (valid) spikes[out] = s_t;
         float G[S], I[S], I_leak;
         const float v_next = membrane<S>(v[i], r_hold, gr[i], gd[i], syn, p0.z, p0.w, p0.y,
                                          Leak{p1.y, p1.z}, dt, G, I, I_leak);
-        if (EXTRA && A.io.v_saved) {
+        if (EXTRA && valid && A.io.v_saved) {
           A.io.v_saved[out] = v[i];
 #pragma unroll
           for (int s = 0; s < S; ++s) A.io.G_saved[out * S + s] = G[s];
           if (refractory && A.io.held) A.io.held[out] = (int8_t)(held_t != 0.0f);
         }
-        if (EXTRA && A.io.track_v && (A.io.track_b < 0 || A.io.track_b == b)) {
+        if (EXTRA && valid && A.io.track_v && (A.io.track_b < 0 || A.io.track_b == b)) {
           const int64_t bt = A.io.track_b < 0 ? b : 0;
           const int64_t trow = (bt * T + t) * N + n;
           A.io.track_v[trow] = v_next;
@@ -496,10 +516,10 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
                                           r_next, held);
           if (s_next != 0.0f) {
             masks_next |= 1u << i;
-            if (recurrent) atomicOr(&s_bits[q * words + (ln >> 5)], 1u << (ln & 31));
+            if (recurrent && valid) atomicOr(&s_bits[q * words + (ln >> 5)], 1u << (ln & 31));
           }
           if (held != 0.0f) masks_next |= 256u << i;
-          if (EXTRA && A.io.prob) {
+          if (EXTRA && valid && A.io.prob) {
             const float pr = 1.0f / (1.0f + expf(-(*A.tab.surr * (v_next - p0.x))));
             A.io.prob[out + N] = refractory ? pr * (1.0f - held) : pr;
           }
@@ -509,10 +529,14 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
         __builtin_amdgcn_sched_barrier(0);
       }
       masks = masks_next;
-    }
-    tick(my_time, last, 0);
+    };
+    if (t == 0)
+      update(std::false_type{});
+    else
+      update(std::true_type{});
+    tick(s_time, 0);
     __syncthreads();  // the accumulator is read and cleared; the next bits are complete
-    tick(my_time, last, 1);
+    tick(s_time, 1);
 
     // ---------------- publish step t+1's spikes ----------------
     const bool publish = recurrent && more;
@@ -549,7 +573,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
             if (k >= 0)
               append_event(EL, acc, P->rec.targets, P->rec.weights, 0, gload(sp),
                            gload(sp + 1), k * acc_stride + (int64_t)q * range_n, lo, 1.0f,
-                           fscale);
+                           fx);
           }
           ++pos;
         }
@@ -579,7 +603,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
             if (k < 0) continue;
             const int64_t* sp = P->ff.split + j * (R + 1) + r;
             append_event(EL, acc, P->ff.targets, P->ff.weights, 1, gload(sp), gload(sp + 1),
-                         row_base + k * acc_stride, lo, xv, fscale);
+                         row_base + k * acc_stride, lo, xv, fx);
           }
         }
       }
@@ -590,7 +614,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     } else {
       __syncthreads();
     }
-    tick(my_time, last, 2);
+    tick(s_time, 2);
     // (2) One thread per listed fired source and per prefetched input: every range
     // lookup in flight together, then the events appended.
     {
@@ -616,12 +640,12 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       }
       if (rk >= 0)
         append_event(EL, acc, P->rec.targets, P->rec.weights, 0, re0, re1,
-                     rk * acc_stride + (int64_t)(rj >> 24) * range_n, lo, 1.0f, fscale);
+                     rk * acc_stride + (int64_t)(rj >> 24) * range_n, lo, 1.0f, fx);
       if (ik >= 0)
         append_event(EL, acc, P->ff.targets, P->ff.weights, 1, ie0, ie1,
                      (P->tab.K_rec * tpg + (int64_t)(threadIdx.x / kInCap)) * range_n +
                          ik * acc_stride,
-                     lo, in_v, fscale);
+                     lo, in_v, fx);
     }
     __syncthreads();
     {
@@ -632,18 +656,18 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
         BlockScan().exclusive_scan(c, c, 0, total, s_scan);
         if (tid < m) s_count[tid] = c;
         __syncthreads();
-        run_events(EL, m, total, acc, lo, fscale);
+        run_events(EL, m, total, acc, lo, fx);
       }
     }
     __syncthreads();  // the accumulator is complete for the next update
-    tick(my_time, last, 4);
+    tick(s_time, 4);
   }
 
   // The activations of the last step enter the conductances that leave the chunk.
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) {
     const uint32_t d = desc[i];
-    if (d == kNoItem || T == 0) continue;
+    if (threadIdx.x + (uint32_t)i * kRunBlock >= items || T == 0) continue;
     const uint32_t ln = d & 0xffffu, q = (d >> 16) & 0xffu;
     const float* row = s_types + (d >> 24) * kRow;
     const int64_t n = lo + ln, b = g + (int64_t)q * groups;
@@ -652,9 +676,9 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       gr[i][s] = gr[i][s] * syn.decay_r[s];
       gd[i][s] = gd[i][s] * syn.decay_d[s];
     }
-    const long long* cell = acc + q * range_n + ln;
+    const double* cell = acc + q * range_n + ln;
     for (int64_t k = 0; k < K; ++k, cell += acc_stride) {
-      const float a = from_fixed(*cell, inv_fscale);
+      const float a = (float)*cell;
       if (EXTRA && A.io.A_saved) A.io.A_saved[((k * B + b) * T + (T - 1)) * N + n] = a;
       const float sc = row[8 + k];
 #pragma unroll
@@ -680,7 +704,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) {
     const uint32_t d = desc[i];
-    if (d == kNoItem) continue;
+    if (threadIdx.x + (uint32_t)i * kRunBlock >= items) continue;
     const uint32_t ln = d & 0xffffu, q = (d >> 16) & 0xffu;
     const int64_t n = lo + ln, b = g + (int64_t)q * groups;
     A.io.v[b * N + n] = v[i];
@@ -694,21 +718,27 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   if (A.timing && threadIdx.x < kPhases) A.timing[wg * kPhases + threadIdx.x] = s_time[threadIdx.x];
 }
 
-template <int S, int MAXI>
-inline hipError_t launch_run(RunArgs& a, size_t lds, hipStream_t stream, bool coop) {
-  const bool extra = a.io.prob || a.io.v_saved || a.io.A_saved || a.io.track_v || a.io.track_g;
-  const void* fn = extra ? reinterpret_cast<const void*>(&cond_run_kernel<S, MAXI, true>)
-                         : reinterpret_cast<const void*>(&cond_run_kernel<S, MAXI, false>);
+template <int S, int MAXI, bool EXTRA, bool REFR>
+inline hipError_t launch_one(RunArgs& a, size_t lds, hipStream_t stream, bool coop) {
+  const void* fn = reinterpret_cast<const void*>(&cond_run_kernel<S, MAXI, EXTRA, REFR>);
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   dim3 grid((unsigned)(a.geo.groups * a.geo.R)), blk((unsigned)kRunBlock);
   void* params[] = {&a};
   if (coop) return hipLaunchCooperativeKernel(fn, grid, blk, params, (unsigned)lds, stream);
-  if (extra)
-    hipLaunchKernelGGL((cond_run_kernel<S, MAXI, true>), grid, blk, lds, stream, a);
-  else
-    hipLaunchKernelGGL((cond_run_kernel<S, MAXI, false>), grid, blk, lds, stream, a);
+  hipLaunchKernelGGL((cond_run_kernel<S, MAXI, EXTRA, REFR>), grid, blk, lds, stream, a);
   return hipGetLastError();
+}
+
+template <int S, int MAXI>
+inline hipError_t launch_run(RunArgs& a, size_t lds, hipStream_t stream, bool coop) {
+  const bool extra = a.io.prob || a.io.v_saved || a.io.A_saved || a.io.track_v || a.io.track_g;
+  const bool refr = a.tab.n_ref != nullptr;
+  if (extra)
+    return refr ? launch_one<S, MAXI, true, true>(a, lds, stream, coop)
+                : launch_one<S, MAXI, true, false>(a, lds, stream, coop);
+  return refr ? launch_one<S, MAXI, false, true>(a, lds, stream, coop)
+              : launch_one<S, MAXI, false, false>(a, lds, stream, coop);
 }
 
 template <int S>

@@ -223,11 +223,11 @@ def geometry(B: int, N: int, K: int, n_cu: int, max_lds: int) -> tuple[int, int,
     groups = max(1, min(MAX_GROUPS, B))
     tpg = -(-B // groups)
     limit = max(1, n_cu // groups)
-    budget = max_lds - 28 * 1024 - MAX_TYPES * 64 - 16  # event lists, type table
+    budget = max_lds - 46 * 1024  # static: event lists, type table, own bits
 
     def fits(R):
         range_n = -(-(-(-N // R)) // 32) * 32
-        lds = max(K, 1) * tpg * range_n * 8 + tpg * (range_n // 32) * 4
+        lds = max(K, 1) * tpg * range_n * 8
         return lds <= budget and tpg * range_n <= 8 * BLOCK, range_n
 
     R = max(1, min(limit, -(-N * tpg // BLOCK)))
