@@ -122,9 +122,11 @@ int wt_cond_run(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
                 wt_stream_t stream);
 
 /* wt_cond_run_timed — wt_cond_run with per-workgroup wall-clock ticks (100 MHz) of each
- * phase of the step loop added to timing[wg * 5 + phase], phases: neuron update,
- * publishing the fired bitmap, feedforward push, barrier wait, recurrent push. For
- * profiling; no counterpart in the reference. timing: (groups * R * 5) u64. */
+ * phase of the step loop, as seen by the workgroup's first thread, added to
+ * timing[wg * 5 + phase], phases: its own neuron update, the wait for the rest of the
+ * workgroup's update, publication + event listing + barrier arrival, barrier wait,
+ * range lookups + scan + synapse push. For profiling; no counterpart in the reference.
+ * timing: (groups * R * 5) u64. */
 int wt_cond_run_timed(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
                       const wt_geometry* geo, const wt_run_io* io, void* scratch,
                       uint64_t* timing, wt_stream_t stream);
@@ -162,6 +164,21 @@ typedef struct {
 
 int wt_cond_scan_backward(const wt_tables* tab, const wt_backward_io* io,
                           wt_stream_t stream);
+
+/* wt_cond_recurrent_backward — the same adjoint when gradients also flow back through
+ * the recurrent spikes (recurrent_gradients=True): per reverse step, dL/da of every
+ * neuron, then R_j = sum over source j's synapses e of w_e * dL/da_k(j)[target e] added
+ * to dL/ds_j before the surrogate. io as for wt_cond_scan_backward; rec is the
+ * recurrent side (indptr, targets, weights, pathway; split unused), n_src == N.
+ * scratch: wt_cond_recurrent_backward_scratch_bytes(S, K_rec, B, N) bytes, no zeroing
+ * needed (adjoint state between the steps and the current step's dL/da).
+ * Replaces: conductance/engine.py:386-438 _recurrent_backward — per step
+ * conductance/kernels.py:704-823 inject_backward, network_simulators/engine.py:257-271
+ * carry_to_sources, network_simulators/kernels.py:214-241 spike_backward. */
+int64_t wt_cond_recurrent_backward_scratch_bytes(int64_t S, int64_t K_rec, int64_t B,
+                                                 int64_t N);
+int wt_cond_recurrent_backward(const wt_tables* tab, const wt_side* rec,
+                               const wt_backward_io* io, void* scratch, wt_stream_t stream);
 
 /* wt_edge_sources — edge_src[e] = the source of edge e (E = indptr[n_src]). */
 int wt_edge_sources(const int64_t* indptr, int64_t n_src, int64_t* edge_src,

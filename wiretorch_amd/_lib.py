@@ -66,6 +66,9 @@ SIGNATURES = {
                                          ctypes.POINTER(RunIO), P, P, P]),
     "wt_cond_scan_backward": (ctypes.c_int, [ctypes.POINTER(Tables),
                                              ctypes.POINTER(BackwardIO), P]),
+    "wt_cond_recurrent_backward_scratch_bytes": (I64, [I64, I64, I64, I64]),
+    "wt_cond_recurrent_backward": (ctypes.c_int, [ctypes.POINTER(Tables), ctypes.POINTER(Side),
+                                                  ctypes.POINTER(BackwardIO), P, P]),
     "wt_edge_sources": (ctypes.c_int, [P, I64, P, P]),
     "wt_weight_gradient": (ctypes.c_int, [ctypes.POINTER(Side), P, I64, P, P, P, P, I64,
                                           I64, I64, I64, P, P]),

@@ -1,0 +1,344 @@
+// wt_back.h — the surrogate-gradient backward of the conductance-LIF scan: the reverse
+// step shared by two drivers, instantiated per synapse count S in wt_run_s<S>.hip.
+//
+//  * BackLaunch<S>::run (wt_cond_scan_backward): one thread per (trial, neuron) runs all
+//    T steps in reverse with its adjoint state in registers. The recurrent activations
+//    are treated as inputs (gradients do not flow back through the recurrent spikes).
+//  * BackLaunch<S>::recurrent (wt_cond_recurrent_backward): gradients also flow through
+//    the recurrent spikes (the reference's recurrent_gradients=True). Every step couples
+//    all neurons: dL/ds_j(t) gains R_j = sum over j's synapses e of w_e dL/da(t)[target e].
+//    Each step is then two launches, with the adjoint state in global memory between
+//    them: (1) every neuron's adjoint through the membrane and the conductances, which
+//    gives dL/da(t); (2) per source, R gathered along its synapses (CSR by source, a
+//    fixed order: deterministic) and the surrogate spike term.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/wiretorch_amd.h"
+#include "wt_math.h"
+
+namespace wt {
+
+struct BackArgs {
+  wt_tables tab;
+  wt_backward_io io;
+  wt_side rec;      // recurrent side (recurrent path only)
+  float* state;     // adjoint state, [back_fields<S>()][B * N] (recurrent path only)
+  float* grad_now;  // dL/da of the current step, [K_rec][N][B] (recurrent path only)
+};
+
+// The adjoint state of one (trial, neuron) between reverse steps.
+template <int S>
+struct BackState {
+  float dv;                          // dL/dv entering the step after
+  float lr[S], ld[S];                // dL/dg (rise, decay) entering the step after
+  float Hr[S], Hd[S];                // decay-gradient recursions
+  float accE[S], accDr[S], accDd[S], accJr[S], accJd[S];
+  float acc_scale[WT_MAX_K];
+  float acc_theta, acc_reset, acc_EL, acc_Cm, acc_beta;
+};
+template <int S>
+constexpr int back_fields() { return 1 + 9 * S + WT_MAX_K + 5; }
+
+// Global layout of the recurrent path's state: field f of item idx at f * BN + idx.
+template <int S>
+__device__ inline void state_io(BackState<S>& st, float* base, int64_t BN, int64_t idx,
+                                bool store) {
+  float* p = base + idx;
+  auto x = [&](float& v) {
+    if (store) *p = v; else v = *p;
+    p += BN;
+  };
+  x(st.dv);
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    x(st.lr[s]); x(st.ld[s]); x(st.Hr[s]); x(st.Hd[s]); x(st.accE[s]);
+    x(st.accDr[s]); x(st.accDd[s]); x(st.accJr[s]); x(st.accJd[s]);
+  }
+#pragma unroll
+  for (int k = 0; k < WT_MAX_K; ++k) x(st.acc_scale[k]);
+  x(st.acc_theta); x(st.acc_reset); x(st.acc_EL); x(st.acc_Cm); x(st.acc_beta);
+}
+
+template <int S>
+__device__ inline void state_zero(BackState<S>& st) {
+  st.dv = 0.0f;
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+    st.lr[s] = st.ld[s] = st.Hr[s] = st.Hd[s] = st.accE[s] = st.accDr[s] = st.accDd[s] =
+        st.accJr[s] = st.accJd[s] = 0.0f;
+#pragma unroll
+  for (int k = 0; k < WT_MAX_K; ++k) st.acc_scale[k] = 0.0f;
+  st.acc_theta = st.acc_reset = st.acc_EL = st.acc_Cm = st.acc_beta = 0.0f;
+}
+
+// One neuron's constants of the backward.
+struct BackNeuron {
+  float theta, E_L, C_m, beta, dt, k_surr;
+  Leak lk;
+};
+
+__device__ inline BackNeuron back_neuron(const wt_tables& tab, int64_t n) {
+  BackNeuron c;
+  c.theta = tab.theta[n];
+  c.E_L = tab.E_L[n];
+  c.C_m = tab.C_m[n];
+  c.beta = tab.beta[n];
+  c.dt = *tab.dt;
+  c.k_surr = *tab.surr;
+  c.lk = leak(c.C_m, c.beta, c.dt);
+  return c;
+}
+
+// Reverse step t, all but the spike of step t: the injections of step t (dL/da_k, the
+// jump and decay partials), the membrane update, and the conductances decaying into
+// step t+1. Leaves st.dv = dL/dv_t without the spike's term. When grad_now is set,
+// dL/da_k for the recurrent pathways is also written there, [k][n][b].
+template <int S>
+__device__ inline void back_membrane_step(BackState<S>& st, const BackArgs& P,
+                                          const Synapses<S>& syn, const BackNeuron& c,
+                                          int64_t b, int64_t n, int64_t t) {
+  const wt_tables& tab = P.tab;
+  const wt_backward_io& io = P.io;
+  const int64_t N = tab.N, K = tab.K, B = io.B, T = io.T;
+  const bool refractory = io.held != nullptr;
+  const bool want_A = io.grad_A != nullptr, want_scale = io.grad_scale != nullptr;
+  const bool want_decay = io.grad_decay != nullptr, want_jump = io.grad_jump != nullptr;
+  const int64_t out = (b * T + t) * N + n;
+  const float v = io.v_saved[out];
+  const float s_sp = io.spikes[out];
+  const float held = refractory ? (float)io.held[out] : 0.0f;
+  const float r = refractory ? fmaxf(s_sp, held) : s_sp;
+  float G[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) G[s] = io.G_saved[out * S + s];
+
+  // Injections of step t: per unit jump, sum_k a_k scale_k made_k (jump, decay).
+  if (want_decay || want_jump) {
+    float base[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) base[s] = 0.0f;
+    for (int64_t k = 0; k < K; ++k) {
+      const float as = io.A[((k * B + b) * T + t) * N + n] * tab.scale[k * N + n];
+#pragma unroll
+      for (int s = 0; s < S; ++s) base[s] += as * tab.made[k * S + s];
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      if (want_jump) {
+        st.accJr[s] += st.lr[s] * base[s];
+        st.accJd[s] += st.ld[s] * base[s];
+      }
+      if (want_decay) {
+        st.accDr[s] += syn.jump_r[s] * base[s] * st.Hr[s];
+        st.accDd[s] += syn.jump_d[s] * base[s] * st.Hd[s];
+        st.Hr[s] = st.lr[s] + syn.decay_r[s] * st.Hr[s];
+        st.Hd[s] = st.ld[s] + syn.decay_d[s] * st.Hd[s];
+      }
+    }
+  }
+  // dL/da_k of step t: the adjoint of the conductances it was injected into.
+#pragma unroll
+  for (int k = 0; k < WT_MAX_K; ++k) {
+    if (k >= K) break;
+    float qk = 0.0f;
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+      qk += (syn.jump_r[s] * st.lr[s] + syn.jump_d[s] * st.ld[s]) * tab.made[k * S + s];
+    const int64_t ka = ((k * B + b) * T + t) * N + n;
+    const float ga = qk * tab.scale[k * N + n];
+    if (want_A) io.grad_A[ka] = ga;
+    if (P.grad_now && k < tab.K_rec) P.grad_now[(k * N + n) * B + b] = ga;
+    if (want_scale) st.acc_scale[k] += qk * io.A[ka];
+  }
+  // Membrane.
+  const float gx = st.dv * (1.0f - r);
+  float dG[S], Gc[S];
+  const MembraneAdjoint m =
+      membrane_adjoint<S>(gx, v, G, syn, c.E_L, c.C_m, c.lk, c.dt, dG, Gc);
+  st.acc_reset += st.dv * r;
+  st.acc_EL += gx * m.phi * c.lk.g_L;
+  if (io.grad_C_m || io.grad_beta) {
+    const float g_v = v - c.E_L;
+    if (io.grad_C_m) {  // g_L = C rate and a both depend on C
+      const float inv_C = 1.0f / c.C_m;
+      const float dphi =
+          -(m.a * c.dt * m.Gt * inv_C * inv_C + m.phi * c.lk.g_L * inv_C) * m.inv_g;
+      st.acc_Cm -= gx * (dphi * m.J + m.phi * g_v * c.lk.g_L * inv_C);
+    }
+    if (io.grad_beta) {  // rate = -log(beta) / dt
+      const float dg_L = -c.C_m / (c.beta * c.dt);
+      const float dphi = -(m.a / c.beta + m.phi * dg_L) * m.inv_g;
+      st.acc_beta -= gx * (dphi * m.J + m.phi * g_v * dg_L);
+    }
+  }
+  if (io.grad_E_syn) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) st.accE[s] += gx * m.phi * Gc[s];
+  }
+  st.dv = m.dv;
+  // Conductances decay into step t+1 and feed the currents of step t.
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    st.lr[s] = st.lr[s] * syn.decay_r[s] + dG[s];
+    st.ld[s] = st.ld[s] * syn.decay_d[s] + dG[s];
+  }
+}
+
+// The spike (and probability) of step t, both functions of v - theta; `carried` is
+// dL/ds_t through the recurrent synapses (0 when gradients do not flow there).
+template <int S>
+__device__ inline void back_spike_step(BackState<S>& st, const BackArgs& P,
+                                       const BackNeuron& c, int64_t b, int64_t n, int64_t t,
+                                       float carried) {
+  const wt_backward_io& io = P.io;
+  const int64_t N = P.tab.N, T = io.T;
+  const int64_t out = (b * T + t) * N + n;
+  const float x = io.v_saved[out] - c.theta;
+  float g_x = surrogate(x, io.grad_spikes[out] + carried, c.k_surr);
+  if (io.grad_prob) {
+    const float p = 1.0f / (1.0f + expf(-(c.k_surr * x)));
+    g_x += io.grad_prob[out] * c.k_surr * p * (1.0f - p);
+  }
+  if (io.held) g_x *= 1.0f - (float)io.held[out];
+  st.dv += g_x;
+  st.acc_theta -= g_x;
+}
+
+// The accumulated partials of one (trial, neuron), written once after step 0.
+template <int S>
+__device__ inline void back_finish(const BackState<S>& st, const BackArgs& P, int64_t b,
+                                   int64_t n) {
+  const wt_tables& tab = P.tab;
+  const wt_backward_io& io = P.io;
+  const int64_t N = tab.N, K = tab.K, B = io.B;
+  const int64_t idx = b * N + n;
+  if (io.grad_scale) {
+#pragma unroll
+    for (int k = 0; k < WT_MAX_K; ++k)
+      if (k < K) io.grad_scale[k * B * N + idx] = st.acc_scale[k];
+  }
+  if (io.grad_theta) io.grad_theta[idx] = st.acc_theta;
+  if (io.grad_reset) io.grad_reset[idx] = st.acc_reset;
+  if (io.grad_E_L) io.grad_E_L[idx] = st.acc_EL;
+  if (io.grad_C_m) io.grad_C_m[idx] = st.acc_Cm;
+  if (io.grad_beta) io.grad_beta[idx] = st.acc_beta;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    if (io.grad_E_syn) io.grad_E_syn[(b * S + s) * N + n] = st.accE[s];
+    if (io.grad_jump) {
+      io.grad_jump[(b * 2 * S + s) * N + n] = st.accJr[s];
+      io.grad_jump[(b * 2 * S + S + s) * N + n] = st.accJd[s];
+    }
+    if (io.grad_decay) {  // the conductances entering the chunk
+      const float gr0 = io.g_init[(b * 2 * S + s) * N + n];
+      const float gd0 = io.g_init[(b * 2 * S + S + s) * N + n];
+      io.grad_decay[(b * 2 * S + s) * N + n] = st.accDr[s] + gr0 * st.Hr[s];
+      io.grad_decay[(b * 2 * S + S + s) * N + n] = st.accDd[s] + gd0 * st.Hd[s];
+    }
+  }
+}
+
+// Recurrent activations as inputs: one thread per (trial, neuron), all steps.
+template <int S>
+__global__ __launch_bounds__(256) void cond_backward_kernel(BackArgs P) {
+  const int64_t N = P.tab.N, B = P.io.B, T = P.io.T;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= B * N) return;
+  const int64_t b = idx / N, n = idx - b * N;
+  Synapses<S> syn;
+  load_synapses<S>(P.tab, syn);
+  const BackNeuron c = back_neuron(P.tab, n);
+  BackState<S> st;
+  state_zero(st);
+  for (int64_t t = T - 1; t >= 0; --t) {
+    back_membrane_step<S>(st, P, syn, c, b, n, t);
+    back_spike_step<S>(st, P, c, b, n, t, 0.0f);
+  }
+  back_finish<S>(st, P, b, n);
+}
+
+// Recurrent path, per step: (1) the membrane part, state in global memory.
+template <int S>
+__global__ __launch_bounds__(256) void rg_membrane_kernel(BackArgs P, int64_t t) {
+  const int64_t N = P.tab.N, B = P.io.B;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= B * N) return;
+  const int64_t b = idx / N, n = idx - b * N;
+  Synapses<S> syn;
+  load_synapses<S>(P.tab, syn);
+  const BackNeuron c = back_neuron(P.tab, n);
+  BackState<S> st;
+  if (t == P.io.T - 1) state_zero(st); else state_io<S>(st, P.state, B * N, idx, false);
+  back_membrane_step<S>(st, P, syn, c, b, n, t);
+  state_io<S>(st, P.state, B * N, idx, true);
+}
+
+// (2) Per (source j, trial b), threads b fastest: R gathered along j's synapses, then
+// the spike term of item (b, j). Only dv and the threshold partial change.
+template <int S>
+__global__ __launch_bounds__(256) void rg_spike_kernel(BackArgs P, int64_t t) {
+  const int64_t N = P.tab.N, B = P.io.B;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= B * N) return;
+  const int64_t j = idx / B, b = idx - j * B;
+  float R = 0.0f;
+  const int32_t k = j < P.rec.n_src ? P.rec.pathway[j] : -1;
+  if (k >= 0 && k < P.tab.K_rec) {
+    const float* g = P.grad_now + (int64_t)k * N * B + b;
+    for (int64_t e = P.rec.indptr[j], e1 = P.rec.indptr[j + 1]; e < e1; ++e)
+      R += P.rec.weights[e] * g[(int64_t)P.rec.targets[e] * B];
+  }
+  BackNeuron c;
+  c.theta = P.tab.theta[j];
+  c.k_surr = *P.tab.surr;
+  const int64_t BN = B * N, item = b * N + j;
+  BackState<S> st;
+  st.dv = P.state[item];
+  st.acc_theta = P.state[(int64_t)(back_fields<S>() - 5) * BN + item];
+  back_spike_step<S>(st, P, c, b, j, t, R);
+  P.state[item] = st.dv;
+  P.state[(int64_t)(back_fields<S>() - 5) * BN + item] = st.acc_theta;
+}
+
+// After step 0: the partials from the global state.
+template <int S>
+__global__ __launch_bounds__(256) void rg_finish_kernel(BackArgs P) {
+  const int64_t N = P.tab.N, B = P.io.B;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= B * N) return;
+  BackState<S> st;
+  state_io<S>(st, P.state, B * N, idx, false);
+  back_finish<S>(st, P, idx / N, idx % N);
+}
+
+template <int S>
+struct BackLaunch {
+  static hipError_t run(BackArgs& a, hipStream_t stream);
+  static hipError_t recurrent(BackArgs& a, hipStream_t stream);
+};
+
+template <int S>
+hipError_t BackLaunch<S>::run(BackArgs& a, hipStream_t stream) {
+  const int64_t total = a.io.B * a.tab.N;
+  const int block = 256;
+  hipLaunchKernelGGL(cond_backward_kernel<S>, dim3((unsigned)((total + block - 1) / block)),
+                     dim3(block), 0, stream, a);
+  return hipGetLastError();
+}
+
+template <int S>
+hipError_t BackLaunch<S>::recurrent(BackArgs& a, hipStream_t stream) {
+  const int64_t total = a.io.B * a.tab.N;
+  const int block = 256;
+  const dim3 grid((unsigned)((total + block - 1) / block));
+  for (int64_t t = a.io.T - 1; t >= 0; --t) {
+    hipLaunchKernelGGL(rg_membrane_kernel<S>, grid, dim3(block), 0, stream, a, t);
+    hipLaunchKernelGGL(rg_spike_kernel<S>, grid, dim3(block), 0, stream, a, t);
+  }
+  hipLaunchKernelGGL(rg_finish_kernel<S>, grid, dim3(block), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace wt

@@ -31,6 +31,7 @@
 #include "../../include/wiretorch_amd.h"
 #include "wt_math.h"
 
+#include "wt_back.h"
 #include "wt_run.h"
 
 namespace wt {
@@ -79,154 +80,6 @@ __global__ void split_ranges_kernel(const int64_t* indptr, const int32_t* target
 }
 
 // ---------------------------------------------------------------------------------
-// Backward: one thread per (trial, neuron), steps t = T-1 .. 0.
-struct BackArgs {
-  wt_tables tab;
-  wt_backward_io io;
-};
-
-template <int S>
-__global__ __launch_bounds__(256) void cond_backward_kernel(BackArgs P) {
-  const wt_tables& tab = P.tab;
-  const wt_backward_io& io = P.io;
-  const int64_t N = tab.N, K = tab.K, B = io.B, T = io.T;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= B * N) return;
-  const int64_t b = idx / N, n = idx - b * N;
-  const float dt = *tab.dt, k_surr = *tab.surr;
-  Synapses<S> syn;
-  load_synapses<S>(tab, syn);
-  const float theta = tab.theta[n], E_L = tab.E_L[n], C_m = tab.C_m[n], beta = tab.beta[n];
-  const Leak lk = leak(C_m, beta, dt);
-  const bool refractory = io.held != nullptr;
-  const bool want_A = io.grad_A != nullptr, want_scale = io.grad_scale != nullptr;
-  const bool want_decay = io.grad_decay != nullptr, want_jump = io.grad_jump != nullptr;
-  const bool want_E = io.grad_E_syn != nullptr;
-
-  float dv = 0.0f;
-  float lr[S], ld[S], Hr[S], Hd[S], accE[S], accDr[S], accDd[S], accJr[S], accJd[S];
-#pragma unroll
-  for (int s = 0; s < S; ++s) {
-    lr[s] = ld[s] = Hr[s] = Hd[s] = accE[s] = accDr[s] = accDd[s] = accJr[s] = accJd[s] = 0.0f;
-  }
-  float acc_scale[WT_MAX_K];
-  for (int k = 0; k < WT_MAX_K; ++k) acc_scale[k] = 0.0f;
-  float acc_theta = 0.0f, acc_reset = 0.0f, acc_EL = 0.0f, acc_Cm = 0.0f, acc_beta = 0.0f;
-
-  for (int64_t t = T - 1; t >= 0; --t) {
-    const int64_t out = (b * T + t) * N + n;
-    const float v = io.v_saved[out];
-    const float s_sp = io.spikes[out];
-    const float held = refractory ? (float)io.held[out] : 0.0f;
-    const float r = refractory ? fmaxf(s_sp, held) : s_sp;
-    float G[S];
-#pragma unroll
-    for (int s = 0; s < S; ++s) G[s] = io.G_saved[out * S + s];
-
-    // Injections of step t: per unit jump, sum_k a_k scale_k made_k (jump, decay).
-    if (want_decay || want_jump) {
-      float base[S];
-#pragma unroll
-      for (int s = 0; s < S; ++s) base[s] = 0.0f;
-      for (int64_t k = 0; k < K; ++k) {
-        const float as = io.A[((k * B + b) * T + t) * N + n] * tab.scale[k * N + n];
-#pragma unroll
-        for (int s = 0; s < S; ++s) base[s] += as * tab.made[k * S + s];
-      }
-#pragma unroll
-      for (int s = 0; s < S; ++s) {
-        if (want_jump) {
-          accJr[s] += lr[s] * base[s];
-          accJd[s] += ld[s] * base[s];
-        }
-        if (want_decay) {
-          accDr[s] += syn.jump_r[s] * base[s] * Hr[s];
-          accDd[s] += syn.jump_d[s] * base[s] * Hd[s];
-          Hr[s] = lr[s] + syn.decay_r[s] * Hr[s];
-          Hd[s] = ld[s] + syn.decay_d[s] * Hd[s];
-        }
-      }
-    }
-    // dL/da_k of step t: the adjoint of the conductances it was injected into.
-#pragma unroll
-    for (int k = 0; k < WT_MAX_K; ++k) {
-      if (k >= K) break;
-      float qk = 0.0f;
-#pragma unroll
-      for (int s = 0; s < S; ++s)
-        qk += (syn.jump_r[s] * lr[s] + syn.jump_d[s] * ld[s]) * tab.made[k * S + s];
-      const int64_t ka = ((k * B + b) * T + t) * N + n;
-      if (want_A) io.grad_A[ka] = qk * tab.scale[k * N + n];
-      if (want_scale) acc_scale[k] += qk * io.A[ka];
-    }
-    // Membrane.
-    const float gx = dv * (1.0f - r);
-    float dG[S], Gc[S];
-    const MembraneAdjoint m = membrane_adjoint<S>(gx, v, G, syn, E_L, C_m, lk, dt, dG, Gc);
-    acc_reset += dv * r;
-    acc_EL += gx * m.phi * lk.g_L;
-    if (io.grad_C_m || io.grad_beta) {
-      const float g_v = v - E_L;
-      if (io.grad_C_m) {  // g_L = C rate and a both depend on C
-        const float inv_C = 1.0f / C_m;
-        const float dphi = -(m.a * dt * m.Gt * inv_C * inv_C + m.phi * lk.g_L * inv_C) * m.inv_g;
-        acc_Cm -= gx * (dphi * m.J + m.phi * g_v * lk.g_L * inv_C);
-      }
-      if (io.grad_beta) {  // rate = -log(beta) / dt
-        const float dg_L = -C_m / (beta * dt);
-        const float dphi = -(m.a / beta + m.phi * dg_L) * m.inv_g;
-        acc_beta -= gx * (dphi * m.J + m.phi * g_v * dg_L);
-      }
-    }
-    if (want_E) {
-#pragma unroll
-      for (int s = 0; s < S; ++s) accE[s] += gx * m.phi * Gc[s];
-    }
-    dv = m.dv;
-    // Spike (and probability) of step t, both functions of v - theta.
-    const float x = v - theta;
-    float g_x = surrogate(x, io.grad_spikes[out], k_surr);
-    if (io.grad_prob) {
-      const float p = 1.0f / (1.0f + expf(-(k_surr * x)));
-      g_x += io.grad_prob[out] * k_surr * p * (1.0f - p);
-    }
-    if (refractory) g_x *= 1.0f - held;
-    dv += g_x;
-    acc_theta -= g_x;
-    // Conductances decay into step t+1 and feed the currents of step t.
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      lr[s] = lr[s] * syn.decay_r[s] + dG[s];
-      ld[s] = ld[s] * syn.decay_d[s] + dG[s];
-    }
-  }
-  if (want_scale) {
-#pragma unroll
-    for (int k = 0; k < WT_MAX_K; ++k)
-      if (k < K) io.grad_scale[k * B * N + idx] = acc_scale[k];
-  }
-  if (io.grad_theta) io.grad_theta[idx] = acc_theta;
-  if (io.grad_reset) io.grad_reset[idx] = acc_reset;
-  if (io.grad_E_L) io.grad_E_L[idx] = acc_EL;
-  if (io.grad_C_m) io.grad_C_m[idx] = acc_Cm;
-  if (io.grad_beta) io.grad_beta[idx] = acc_beta;
-#pragma unroll
-  for (int s = 0; s < S; ++s) {
-    if (want_E) io.grad_E_syn[(b * S + s) * N + n] = accE[s];
-    if (want_jump) {
-      io.grad_jump[(b * 2 * S + s) * N + n] = accJr[s];
-      io.grad_jump[(b * 2 * S + S + s) * N + n] = accJd[s];
-    }
-    if (want_decay) {  // the conductances entering the chunk
-      const float gr0 = io.g_init[(b * 2 * S + s) * N + n];
-      const float gd0 = io.g_init[(b * 2 * S + S + s) * N + n];
-      io.grad_decay[(b * 2 * S + s) * N + n] = accDr[s] + gr0 * Hr[s];
-      io.grad_decay[(b * 2 * S + S + s) * N + n] = accDd[s] + gd0 * Hd[s];
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------------
 // Weight gradient on the support: one thread per synapse; it walks its source's
 // events (the (trial, step) where the source was active, ascending) and sums the
 // target's dL/da of that step.
@@ -269,6 +122,26 @@ extern template struct wt::RunLaunch<5>;
 extern template struct wt::RunLaunch<6>;
 extern template struct wt::RunLaunch<7>;
 extern template struct wt::RunLaunch<8>;
+extern template struct wt::BackLaunch<1>;
+extern template struct wt::BackLaunch<2>;
+extern template struct wt::BackLaunch<3>;
+extern template struct wt::BackLaunch<4>;
+extern template struct wt::BackLaunch<5>;
+extern template struct wt::BackLaunch<6>;
+extern template struct wt::BackLaunch<7>;
+extern template struct wt::BackLaunch<8>;
+
+// The two backward drivers as dispatch targets.
+template <int S>
+struct BackRun {
+  static hipError_t run(BackArgs& a, hipStream_t stream) { return BackLaunch<S>::run(a, stream); }
+};
+template <int S>
+struct BackRecurrent {
+  static hipError_t run(BackArgs& a, hipStream_t stream) {
+    return BackLaunch<S>::recurrent(a, stream);
+  }
+};
 
 template <template <int> class F, typename... Args>
 static hipError_t dispatch_S(int64_t S, Args&&... args) {
@@ -410,17 +283,6 @@ extern "C" int wt_split_ranges(const int64_t* indptr, const int32_t* targets, in
   return hipGetLastError();
 }
 
-template <int S>
-struct BackLaunch {
-  static hipError_t run(BackArgs& a, hipStream_t stream) {
-    const int64_t total = a.io.B * a.tab.N;
-    const int block = 256;
-    hipLaunchKernelGGL(cond_backward_kernel<S>, dim3((unsigned)((total + block - 1) / block)),
-                       dim3(block), 0, stream, a);
-    return hipGetLastError();
-  }
-};
-
 extern "C" int wt_cond_scan_backward(const wt_tables* tab, const wt_backward_io* io,
                                      wt_stream_t stream) {
   if (!tab || !io || !io->grad_spikes || !io->spikes || !io->v_saved || !io->G_saved)
@@ -430,10 +292,43 @@ extern "C" int wt_cond_scan_backward(const wt_tables* tab, const wt_backward_io*
   if ((io->grad_decay || io->grad_jump || io->grad_scale) && !io->A) return hipErrorInvalidValue;
   if (io->grad_decay && !io->g_init) return hipErrorInvalidValue;
   if (io->B * tab->N == 0 || io->T == 0) return hipSuccess;
-  BackArgs a;
+  BackArgs a = {};
   a.tab = *tab;
   a.io = *io;
-  return dispatch_S<BackLaunch>(tab->S, a, (hipStream_t)stream);
+  return dispatch_S<BackRun>(tab->S, a, (hipStream_t)stream);
+}
+
+static int64_t back_fields_of(int64_t S) { return 1 + 9 * S + WT_MAX_K + 5; }
+
+extern "C" int64_t wt_cond_recurrent_backward_scratch_bytes(int64_t S, int64_t K_rec, int64_t B,
+                                                            int64_t N) {
+  const int64_t state = (back_fields_of(S) * B * N * 4 + 255) / 256 * 256;
+  return state + K_rec * N * B * 4;
+}
+
+extern "C" int wt_cond_recurrent_backward(const wt_tables* tab, const wt_side* rec,
+                                          const wt_backward_io* io, void* scratch,
+                                          wt_stream_t stream) {
+  if (!tab || !rec || !io || !scratch || !io->grad_spikes || !io->spikes || !io->v_saved ||
+      !io->G_saved)
+    return hipErrorInvalidValue;
+  if (tab->S < 1 || tab->S > WT_MAX_S || tab->K < 0 || tab->K > WT_MAX_K ||
+      tab->K_rec < 1 || tab->K_rec > tab->K)
+    return hipErrorInvalidValue;
+  if ((io->grad_decay || io->grad_jump || io->grad_scale) && !io->A) return hipErrorInvalidValue;
+  if (io->grad_decay && !io->g_init) return hipErrorInvalidValue;
+  if (rec->n_src != tab->N) return hipErrorInvalidValue;
+  if (io->B * tab->N == 0 || io->T == 0) return hipSuccess;
+  if (!rec->indptr || !rec->pathway) return hipErrorInvalidValue;
+  BackArgs a = {};
+  a.tab = *tab;
+  a.io = *io;
+  a.rec = *rec;
+  a.state = static_cast<float*>(scratch);
+  a.grad_now = reinterpret_cast<float*>(
+      static_cast<char*>(scratch) +
+      (back_fields_of(tab->S) * io->B * tab->N * 4 + 255) / 256 * 256);
+  return dispatch_S<BackRecurrent>(tab->S, a, (hipStream_t)stream);
 }
 
 extern "C" int wt_edge_sources(const int64_t* indptr, int64_t n_src, int64_t* edge_src,

@@ -1,4 +1,6 @@
-// The persistent forward kernel for S = 6 synapse types (see wt_run.h).
+// The persistent forward kernel and the backward for S = 6 synapse types (see wt_run.h).
+#include "wt_back.h"
 #include "wt_run.h"
 
 template struct wt::RunLaunch<6>;
+template struct wt::BackLaunch<6>;

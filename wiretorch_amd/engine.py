@@ -15,13 +15,14 @@ What differs from the reference is underneath:
 * connectivity is compressed by source (``connectome.Connectome``); dense pathways are
   converted once (cached while their tensors are unchanged);
 * gradients (``_Run``, the counterpart of ``_FeedforwardScan`` / ``_RecurrentRun``,
-  ``conductance/engine.py:444-544``) come from ``wt_cond_scan_backward`` and the
-  event-driven ``wt_weight_gradient``.
+  ``conductance/engine.py:444-544``) come from ``wt_cond_scan_backward`` — or, when the
+  drive asks for gradients through the recurrent spikes (``recurrent_gradients``),
+  ``wt_cond_recurrent_backward`` — and the event-driven ``wt_weight_gradient``.
 
 The engine runs only on a GPU with the library built; it raises otherwise. Not
 supported (raising ``NotImplementedError``): per-step gradient retention
-(``retain``), gradients through the recurrent spikes (``recurrent_gradients``),
-float16 storage, sampled spikes, presynaptic dynamics, Mg block, adaptation.
+(``retain``), float16 storage, sampled spikes, presynaptic dynamics, Mg block,
+adaptation.
 """
 
 from __future__ import annotations
@@ -169,7 +170,7 @@ def _from_pathways(pathways, n_src: int, N: int, device) -> _Side:
 
 
 _CACHE: OrderedDict = OrderedDict()
-_CACHE_SIZE = 8
+_CACHE_SIZE = 32
 
 
 def _side_of(pathways, sparse, n_src: int, N: int, device) -> _Side:
@@ -267,6 +268,26 @@ def _type_table(tables: dict, scale: torch.Tensor, device):
     return types.contiguous(), type_of.to(torch.int32).contiguous()
 
 
+def _key(*tensors) -> tuple:
+    """Identity of tensors' current contents: address, version and shape."""
+    return tuple((t.data_ptr(), t._version, tuple(t.shape), t.dtype) if t is not None else None
+                 for t in tensors)
+
+
+def _cached(key: tuple, keep: tuple, make):
+    """``make()``, cached under ``key`` while the tensors in ``keep`` are unchanged
+    (holding them keeps their addresses from being reused)."""
+    hit = _CACHE.get(key)
+    if hit is not None:
+        _CACHE.move_to_end(key)
+        return hit[0]
+    value = make()
+    _CACHE[key] = (value, keep)
+    while len(_CACHE) > _CACHE_SIZE:
+        _CACHE.popitem(last=False)
+    return value
+
+
 def _f32(t: torch.Tensor, device) -> torch.Tensor:
     return t.detach().to(device=device, dtype=torch.float32).contiguous()
 
@@ -293,6 +314,8 @@ class _Plan:
     track_b: int
     stream: int
     device: torch.device
+    #: gradients flow back through the recurrent spikes (set by ``simulate``)
+    recurrent_gradients: bool = False
 
     @property
     def K(self) -> int:
@@ -333,15 +356,25 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
     groups, R, range_n = geometry(B, N, K_rec + K_ff, n_cu, max_lds)
     bound = rec.max_in_sum
     if ff.n_src and ff.conn.n_edges:
-        bound += ff.max_in_sum * float(x.detach().abs().max())
-    tables = {name: _f32(getattr(p, name), device) for name in
-              ("theta", "U_reset", "E_L", "C_m", "beta", "E_syn", "g_clip", "decay", "jump")}
-    tables["made"] = drive.made.to(device=device, dtype=torch.float32).contiguous()
-    tables["dt"] = _f32(p.dt, device)
-    tables["surr"] = _f32(p.surr_scale, device)
-    tables["n_ref"] = (None if p.n_ref is None
-                       else p.n_ref.to(device=device, dtype=torch.int32).contiguous())
-    tables["types"], tables["type_of"] = _type_table(tables, drive.scale, device)
+        xd = x.detach()
+        x_max = _cached(("x_max",) + _key(xd), (xd,), lambda: float(xd.abs().max()))
+        bound += ff.max_in_sum * x_max
+    names = ("theta", "U_reset", "E_L", "C_m", "beta", "E_syn", "g_clip", "decay", "jump")
+    sources = tuple(getattr(p, name) for name in names) + (
+        drive.made, drive.scale, p.dt, p.surr_scale, p.n_ref)
+
+    def make_tables():
+        tables = {name: _f32(getattr(p, name), device) for name in names}
+        tables["made"] = drive.made.to(device=device, dtype=torch.float32).contiguous()
+        tables["dt"] = _f32(p.dt, device)
+        tables["surr"] = _f32(p.surr_scale, device)
+        tables["n_ref"] = (None if p.n_ref is None
+                           else p.n_ref.to(device=device, dtype=torch.int32).contiguous())
+        tables["types"], tables["type_of"] = _type_table(tables, drive.scale, device)
+        return tables
+
+    # the tables (and the distinct-row search) are rebuilt only when a source changes
+    tables = _cached(("tables", str(device)) + _key(*sources), sources, make_tables)
     return _Plan(
         B=B, T=T, N=N, S=S, K_rec=K_rec, K_ff=K_ff, n_in=n_in, tables=tables, rec=rec,
         ff=ff, geo=(groups, R, range_n), frac_bits=_frac_bits(bound),
@@ -448,8 +481,18 @@ class _Run(torch.autograd.Function):
             g_init.data_ptr() if g_init.numel() else None, B, T,
             _lib.ptr(grad_A), _lib.ptr(partial), *[_lib.ptr(t) for t in phys],
         )  # fmt: skip
-        _lib.check(_lib.load().wt_cond_scan_backward(L.abi_tables(scale.detach().float().contiguous()),
-                                                     io, L.stream), "wt_cond_scan_backward")
+        tab = L.abi_tables(scale.detach().float().contiguous())
+        lib = _lib.load()
+        if L.recurrent_gradients:  # through the recurrent spikes: per-step coupling
+            groups, R, range_n = L.geo
+            rec_w = _sparse_weights(L, weights, n_rec_w)[0]
+            rec = L.rec.abi(R, range_n, L.stream, rec_w)
+            scratch = torch.empty(int(lib.wt_cond_recurrent_backward_scratch_bytes(S, L.K_rec, B, N)),
+                                  dtype=torch.uint8, device=dev)
+            _lib.check(lib.wt_cond_recurrent_backward(tab, rec, io, scratch.data_ptr(), L.stream),
+                       "wt_cond_recurrent_backward")
+        else:
+            _lib.check(lib.wt_cond_scan_backward(tab, io, L.stream), "wt_cond_scan_backward")
         grad_scale = partial.sum(dim=1) if want_scale else None
         dims = [0] * 5 + [(0, 2), (0, 3), (0, 3)]
         grad_phys = [t.sum(d) if t is not None else None for t, d in zip(phys, dims)]
@@ -591,8 +634,7 @@ def simulate(
         or any(W.requires_grad for W in rec_w + ff_w)
         or any(t.requires_grad for t in physiology)
     )  # fmt: skip
-    if grad and drive.recurrent_gradients and L.K_rec:
-        raise NotImplementedError("gradients through the recurrent spikes (recurrent_gradients)")
+    L.recurrent_gradients = bool(drive.recurrent_gradients and L.K_rec and L.rec.n_src)
     if grad:
         spikes, prob, v, g_state, counter = _Run.apply(
             L, len(rec_w), drive.scale, x, v, g_state, counter, *rec_w, *ff_w, *physiology
