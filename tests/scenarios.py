@@ -1,9 +1,10 @@
 """The reference's seeded fixture networks, rebuilt through this package's API.
 
-Restates the conductance-based builders of the reference's ``tests/networks.py``
+Restates the conductance-based and rate builders of the reference's ``tests/networks.py``
 (physiology ``:57-98``, random structure ``:105-213``, ``recurrent`` ``:276-355``,
-``feedforward`` ``:358-429``, scenarios ``:885-957``, ``fingerprint`` ``:963-970``,
-``loss_readout`` ``:973-976``) and the drive/readout code of ``tests/harness.py:11-111``.
+``feedforward`` ``:358-429``, rate networks ``:735-880``, scenarios ``:885-957``,
+``fingerprint`` ``:963-970``, ``loss_readout`` ``:973-976``) and the drive/readout code
+of ``tests/harness.py:11-111``.
 The numpy random streams are consumed in the same order, so a rebuilt network's
 SHA-256 fingerprint equals the one its fixture records (``meta["fingerprint"]``); every
 fixture test checks that first.
@@ -27,6 +28,7 @@ from wiretorch_amd.projections import (
     ScalingFactorProjection,
     make_frozen_projections,
 )
+from wiretorch_amd.rate import FeedforwardRateNetwork, RecurrentRateNetwork
 
 FIXTURES = Path(__file__).parent / "golden" / "reference"
 DT = 1.0
@@ -126,6 +128,7 @@ class Built:
     model: torch.nn.Module
     input_spikes: np.ndarray
     structure: dict
+    output: str = "spikes"  # what the model outputs per step: "spikes" or "rates"
 
 
 @dataclass(frozen=True)
@@ -134,6 +137,7 @@ class Scenario:
     build: Callable[[int], Built]
     state_keys: tuple[str, ...] = ()
     returns_probabilities: bool = False
+    rates: bool = False
 
 
 def _structure(seed, n=N, n_ff=N_FF):
@@ -223,6 +227,105 @@ def feedforward(batch_size, seed, learnt_weights=False, probabilities=False, n=N
     return Built(model, inputs, dict(types=types, weights=weights, **drawn))
 
 
+# Rate networks (reference ``tests/networks.py:735-880``): each cell type has its own
+# nonlinearity; excitation makes a fast and a slow synapse type, inhibition an
+# instantaneous one. The input is white noise.
+RATE_CELLS = [
+    dict(name="excitatory", cell_id=E, tau_mem=10.0, nonlinearity="softplus",
+         theta=0.5, gain=1.0),
+    dict(name="inhibitory", cell_id=I, tau_mem=5.0, nonlinearity="relu",
+         theta=0.0, gain=2.0),
+]  # fmt: skip
+RATE_SYNAPSES = [
+    dict(name="fast", synapse_id=0, cell_id=E, tau_syn=5.0, type="excitatory"),
+    dict(name="slow", synapse_id=1, cell_id=E, tau_syn=50.0, type="excitatory"),
+    dict(name="inh", synapse_id=2, cell_id=I, tau_syn=0.0, type="inhibitory"),
+]
+RATE_INPUT_CELLS = [dict(name="input", cell_id=0)]
+RATE_INPUT_SYNAPSES = [
+    dict(name="fast", synapse_id=0, cell_id=0, tau_syn=2.0, type="excitatory")
+]
+RATE_WEIGHTS = {E: 0.05, I: 0.15, "input": 0.05}
+RATE_INPUT = (1.0, 1.0)
+RATE_LEARN = {"tau_mem": True, "theta": ["excitatory"], "gain": True, "tau_syn": ["slow"]}
+
+
+def white_noise(rng, batch, n_steps, n_inputs, mean=RATE_INPUT[0], std=RATE_INPUT[1]):
+    return (mean + std * rng.standard_normal((batch, n_steps, n_inputs))).astype(np.float32)
+
+
+def rate_recurrent(batch_size, seed, learn=None, n=N, n_ff=N_FF, n_steps=200, input_seed=0,
+                   learnt_excitatory=False, storage_dtype=torch.float32):
+    """``RecurrentRateNetwork`` with perturbed scaling factors; with ``learn`` also that
+    physiology and full-rank input weights (reference ``tests/networks.py:767-828``)."""
+    rng = np.random.default_rng([seed, 3])
+    types = cell_types(rng, n)
+    p_conn = {E: 0.15, I: 0.3}
+    w_rec = np.concatenate(
+        [sparse_lognormal(rng, 1, n, p_conn[t] * (N / n), RATE_WEIGHTS[t]) for t in types]
+    )
+    w_ff = sparse_lognormal(rng, n_ff, n, 0.3 * (N_FF / n_ff), RATE_WEIGHTS["input"])
+    ff_types = np.zeros(n_ff, dtype=np.int64)
+    rec = {
+        (src, tgt): FullRankProjection(b, mask=b != 0)
+        if learnt_excitatory and src == "excitatory"
+        else ScalingFactorProjection(b)
+        for (src, tgt), b in per_type_blocks(w_rec, types, types, REC_NAMES, REC_NAMES).items()
+    }
+    ff = {}
+    for key, block in per_type_blocks(w_ff, ff_types, types, ["input"], REC_NAMES).items():
+        if learn:
+            init = block * rng.lognormal(0.0, 0.2, block.shape)
+            ff[key] = FullRankProjection(init, mask=block != 0)
+        else:
+            ff[key] = ScalingFactorProjection(block)
+    model = RecurrentRateNetwork(
+        dt=DT, rec_projections=rec, ff_projections=ff, cell_type_indices=types,
+        cell_type_indices_FF=ff_types, cell_params=RATE_CELLS,
+        cell_params_FF=RATE_INPUT_CELLS, synapse_params=RATE_SYNAPSES,
+        synapse_params_FF=RATE_INPUT_SYNAPSES, batch_size=batch_size, learn=learn,
+        storage_dtype=storage_dtype,
+    )  # fmt: skip
+    scaled = [p for p in (*rec.values(), *ff.values()) if hasattr(p, "log_sf")]
+    sfs = move_scaling_factors(np.random.default_rng([seed, 4]), scaled)
+    inputs = white_noise(_input_rng(seed, input_seed), batch_size, n_steps, n_ff)
+    structure = dict(types=types, w_rec=w_rec, w_ff=w_ff, sf=sfs)
+    return Built(model, inputs, structure, output="rates")
+
+
+def rate_feedforward(batch_size, seed, n=N, n_ff=N_FF, n_steps=200, input_seed=0):
+    """``FeedforwardRateNetwork``: rows are white-noise inputs, then a ``rate_recurrent``
+    network's neurons (reference ``tests/networks.py:831-877``)."""
+    source = rate_recurrent(batch_size, seed, n=n, n_ff=n_ff)
+    types, w_rec, w_ff = (source.structure[k] for k in ("types", "w_rec", "w_ff"))
+    cells = RATE_INPUT_CELLS + [dict(name=c["name"], cell_id=c["cell_id"] + 1) for c in RATE_CELLS]
+    synapses = RATE_INPUT_SYNAPSES + [
+        {**s, "cell_id": s["cell_id"] + 1, "synapse_id": s["synapse_id"] + 1}
+        for s in RATE_SYNAPSES
+    ]
+    row_types = np.concatenate([np.zeros(n_ff, dtype=np.int64), types + 1])
+    blocks = per_type_blocks(np.concatenate([w_ff, w_rec]), row_types, types,
+                             [c["name"] for c in cells], REC_NAMES)
+    projections = {k: ScalingFactorProjection(b) for k, b in blocks.items()}
+    model = FeedforwardRateNetwork(
+        dt=DT, projections=projections, cell_type_indices=types,
+        cell_type_indices_FF=row_types, cell_params=RATE_CELLS, cell_params_FF=cells,
+        synapse_params_FF=synapses, batch_size=batch_size,
+        learn={"theta": True, "tau_syn": ["slow"]},
+    )  # fmt: skip
+    sfs = move_scaling_factors(np.random.default_rng([seed, 5]), list(projections.values()))
+    rng = _input_rng(seed, input_seed)
+    inputs = np.concatenate(
+        [
+            white_noise(rng, batch_size, n_steps, n_ff),
+            white_noise(rng, batch_size, n_steps, n, mean=1.0, std=0.5).clip(0),
+        ],
+        axis=2,
+    )
+    structure = dict(types=types, w_rec=w_rec, w_ff=w_ff, sf=sfs)
+    return Built(model, inputs, structure, output="rates")
+
+
 SCENARIOS = {
     s.name: s
     for s in [
@@ -235,6 +338,18 @@ SCENARIOS = {
         Scenario("feedforward_probabilities",
                  lambda b: feedforward(b, SEED, probabilities=True), ("v", "g_FF"),
                  returns_probabilities=True),
+    ]
+}  # fmt: skip
+#: The rate scenarios (reference ``tests/networks.py:915-932``), kept apart: the spiking
+#: tests iterate over ``SCENARIOS``.
+RATE_SCENARIOS = {
+    s.name: s
+    for s in [
+        Scenario("rate_recurrent", lambda b: rate_recurrent(b, SEED), ("v", "I_syn"), rates=True),
+        Scenario("rate_recurrent_learnt", lambda b: rate_recurrent(b, SEED, learn=RATE_LEARN),
+                 ("v", "I_syn"), rates=True),
+        Scenario("rate_feedforward", lambda b: rate_feedforward(b, SEED), ("v", "I_syn"),
+                 rates=True),
     ]
 }  # fmt: skip
 
@@ -270,13 +385,13 @@ def load_fixture(name: str):
     return arrays, meta
 
 
-def unpack_output(out) -> dict:
+def unpack_output(out, output: str = "spikes") -> dict:
     if isinstance(out, torch.Tensor):
-        return {"spikes": out}
+        return {output: out}
     if isinstance(out, tuple):
         probabilities, spikes = out
         return {"spikes": spikes, "probabilities": probabilities}
-    keep = ("spikes", "voltages", "probabilities")
+    keep = ("spikes", "rates", "voltages", "probabilities")
     return {k: out[k] for k in keep if k in out}
 
 
@@ -296,12 +411,13 @@ def free_run(scenario: Scenario, built: Built, device="cpu") -> dict:
         for start in range(0, x.shape[1], WINDOW):
             for key, value in model.get_checkpoint_state().items():
                 states[key].append(np.array(value))
-            out = unpack_output(model(x[:, start : start + WINDOW]))
+            out = unpack_output(model(x[:, start : start + WINDOW]), built.output)
             chunks.append({k: v.cpu().numpy() for k, v in out.items()})
         for key, value in model.get_checkpoint_state().items():
             states[key].append(np.array(value))
     record = {k: np.concatenate([c[k] for c in chunks], axis=1) for k in chunks[0]}
-    record["spikes"] = record["spikes"] > 0.5
+    if "spikes" in record:
+        record["spikes"] = record["spikes"] > 0.5
     record.update({f"state.{k}": np.stack(v) for k, v in states.items()})
     return record
 
@@ -322,7 +438,7 @@ def gradients(built: Built, device="cpu", track=False, steps=GRAD_STEPS):
     if track:
         model.track_batch_idx = 0
     x = torch.from_numpy(built.input_spikes[:, :steps]).to(device)
-    loss = readout_loss(unpack_output(model(x)))
+    loss = readout_loss(unpack_output(model(x), built.output))
     loss.backward()
     grads = {
         name: p.grad.detach().cpu().numpy()

@@ -244,19 +244,21 @@ def _unsupported(cell_params, synapse_lists, stp) -> None:
 # =====================================================================
 
 
-class ConductanceNetwork(nn.Module):
-    """Base of the conductance-based LIF networks (``network.py:354-1026`` and
-    ``conductance/network.py:44-255`` for the mechanisms this build supports).
+class ProjectionNetwork(nn.Module):
+    """What every network family shares (``network.py:354-1026``): input sides of
+    projections organised into pathways, the per-call ``Drive``, and the state ``v``
+    ``(B, N)`` plus the family's synaptic state, continued from one ``forward`` call to
+    the next until ``reset_state``.
 
-    State ``v`` ``(B, N)``, conductances ``(B, N, 2, S)`` (stored ``(B, 2, S, N)``) and
-    refractory counters ``(B, N)`` int32 continue from one ``forward`` call to the next
-    until ``reset_state``.
+    A family supplies its physiology through ``_register_physiology``,
+    ``_set_timestep``, ``_physiology`` and ``_initial_state``, its engine as
+    ``_engine``, and optionally extra engine arguments and state (``_engine_kwargs``,
+    ``_extra_state``).
     """
 
-    state_name = "g"
-    output_name = "s"
+    state_name = "syn"
+    output_name = "output"
     recurrent_gradients = False
-    has_refractory = True
 
     def __init__(
         self,
@@ -266,9 +268,7 @@ class ConductanceNetwork(nn.Module):
         cell_type_indices: np.ndarray,
         sides: list[InputSide],
         unify_synapses: bool,
-        surrgrad_scale: float,
         batch_size: int,
-        spike_mode: str,
         track_variables: bool,
         track_gradients: bool,
         track_batch_idx: int | None,
@@ -276,12 +276,8 @@ class ConductanceNetwork(nn.Module):
         learn: dict | None = None,
     ):
         super().__init__()
-        assert isinstance(surrgrad_scale, (int, float)) and surrgrad_scale > 0
         validate(dt, cell_params, cell_type_indices, sides)
-        if spike_mode != "deterministic":
-            raise NotImplementedError("only spike_mode='deterministic' is supported")
         self.learn = dict(learn or {})
-        self.spike_mode = spike_mode
         self.batch_size = batch_size
         self.track_variables = track_variables
         self.track_gradients = track_gradients
@@ -301,7 +297,7 @@ class ConductanceNetwork(nn.Module):
             modules = {f"{s}__{t}": p for (s, t), p in side.projections.items()}
             setattr(self, side.attribute, nn.ModuleDict(modules))
             self.register_buffer(side.mask_buffer, torch.from_numpy(self._mask(side)))
-        self._register_physiology(surrgrad_scale)
+        self._register_physiology()
         self.pathways = self._build_pathways()
         self.set_timestep(float(dt))
 
@@ -341,73 +337,6 @@ class ConductanceNetwork(nn.Module):
         for cell in self.cell_params:
             lookup[cell["cell_id"]] = cell[name] if default is None else cell.get(name, default)
         return torch.from_numpy(lookup[self.cell_type_indices.cpu().numpy()])
-
-    def _register_physiology(self, surrgrad_scale: float) -> None:
-        for name in NEURON_PARAMETERS:
-            self.register_buffer(name, self._per_neuron(name))
-        self.register_buffer("C_m", self.tau_mem * self.g_L)
-        for name in SYNAPSE_PARAMETERS:
-            self.register_buffer(name, self.registry.table(name))
-        self.register_buffer("g_clip", self.registry.table("g_clip", default=float("inf")))
-        tau_ref = self._per_neuron("tau_ref", 0.0)
-        assert bool((tau_ref >= 0).all()), "cell_params: tau_ref must be >= 0"
-        self.register_buffer("tau_ref", tau_ref, persistent=False)
-        self.register_buffer(
-            "surrgrad_scale", torch.tensor(float(surrgrad_scale), dtype=torch.float32)
-        )
-        self._register_learnt()
-
-    def _register_learnt(self) -> None:
-        learn = self.learn
-        unknown = set(learn) - set(LEARNABLE) - set(LEARNABLE_SYNAPSE)
-        assert not unknown, f"learn: unknown parameters {sorted(unknown)}"
-        cells = sorted(self.cell_params, key=lambda c: c["cell_id"])
-        names = [c["name"] for c in cells]
-        learnt = {
-            name: learnt_types(learn[name], names, f"learn[{name!r}]")
-            for name in LEARNABLE
-            if learn.get(name)
-        }
-        if learnt:
-            values = {name: [c[name] for c in cells] for name in learnt}
-            self.cell_parameters = TypeParameters(
-                values, learnt=learnt, positive=POSITIVE & set(learnt)
-            )
-            for name, types in learnt.items():
-                mask = torch.isin(self.cell_type_indices, torch.tensor(types))
-                self.register_buffer(f"_learnt_{name}", mask, persistent=False)
-        synapses = self.registry.synapses
-        learnt = {
-            name: learnt_synapses(learn[name], synapses, f"learn[{name!r}]")
-            for name in LEARNABLE_SYNAPSE
-            if learn.get(name)
-        }
-        if learnt:
-            values = {name: self.registry.table(name).tolist() for name in learnt}
-            self.synapse_parameters = TypeParameters(
-                values, learnt=learnt, positive=POSITIVE & set(learnt)
-            )
-            for name, types in learnt.items():
-                mask = torch.zeros(len(synapses), dtype=torch.bool)
-                mask[types] = True
-                self.register_buffer(f"_learnt_{name}", mask, persistent=False)
-
-    def _learnt(self, name: str, fixed: torch.Tensor, decay: bool = False):
-        """``fixed`` with the learnt types' values in place (``decay``: as
-        ``exp(-dt / value)``), ``network.py:621-634``."""
-        mask = getattr(self, f"_learnt_{name}", None)
-        if mask is None:
-            return fixed
-        if name in LEARNABLE_SYNAPSE:
-            value = self.synapse_parameters.value(name)
-        else:
-            value = self.cell_parameters.value(name)[self.cell_type_indices]
-        if decay:
-            value = torch.exp(-self.dt / value)
-        return torch.where(mask, value, fixed)
-
-    def _learns(self, *names: str) -> bool:
-        return any(hasattr(self, f"_learnt_{n}") for n in names)
 
     def _build_pathways(self) -> list[Pathway]:
         pathways, made = [], []
@@ -466,15 +395,7 @@ class ConductanceNetwork(nn.Module):
         """Set the time step, recompute what depends on it, reset the state."""
         assert isinstance(dt, float) and dt > 0, "dt must be a positive float"
         self.register_buffer("dt", torch.tensor(dt, device=self.device))
-        self.register_buffer("tau_syn", torch.stack((self.tau_rise, self.tau_decay)))
-        self.register_buffer("alpha", torch.exp(-self.dt / self.tau_syn))
-        self.register_buffer("beta", torch.exp(-self.dt / self.tau_mem))
-        self.register_buffer(
-            "g_scale", conductance_kernel(self.tau_rise, self.tau_decay, self.g_bar)
-        )
-        n_ref = torch.round(self.tau_ref / self.dt).to(torch.int32)
-        self.register_buffer("n_ref", n_ref, persistent=False)
-        self._refractory = bool(n_ref.any())
+        self._set_timestep()
         self._cache_weights()
         self.reset_state()
 
@@ -530,6 +451,193 @@ class ConductanceNetwork(nn.Module):
             recurrent_gradients=self.recurrent_gradients,
         )
 
+    @torch.compiler.disable
+    def _simulate(self, input_spikes, probabilities: bool = False) -> Run:
+        if isinstance(input_spikes, np.ndarray):
+            input_spikes = torch.from_numpy(input_spikes).to(self.device)
+        self._validate_forward(input_spikes)
+        retain = [] if self.track_gradients else None
+        run = self._engine.simulate(
+            self.v,
+            self._synaptic,
+            input_spikes.to(self.dt.dtype),
+            self._drive(),
+            self._physiology(),
+            probabilities=probabilities,
+            track=self.track_variables,
+            track_batch_idx=self.track_batch_idx,
+            retain=retain,
+            **self._engine_kwargs(),
+        )
+        if retain is not None:
+            self._retained = retain
+        self.v = run.v.detach()
+        self._synaptic = run.syn.detach()
+        self._after_run(run)
+        return run
+
+    def _engine_kwargs(self) -> dict:
+        """Family-specific arguments of ``engine.simulate``."""
+        return {}
+
+    def _after_run(self, run: Run) -> None:
+        """Keep the family's extra state from ``run``."""
+
+    def _validate_forward(self, input_spikes: torch.Tensor) -> None:
+        assert isinstance(input_spikes, torch.Tensor), "input_spikes must be a Tensor"
+        assert input_spikes.device == self.device, (
+            f"input_spikes on {input_spikes.device}, model on {self.device}"
+        )
+        assert input_spikes.ndim == 3, f"input_spikes must be 3D, got {input_spikes.shape}"
+        assert input_spikes.shape[2] == self.n_inputs, (
+            f"input_spikes shape[2]={input_spikes.shape[2]}, expected {self.n_inputs}"
+        )
+        if input_spikes.shape[0] != self.batch_size:
+            raise ValueError(
+                f"Input batch size {input_spikes.shape[0]} != model batch size "
+                f"{self.batch_size}; call reset_state(batch_size=...) first"
+            )
+
+    # ------------------------------------------------------------------
+    # State
+    # ------------------------------------------------------------------
+
+    @property
+    def _synaptic(self) -> torch.Tensor:
+        return getattr(self, self.state_name)
+
+    @_synaptic.setter
+    def _synaptic(self, value: torch.Tensor) -> None:
+        setattr(self, self.state_name, value)
+
+    def reset_state(self, batch_size: int | None = None) -> None:
+        if batch_size is not None:
+            self.batch_size = batch_size
+        v, syn = self._initial_state()
+        self.register_buffer("v", v, persistent=False)
+        self.register_buffer(self.state_name, syn, persistent=False)
+        self._reset_extra()
+
+    def _reset_extra(self) -> None:
+        """Reset the family's extra state."""
+
+    def get_checkpoint_state(self) -> dict[str, np.ndarray]:
+        """The state as arrays (``network.py:971-1005``)."""
+        return {"v": self.v.cpu().numpy(), self.state_name: self._synaptic.cpu().numpy()}
+
+    def load_checkpoint_state(self, state: dict[str, np.ndarray]) -> None:
+        self.v = torch.from_numpy(state["v"]).to(self.device)
+        self._synaptic = torch.from_numpy(state[self.state_name]).to(self.device)
+
+    def _weight_matrix(self, side_index: int) -> torch.Tensor:
+        side = self._sides[side_index]
+        W = torch.zeros((len(side.cell_type_indices), self.n_neurons), **self._float)
+        for (src, tgt), _ in side.projections.items():
+            rows, cols = self._block(side, src, tgt)
+            if rows.size and cols.size:
+                W[np.ix_(rows, cols)] = getattr(self, side.attribute)[f"{src}__{tgt}"]()
+        return W
+
+
+class ConductanceNetwork(ProjectionNetwork):
+    """Base of the conductance-based LIF networks (``conductance/network.py:44-255`` for
+    the mechanisms this build supports).
+
+    State ``v`` ``(B, N)``, conductances ``(B, N, 2, S)`` (stored ``(B, 2, S, N)``) and
+    refractory counters ``(B, N)`` int32 continue from one ``forward`` call to the next
+    until ``reset_state``.
+    """
+
+    state_name = "g"
+    output_name = "s"
+    has_refractory = True
+
+    def __init__(self, *, surrgrad_scale: float, spike_mode: str, **kwargs):
+        assert isinstance(surrgrad_scale, (int, float)) and surrgrad_scale > 0
+        if spike_mode != "deterministic":
+            raise NotImplementedError("only spike_mode='deterministic' is supported")
+        self.spike_mode = spike_mode
+        self._surrgrad_scale = float(surrgrad_scale)
+        super().__init__(**kwargs)
+
+    def _register_physiology(self) -> None:
+        for name in NEURON_PARAMETERS:
+            self.register_buffer(name, self._per_neuron(name))
+        self.register_buffer("C_m", self.tau_mem * self.g_L)
+        for name in SYNAPSE_PARAMETERS:
+            self.register_buffer(name, self.registry.table(name))
+        self.register_buffer("g_clip", self.registry.table("g_clip", default=float("inf")))
+        tau_ref = self._per_neuron("tau_ref", 0.0)
+        assert bool((tau_ref >= 0).all()), "cell_params: tau_ref must be >= 0"
+        self.register_buffer("tau_ref", tau_ref, persistent=False)
+        self.register_buffer(
+            "surrgrad_scale", torch.tensor(self._surrgrad_scale, dtype=torch.float32)
+        )
+        self._register_learnt()
+
+    def _register_learnt(self) -> None:
+        learn = self.learn
+        unknown = set(learn) - set(LEARNABLE) - set(LEARNABLE_SYNAPSE)
+        assert not unknown, f"learn: unknown parameters {sorted(unknown)}"
+        cells = sorted(self.cell_params, key=lambda c: c["cell_id"])
+        names = [c["name"] for c in cells]
+        learnt = {
+            name: learnt_types(learn[name], names, f"learn[{name!r}]")
+            for name in LEARNABLE
+            if learn.get(name)
+        }
+        if learnt:
+            values = {name: [c[name] for c in cells] for name in learnt}
+            self.cell_parameters = TypeParameters(
+                values, learnt=learnt, positive=POSITIVE & set(learnt)
+            )
+            for name, types in learnt.items():
+                mask = torch.isin(self.cell_type_indices, torch.tensor(types))
+                self.register_buffer(f"_learnt_{name}", mask, persistent=False)
+        synapses = self.registry.synapses
+        learnt = {
+            name: learnt_synapses(learn[name], synapses, f"learn[{name!r}]")
+            for name in LEARNABLE_SYNAPSE
+            if learn.get(name)
+        }
+        if learnt:
+            values = {name: self.registry.table(name).tolist() for name in learnt}
+            self.synapse_parameters = TypeParameters(
+                values, learnt=learnt, positive=POSITIVE & set(learnt)
+            )
+            for name, types in learnt.items():
+                mask = torch.zeros(len(synapses), dtype=torch.bool)
+                mask[types] = True
+                self.register_buffer(f"_learnt_{name}", mask, persistent=False)
+
+    def _learnt(self, name: str, fixed: torch.Tensor, decay: bool = False):
+        """``fixed`` with the learnt types' values in place (``decay``: as
+        ``exp(-dt / value)``), ``network.py:621-634``."""
+        mask = getattr(self, f"_learnt_{name}", None)
+        if mask is None:
+            return fixed
+        if name in LEARNABLE_SYNAPSE:
+            value = self.synapse_parameters.value(name)
+        else:
+            value = self.cell_parameters.value(name)[self.cell_type_indices]
+        if decay:
+            value = torch.exp(-self.dt / value)
+        return torch.where(mask, value, fixed)
+
+    def _learns(self, *names: str) -> bool:
+        return any(hasattr(self, f"_learnt_{n}") for n in names)
+
+    def _set_timestep(self) -> None:
+        self.register_buffer("tau_syn", torch.stack((self.tau_rise, self.tau_decay)))
+        self.register_buffer("alpha", torch.exp(-self.dt / self.tau_syn))
+        self.register_buffer("beta", torch.exp(-self.dt / self.tau_mem))
+        self.register_buffer(
+            "g_scale", conductance_kernel(self.tau_rise, self.tau_decay, self.g_bar)
+        )
+        n_ref = torch.round(self.tau_ref / self.dt).to(torch.int32)
+        self.register_buffer("n_ref", n_ref, persistent=False)
+        self._refractory = bool(n_ref.any())
+
     def _physiology(self) -> Physiology:
         """The engine's parameters for one call (``conductance/network.py:210-246``)."""
         learnt = self._learnt
@@ -565,91 +673,31 @@ class ConductanceNetwork(nn.Module):
         ).permute(0, 3, 1, 2)
         return v, g
 
-    @torch.compiler.disable
-    def _simulate(self, input_spikes, probabilities: bool = False) -> Run:
-        if isinstance(input_spikes, np.ndarray):
-            input_spikes = torch.from_numpy(input_spikes).to(self.device)
-        self._validate_forward(input_spikes)
-        retain = [] if self.track_gradients else None
-        run = self._engine.simulate(
-            self.v,
-            self._synaptic,
-            input_spikes.to(self.dt.dtype),
-            self._drive(),
-            self._physiology(),
-            refractory=self.refractory,
-            probabilities=probabilities,
-            track=self.track_variables,
-            track_batch_idx=self.track_batch_idx,
-            retain=retain,
-        )
-        if retain is not None:
-            self._retained = retain
-        self.v = run.v.detach()
-        self._synaptic = run.syn.detach()
+    def _engine_kwargs(self) -> dict:
+        return {"refractory": self.refractory}
+
+    def _after_run(self, run: Run) -> None:
         if run.refractory is not None:
             self.refractory = run.refractory
-        return run
 
-    def _validate_forward(self, input_spikes: torch.Tensor) -> None:
-        assert isinstance(input_spikes, torch.Tensor), "input_spikes must be a Tensor"
-        assert input_spikes.device == self.device, (
-            f"input_spikes on {input_spikes.device}, model on {self.device}"
-        )
-        assert input_spikes.ndim == 3, f"input_spikes must be 3D, got {input_spikes.shape}"
-        assert input_spikes.shape[2] == self.n_inputs, (
-            f"input_spikes shape[2]={input_spikes.shape[2]}, expected {self.n_inputs}"
-        )
-        if input_spikes.shape[0] != self.batch_size:
-            raise ValueError(
-                f"Input batch size {input_spikes.shape[0]} != model batch size "
-                f"{self.batch_size}; call reset_state(batch_size=...) first"
-            )
-
-    # ------------------------------------------------------------------
-    # State
-    # ------------------------------------------------------------------
-
-    @property
-    def _synaptic(self) -> torch.Tensor:
-        return getattr(self, self.state_name)
-
-    @_synaptic.setter
-    def _synaptic(self, value: torch.Tensor) -> None:
-        setattr(self, self.state_name, value)
-
-    def reset_state(self, batch_size: int | None = None) -> None:
-        if batch_size is not None:
-            self.batch_size = batch_size
-        v, g = self._initial_state()
-        self.register_buffer("v", v, persistent=False)
-        self.register_buffer(self.state_name, g, persistent=False)
-        counter = torch.zeros((self.batch_size, self.n_neurons), dtype=torch.int32, device=self.device)
+    def _reset_extra(self) -> None:
+        counter = torch.zeros((self.batch_size, self.n_neurons), dtype=torch.int32,
+                              device=self.device)
         self.register_buffer("refractory", counter, persistent=False)
 
     def get_checkpoint_state(self) -> dict[str, np.ndarray]:
-        state = {"v": self.v.cpu().numpy(), self.state_name: self._synaptic.cpu().numpy()}
+        state = super().get_checkpoint_state()
         if self._refractory:
             state["refractory"] = self.refractory.cpu().numpy()
         return state
 
     def load_checkpoint_state(self, state: dict[str, np.ndarray]) -> None:
-        self.v = torch.from_numpy(state["v"]).to(self.device)
-        self._synaptic = torch.from_numpy(state[self.state_name]).to(self.device)
+        super().load_checkpoint_state(state)
         self.refractory = (
             torch.from_numpy(state["refractory"]).to(self.device)
             if "refractory" in state
             else torch.zeros_like(self.v, dtype=torch.int32)
         )
-
-    def _weight_matrix(self, side_index: int) -> torch.Tensor:
-        side = self._sides[side_index]
-        W = torch.zeros((len(side.cell_type_indices), self.n_neurons), **self._float)
-        for (src, tgt), _ in side.projections.items():
-            rows, cols = self._block(side, src, tgt)
-            if rows.size and cols.size:
-                W[np.ix_(rows, cols)] = getattr(self, side.attribute)[f"{src}__{tgt}"]()
-        return W
 
 
 def _engine_module():
