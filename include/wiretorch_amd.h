@@ -180,6 +180,87 @@ int64_t wt_cond_recurrent_backward_scratch_bytes(int64_t S, int64_t K_rec, int64
 int wt_cond_recurrent_backward(const wt_tables* tab, const wt_side* rec,
                                const wt_backward_io* io, void* scratch, wt_stream_t stream);
 
+/* ===================================================================================
+ * Rate networks (rate/dynamics.py): r = gain f(v - theta); a_k = r[rows_k] W_k (or the
+ * input's columns times W_k); I <- decay I + (1 - decay) sum_k a_k jump_k;
+ * v <- beta v + (1 - beta) sum_s sign_s I_s.
+ * =================================================================================== */
+
+/* Per-neuron and per-synapse tables of one call (rate/dynamics.py:72-92). */
+typedef struct {
+  const float* theta;          /* (N,) */
+  const float* gain;           /* (N,) */
+  const float* beta;           /* (N,) membrane decay per step */
+  const int8_t* nonlinearity;  /* (N,) 0 relu, 1 softplus, 2 sigmoid, 3 tanh */
+  const float* sign;           /* (S,) +1 excitatory, -1 inhibitory */
+  const float* decay;          /* (S,) current decay per step */
+  const float* jump;           /* (K, N, S) scale_k[n] * made_k[s] (rate/dynamics.py:95-97) */
+  const float* made;           /* (K, S) */
+  int64_t N, S, K, K_rec;
+} wt_rate_tables;
+
+/* The matrix operands, zero-padded to whole 64 x 64 tiles. K dimension: recurrent rows
+ * [0, K_rec_pad) (neurons, in segment order), then input rows [K_rec_pad, +K_ff_pad).
+ * seg[g] = {first row, end row, pathway k, 1 for an input segment}, whole tiles. */
+typedef struct {
+  const void* W;          /* (K_rec_pad + K_ff_pad, N_pad), float32 or bfloat16 */
+  void* rin;              /* [2][B_pad][K_rec_pad] rates of the step (zero-initialised) */
+  const void* X;          /* [T][B_pad][K_ff_pad] input of every step, rows permuted */
+  const int32_t* rpos;    /* (N,) recurrent row of each neuron, or -1 */
+  const int32_t* src_of;  /* (K_rec_pad,) neuron of each recurrent row, or -1 */
+  int32_t seg[16][4];
+  int64_t n_seg, B_pad, N_pad, K_rec_pad, K_ff_pad;
+  int64_t dtype;          /* 0 float32, 1 bfloat16 (what W, rin, X hold) */
+} wt_rate_operand;
+
+typedef struct {
+  int64_t B, T;
+  float* v;             /* (B, N) in/out */
+  float* I;             /* (B, S, N) in/out */
+  float* out;           /* (B, T, N) rates */
+  float* track_v;       /* (Bt, T, N) or null */
+  float* track_I;       /* (Bt, T, N, S) or null */
+  int64_t track_b;      /* -1: all trials */
+  float* v_saved;       /* (B, T, N) voltage entering each step, or null */
+  float* I_saved;       /* (B, T, N, S) currents entering each step, or null */
+  float* target_saved;  /* (B, T, N, S) or null */
+  float* A_saved;       /* (K, B, T, N) activations, or null */
+} wt_rate_io;
+
+/* wt_rate_forward — T steps of a rate network: per step one fused launch (MFMA product
+ * of the rates with the weights, then currents, voltages and the next rates).
+ * Replaces: rate/engine.py:157-300 (_Product, the per-step scan and recurrent kernels
+ * rate/kernels.py:100-219). */
+int wt_rate_forward(const wt_rate_tables* tab, const wt_rate_operand* op, const wt_rate_io* io,
+                    wt_stream_t stream);
+
+typedef struct {
+  int64_t B, T;
+  const float* grad_out;      /* (B, T, N) dL/d rates */
+  const float* v_saved;       /* from the forward */
+  const float* I_saved;
+  const float* target_saved;
+  const float* A_saved;
+  const float* I_final;       /* (B, S, N) currents after the last step */
+  float* lam_v;               /* (B, N) scratch, zeroed */
+  float* lam_I;               /* (B, S, N) scratch, zeroed */
+  float* d_rate;              /* (B, N) scratch, zeroed (recurrent networks) */
+  void* gA_op;                /* (K_rec, B_pad, N_pad) scratch, zeroed, operand dtype */
+  float* grad_A;              /* (K, B, T, N) out: dL/da */
+  float* acc_theta;           /* (B, N) accumulated partials, or null */
+  float* acc_gain;            /* (B, N) */
+  float* acc_beta;            /* (B, N) */
+  float* acc_decay;           /* (B, S, N) */
+  float* acc_scale;           /* (K, B, N) */
+} wt_rate_back_io;
+
+/* wt_rate_backward — the reverse: per step dL/da_k from the currents' and voltages'
+ * adjoints, then dL/dr = sum_k dL/da_k W_k^T (MFMA) into the rates' adjoint. Weight
+ * and input gradients follow from grad_A by plain products on the host.
+ * Replaces: rate/kernels.py:228-465, rate/engine.py:336-383 (_RecurrentRun.backward). */
+int wt_rate_backward(const wt_rate_tables* tab, const wt_rate_operand* op,
+                     const wt_rate_back_io* io, wt_stream_t stream);
+
 /* wt_edge_sources — edge_src[e] = the source of edge e (E = indptr[n_src]). */
 int wt_edge_sources(const int64_t* indptr, int64_t n_src, int64_t* edge_src,
                     wt_stream_t stream);

@@ -53,6 +53,39 @@ class BackwardIO(ctypes.Structure):
     ]  # fmt: skip
 
 
+class RateTables(ctypes.Structure):
+    _fields_ = [
+        ("theta", P), ("gain", P), ("beta", P), ("nonlinearity", P), ("sign", P),
+        ("decay", P), ("jump", P), ("made", P), ("N", I64), ("S", I64), ("K", I64),
+        ("K_rec", I64),
+    ]  # fmt: skip
+
+
+class RateOperand(ctypes.Structure):
+    _fields_ = [
+        ("W", P), ("rin", P), ("X", P), ("rpos", P), ("src_of", P),
+        ("seg", (ctypes.c_int32 * 4) * 16), ("n_seg", I64), ("B_pad", I64), ("N_pad", I64),
+        ("K_rec_pad", I64), ("K_ff_pad", I64), ("dtype", I64),
+    ]  # fmt: skip
+
+
+class RateIO(ctypes.Structure):
+    _fields_ = [
+        ("B", I64), ("T", I64), ("v", P), ("I", P), ("out", P), ("track_v", P),
+        ("track_I", P), ("track_b", I64), ("v_saved", P), ("I_saved", P),
+        ("target_saved", P), ("A_saved", P),
+    ]  # fmt: skip
+
+
+class RateBackIO(ctypes.Structure):
+    _fields_ = [
+        ("B", I64), ("T", I64), ("grad_out", P), ("v_saved", P), ("I_saved", P),
+        ("target_saved", P), ("A_saved", P), ("I_final", P), ("lam_v", P), ("lam_I", P),
+        ("d_rate", P), ("gA_op", P), ("grad_A", P), ("acc_theta", P), ("acc_gain", P),
+        ("acc_beta", P), ("acc_decay", P), ("acc_scale", P),
+    ]  # fmt: skip
+
+
 #: Every entry point the header declares, with its ctypes signature.
 SIGNATURES = {
     "wt_split_ranges": (ctypes.c_int, [P, P, I64, I64, I64, P, P]),
@@ -69,6 +102,11 @@ SIGNATURES = {
     "wt_cond_recurrent_backward_scratch_bytes": (I64, [I64, I64, I64, I64]),
     "wt_cond_recurrent_backward": (ctypes.c_int, [ctypes.POINTER(Tables), ctypes.POINTER(Side),
                                                   ctypes.POINTER(BackwardIO), P, P]),
+    "wt_rate_forward": (ctypes.c_int, [ctypes.POINTER(RateTables), ctypes.POINTER(RateOperand),
+                                       ctypes.POINTER(RateIO), P]),
+    "wt_rate_backward": (ctypes.c_int, [ctypes.POINTER(RateTables),
+                                        ctypes.POINTER(RateOperand),
+                                        ctypes.POINTER(RateBackIO), P]),
     "wt_edge_sources": (ctypes.c_int, [P, I64, P, P]),
     "wt_weight_gradient": (ctypes.c_int, [ctypes.POINTER(Side), P, I64, P, P, P, P, I64,
                                           I64, I64, I64, P, P]),
