@@ -1,13 +1,19 @@
 """Benchmark: neuron-steps/s and synaptic events/s of the fly-scale conductance-LIF
 forward on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2|4]
 
 A step is one forward call of the hot path over one batch of synthetic input: 8 trials
 x 2000 time steps (dt 0.1 ms) of a 140k-neuron, ~50M-synapse network from rest, with
 the input resident in HBM. Prints one JSON line (see the keys below), including the
 roofline of the dominant kernel (``wt_cond_run``, timed with HIP events on its stream)
 and the CPU baseline (the oracle, on a bounded slice of the same workload).
+
+``--config 4`` measures the dense rate network instead (configuration 4, the matrix-core
+path): a step is one forward + backward of 256 trials x 1000 steps of 4096 tanh rate
+neurons with bf16 weights, from rest, with a linear read-out's squared error as the loss;
+the roofline is that of the kernel with the largest share of the step, against the
+matrix cores' dense peak in its arithmetic type.
 """
 
 from __future__ import annotations
@@ -28,6 +34,7 @@ sys.path.insert(0, str(ROOT))
 from wiretorch_amd import engine, synthetic  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f32": 157.3}
 METRIC = "neuron-steps/s and synaptic events/s, fly-scale conductance LIF, 1 MI355X"
 
 
@@ -87,6 +94,129 @@ def cpu_baseline(wl, steps):
     }
 
 
+def rate_cpu_baseline(wl, steps):
+    """The oracle (the reference's PyTorch rate step restated, float32 as the reference's
+    CPU path computes) on forward + backward of the first ``steps`` steps, all trials."""
+    import oracle.rate as oracle_rate
+
+    wl_cpu = synthetic.dense_rate(B=wl.x.shape[0], T=steps, storage_dtype=torch.float32)
+    model = wl_cpu.model
+    model._engine = oracle_rate
+    readout = _readout(wl.N, "cpu")
+    x = torch.from_numpy(wl.x[:, :steps])
+    target = torch.zeros((x.shape[0], steps, readout.shape[1]))
+    _rate_step(model, x[:, :2], readout, target[:, :2])  # warm-up
+    t0 = time.perf_counter()
+    _rate_step(model, x, readout, target)
+    dt = time.perf_counter() - t0
+    B = x.shape[0]
+    return {
+        "value": B * wl.N * steps / dt,
+        "unit": "neuron-steps/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"oracle (float32) forward + backward of the first {steps} of "
+                  f"{wl.x.shape[1]} steps, all {B} trials ({dt:.1f} s)",
+    }
+
+
+def _readout(N, device, n_out=16):
+    g = torch.Generator().manual_seed(5)
+    return (torch.randn((N, n_out), generator=g) / N**0.5).to(device)
+
+
+def _rate_step(model, x, readout, target):
+    """One training step's forward + backward: rates, a linear read-out, squared error."""
+    model.reset_state()
+    model.zero_grad(set_to_none=True)
+    rates = model(x)
+    loss = ((rates @ readout - target) ** 2).mean()
+    loss.backward()
+    return rates
+
+
+def bench_config4(args):
+    from wiretorch_amd import rate_engine
+
+    dev = torch.device("cuda:0")
+    T = args.T if args.T != 2000 else 1000
+    wl = synthetic.config4(T=T)
+    model = wl.model.to(dev)
+    x = torch.from_numpy(wl.x).to(dev)
+    B, N = x.shape[0], wl.N
+    n_in = x.shape[2]
+    readout = _readout(N, dev)
+    target = torch.randn((B, T, readout.shape[1]), generator=torch.Generator().manual_seed(6))
+    target = target.to(dev)
+    for _ in range(args.warmup):
+        _rate_step(model, x, readout, target)
+    torch.cuda.synchronize()
+    rate_engine.LAUNCH_EVENTS = {}
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        rates = _rate_step(model, x, readout, target)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    events, rate_engine.LAUNCH_EVENTS = rate_engine.LAUNCH_EVENTS, None
+    ms = {k: float(np.mean([a.elapsed_time(b) for a, b in v])) for k, v in events.items()}
+    ms_per_step = wall * 1e3 / args.steps
+    # algorithmic flops: per time step the recurrent product and the input product forward,
+    # the recurrent product's transpose backward; per call the weight gradients
+    flops = {
+        "forward": 2.0 * B * N * (N + n_in) * T,
+        "backward": 2.0 * B * N * N * T,
+        "grad_w": 2.0 * B * T * N * (N + n_in),
+    }
+    peak = {"forward": "bf16", "backward": "bf16", "grad_w": "f32"}
+    kernel = {"forward": "rate_step_kernel (wt_rate_forward)",
+              "backward": "rate_back_elem_kernel + rate_back_gemm_kernel (wt_rate_backward)",
+              "grad_w": "weight-gradient GEMM (torch.matmul, float32)"}
+    dominant = max(ms, key=ms.get)
+    achieved = flops[dominant] / (ms[dominant] / 1e3) / 1e12
+    peak_tf = MFMA_PEAK_TFLOPS[peak[dominant]]
+    print(f"# config4: wall {ms_per_step:.2f} ms/step; " + ", ".join(
+        f"{k} {ms[k]:.2f} ms ({flops[k] / (ms[k] / 1e3) / 1e12:.0f} TFLOP/s)" for k in ms),
+        file=sys.stderr, flush=True)
+    mean_rate = float(rates.detach().abs().mean())
+    cpu = rate_cpu_baseline(wl, args.cpu_steps) if args.cpu_steps > 0 else None
+    line = {
+        "metric": METRIC,
+        "value": B * N * T / (ms_per_step / 1e3),
+        "unit": "neuron-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "tflops": sum(flops.values()) / (ms_per_step / 1e3) / 1e12,
+        "mean_abs_rate": mean_rate,
+        "config": {
+            "workload": "config4: dense rate network, forward + backward",
+            "neurons": N, "inputs": n_in, "batch": B, "time_steps": T, "dt_ms": synthetic.RATE_DT,
+            "products": "bf16 operands, f32 accumulation; f32 state; f32 weight gradients",
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": peak_tf,
+            "unit": "TFLOP/s",
+            "frac": achieved / peak_tf,
+            "traffic": None,
+            "kernel": kernel[dominant],
+            "kernel_ms": ms[dominant],
+            "algorithmic_flops_per_launch": flops[dominant],
+            "per_part_ms": ms,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -94,6 +224,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--cpu-steps", type=int, default=int(os.environ.get("BENCH_CPU_STEPS", 400)))
     ap.add_argument("--T", type=int, default=2000)
+    ap.add_argument("--config", type=int, choices=(2, 4), default=2)
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run one device-to-device copy of this many bytes (the "
                          "reference kernel for calibrating rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -110,6 +241,10 @@ def main():
         print("bench.py runs on one GPU only: this build has no multi-GPU path "
               "(the hot path runs on a single GPU)", file=sys.stderr)
         sys.exit(2)
+    if args.config == 4:
+        if "--cpu-steps" not in sys.argv and "BENCH_CPU_STEPS" not in os.environ:
+            args.cpu_steps = 100
+        return bench_config4(args)
     dev = torch.device("cuda:0")
     t_build = time.perf_counter()
     wl = synthetic.fly_scale(T=args.T, device=dev)

@@ -204,6 +204,7 @@ typedef struct {
  * seg[g] = {first row, end row, pathway k, 1 for an input segment}, whole tiles. */
 typedef struct {
   const void* W;          /* (K_rec_pad + K_ff_pad, N_pad), float32 or bfloat16 */
+  const void* Wt;         /* (N_pad, K_rec_pad + K_ff_pad): W transposed, same dtype */
   void* rin;              /* [2][B_pad][K_rec_pad] rates of the step (zero-initialised) */
   const void* X;          /* [T][B_pad][K_ff_pad] input of every step, rows permuted */
   const int32_t* rpos;    /* (N,) recurrent row of each neuron, or -1 */

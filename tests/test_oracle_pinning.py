@@ -10,7 +10,9 @@ the restatement (a dropped term, a wrong sign, a transposed index) fails:
 * the surrogate spike's known answer (reference ``tests/test_training_utils.py:31-36``);
 * refractory timing of single neurons in closed form (reference
   ``tests/test_refractory.py:85-124``);
-* compressed propagation (``oracle.sparse``) against a brute-force dense float64 product.
+* compressed propagation (``oracle.sparse``) against a brute-force dense float64 product;
+* the rate oracle's reduced-precision product: the plain product on operands that are
+  already representable, and which operands and gradients it rounds otherwise.
 
 The refractory closed forms also run on the GPU engine (marked ``gpu``).
 """
@@ -192,3 +194,55 @@ def test_sparse_activations_equal_the_dense_product(seed):
         rows = pathway == k
         expected = s[:, rows].astype(np.float64) @ W[rows].astype(np.float64)
         np.testing.assert_array_equal(got[k].numpy(), expected.astype(np.float32))
+
+
+# ---------------------------------------------------------------------------------
+# The rate oracle's reduced-precision product (oracle/rate.py)
+# ---------------------------------------------------------------------------------
+
+
+def _bf16_exact(shape, gen):
+    return torch.randn(shape, generator=gen).to(torch.bfloat16).float()
+
+
+def test_rounded_product_is_plain_on_representable_operands():
+    """Operands already in bfloat16: forward and both gradients equal the plain float32
+    product's (autograd) — a transposed or swapped operand in the backward fails."""
+    import oracle.rate as oracle_rate
+
+    gen = torch.Generator().manual_seed(0)
+    a, W, g = _bf16_exact((5, 7, 48), gen), _bf16_exact((48, 33), gen), _bf16_exact((5, 7, 33), gen)
+    for round_grad in (False, True):
+        a1, W1 = a.clone().requires_grad_(), W.clone().requires_grad_()
+        a2, W2 = a.clone().requires_grad_(), W.clone().requires_grad_()
+        out1 = oracle_rate.product(a1, W1, torch.bfloat16, round_grad)
+        out2 = a2 @ W2
+        out1.backward(g)
+        out2.backward(g)
+        assert torch.equal(out1, out2)
+        torch.testing.assert_close(a1.grad, a2.grad, rtol=1e-6, atol=1e-6)
+        torch.testing.assert_close(W1.grad, W2.grad, rtol=1e-6, atol=1e-6)
+
+
+def test_rounded_product_rounds_operands_and_dl_da_only():
+    """General operands: the forward is the product of the rounded operands (rounding
+    is not a no-op here), ``dL/dW`` uses the unrounded ``a`` (the reference's float16
+    weight gradient multiplies float32 rates), and ``dL/da`` rounds ``dL/dout`` only when
+    asked to."""
+    import oracle.rate as oracle_rate
+
+    gen = torch.Generator().manual_seed(1)
+    a, W, g = torch.randn((6, 40), generator=gen), torch.randn((40, 9), generator=gen), \
+        torch.randn((6, 9), generator=gen)
+    ra, rW, rg = (t.to(torch.bfloat16).float() for t in (a, W, g))
+    assert not torch.equal(ra, a) and not torch.equal(rg, g)
+    for round_grad, g_used in ((False, g), (True, rg)):
+        a1, W1 = a.clone().requires_grad_(), W.clone().requires_grad_()
+        out = oracle_rate.product(a1, W1, torch.bfloat16, round_grad)
+        torch.testing.assert_close(out, ra @ rW, rtol=1e-6, atol=1e-6)
+        out.backward(g)
+        W_used = rW if round_grad else W
+        torch.testing.assert_close(a1.grad, g_used @ W_used.T, rtol=1e-6, atol=1e-6)
+        torch.testing.assert_close(W1.grad, a.T @ g, rtol=1e-6, atol=1e-6)
+    # float32 storage is the plain product
+    torch.testing.assert_close(oracle_rate.product(a, W, torch.float32, True), a @ W)

@@ -100,3 +100,51 @@ def test_bfloat16_storage_close_to_float32():
     with torch.no_grad():
         r_ref = ref.model(x).numpy()
     np.testing.assert_allclose(r_bf16, r_ref, rtol=0, atol=2e-2 * np.ptp(r_ref))
+
+
+# ---------------------------------------------------------------------------------
+# Dense signed rate network (configuration 4's shape), bfloat16 products
+# ---------------------------------------------------------------------------------
+
+
+def _dense_run(device, engine, **shape):
+    """Rates and gradients of a read-out loss, with every product's operands in bfloat16
+    (the oracle rounds them the same way and multiplies in float32)."""
+    from wiretorch_amd import synthetic
+
+    wl = synthetic.dense_rate(**shape)
+    model = wl.model.to(device)
+    if engine is not None:
+        sc.use_engine(model, engine)
+    x = torch.from_numpy(wl.x).to(device)
+    g = torch.Generator().manual_seed(11)
+    readout = (torch.randn((wl.N, 8), generator=g) / wl.N**0.5).to(device)
+    rates = model(x)
+    loss = ((rates @ readout) ** 2).mean()
+    loss.backward()
+    grads = {k: p.grad.detach().cpu().numpy() for k, p in model.named_parameters()}
+    return rates.detach().cpu().numpy(), float(loss.detach()), grads
+
+
+@pytest.mark.parametrize("shape", [
+    dict(N=320, n_in=64, B=40, T=60, seed=7),       # ragged: N, B not multiples of 64
+    dict(N=4096, n_in=64, B=256, T=6, seed=4),      # configuration 4's full width
+], ids=["small", "config4_width"])
+def test_dense_bfloat16_against_rounded_oracle(shape):
+    """Every product of two bfloat16 operands is exact in float32, so the engine and the
+    oracle differ only in the order of float32 sums — and in the operands whose bfloat16
+    rounding that order flips, each moving its terms by 2^-9 of themselves. Those flips
+    compound along a chaotic trajectory (g^2 = 1.5): two CPU runs of the oracle that
+    differ only in the order of the sums drift apart to 3e-4 of the rates' range by step
+    60 (gradients 1e-4 of their scale). So: the first 15 steps within 1e-4 of the range,
+    every step within 2e-3 of it, gradients within 1e-3 of their scale."""
+    r_ref, l_ref, g_ref = _dense_run("cpu", oracle_rate, **shape)
+    r_gpu, l_gpu, g_gpu = _dense_run(DEV, None, **shape)
+    ptp = np.ptp(r_ref)
+    np.testing.assert_allclose(r_gpu[:, :15], r_ref[:, :15], rtol=0, atol=1e-4 * ptp)
+    np.testing.assert_allclose(r_gpu, r_ref, rtol=0, atol=2e-3 * ptp)
+    np.testing.assert_allclose(l_gpu, l_ref, rtol=1e-4)
+    assert g_ref.keys() == g_gpu.keys()
+    for key, value in g_ref.items():
+        scale = np.abs(value).max()
+        np.testing.assert_allclose(g_gpu[key], value, rtol=0, atol=1e-3 * scale, err_msg=key)

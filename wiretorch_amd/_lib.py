@@ -63,7 +63,7 @@ class RateTables(ctypes.Structure):
 
 class RateOperand(ctypes.Structure):
     _fields_ = [
-        ("W", P), ("rin", P), ("X", P), ("rpos", P), ("src_of", P),
+        ("W", P), ("Wt", P), ("rin", P), ("X", P), ("rpos", P), ("src_of", P),
         ("seg", (ctypes.c_int32 * 4) * 16), ("n_seg", I64), ("B_pad", I64), ("N_pad", I64),
         ("K_rec_pad", I64), ("K_ff_pad", I64), ("dtype", I64),
     ]  # fmt: skip

@@ -24,10 +24,9 @@ namespace rate {
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 64;     // outputs per workgroup, per side
-constexpr int kKB = 32;       // k per LDS stage
-constexpr int kPad = 8;       // LDS row padding (elements)
 constexpr int kThreads = 256;
 constexpr int kMaxS = 8;
 constexpr int kMaxSeg = 16;
@@ -61,58 +60,130 @@ __device__ inline float nonlin_grad(int code, float x) {
   }
 }
 
-template <typename T>
-struct Mma;
-template <>
-struct Mma<float> {  // C[32x32] += A[32x2] B[2x32]: lane l holds A[l%32][l/32], B[l/32][l%32]
-  static constexpr int kStep = 2;
-  __device__ static void run(f32x16& c, const float* a_row, const float* b_col, int lane) {
-    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a_row[lane >> 5], b_col[lane >> 5], c, 0, 0, 0);
-  }
-};
-template <>
-struct Mma<__bf16> {  // C += A[32x16] B[16x32]: lane l holds A[l%32][8(l/32)+e], B[8(l/32)+e][l%32]
-  static constexpr int kStep = 16;
-  __device__ static void run(f32x16& c, const __bf16* a_row, const __bf16* b_col, int lane) {
-    const bf16x8 a = *reinterpret_cast<const bf16x8*>(a_row + 8 * (lane >> 5));
-    const bf16x8 b = *reinterpret_cast<const bf16x8*>(b_col + 8 * (lane >> 5));
-    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-  }
-};
-
 // Output element v of a lane's 32 x 32 block: row 8(v/4) + 4(l/32) + v%4, column l%32.
 __device__ inline int out_row(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
 
-// One k-block of a 64 x 64 tile: A rows [0, 64) x k [kA, kA + 32) (row-major, lda), and
-// B either as [k][j] (row-major, ldb; B_ROWS_ARE_K) or as [j][k], from k = kB. Staged in
-// LDS as sA[i][k] and sB[j][k], then each wave multiplies its 32 x 32 block.
-template <typename T, bool B_ROWS_ARE_K>
-__device__ inline void kblock(f32x16& c, T (*sA)[kKB + kPad], T (*sB)[kKB + kPad], const T* A,
-                              int64_t lda, int64_t kA, const T* Bm, int64_t ldb, int64_t kB,
-                              int wave, int lane) {
-  const int tid = threadIdx.x;
-  for (int e = tid; e < kTile * kKB; e += kThreads) {
-    const int i = e / kKB, kk = e % kKB;
-    sA[i][kk] = A[(int64_t)i * lda + kA + kk];
-  }
-  if (B_ROWS_ARE_K) {
-    for (int e = tid; e < kTile * kKB; e += kThreads) {
-      const int kk = e / kTile, j = e % kTile;
-      sB[j][kk] = Bm[(kB + kk) * ldb + j];
-    }
-  } else {
-    for (int e = tid; e < kTile * kKB; e += kThreads) {
-      const int j = e / kKB, kk = e % kKB;
-      sB[j][kk] = Bm[(int64_t)j * ldb + kB + kk];
-    }
-  }
-  __syncthreads();
-  const int wi = wave >> 1, wj = wave & 1;
-  const T* a_row = &sA[wi * 32 + (lane & 31)][0];
-  const T* b_col = &sB[wj * 32 + (lane & 31)][0];
+// ---------------------------------------------------------------------------------
+// The tile product C[64 x 64] += A[64 x k] Bt[64 x k]^T with both operands k-contiguous
+// (row-major, k along the row: the rates or inputs by trial, the weights transposed by
+// target), in stages of 128 bytes of k (64 bfloat16 or 32 float32).
+//
+// A stage is 8 KB per operand: thread t fetches the 16-byte chunk t % 8 of rows t / 8 and
+// 32 + t / 8, so eight consecutive threads read one row's 128 bytes. Stages are fetched
+// kDepth ahead into a ring of registers and stored to one of two LDS buffers; one
+// barrier per stage. In LDS, chunk c of row r sits in slot c ^ (r % 8) of its row: the
+// MFMA operand reads (one 16-byte chunk per lane, rows r..r+7 at one chunk) then fall in
+// eight different slots — no bank conflicts.
+// ---------------------------------------------------------------------------------
+
+constexpr int kStageBytes = 128;
+constexpr int kDepth = 4;
+
+struct StageRegs {
+  u32x4 a[2], b[2];
+};
+
+__device__ inline u32x4 gload16(const char* p) {
+  return *(const __attribute__((address_space(1))) u32x4*)p;
+}
+
+// One stage's operands: rows [0, 64) of A at byte offset `a` (row pitch lda bytes), of
+// Bt at `b` (pitch ldb).
+__device__ inline void stage_load(StageRegs& r, const char* a, int64_t lda, const char* b,
+                                  int64_t ldb) {
+  const int t = threadIdx.x, row = t >> 3, off = (t & 7) * 16;
+  r.a[0] = gload16(a + row * lda + off);
+  r.a[1] = gload16(a + (row + 32) * lda + off);
+  r.b[0] = gload16(b + row * ldb + off);
+  r.b[1] = gload16(b + (row + 32) * ldb + off);
+}
+
+// LDS: [buffer][operand][row * 8 + slot] in 16-byte units.
+typedef u32x4 StageLds[2][2][512];
+
+__device__ inline void stage_store(StageLds& lds, int buf, const StageRegs& r) {
+  const int t = threadIdx.x, row = t >> 3, slot = (t & 7) ^ (row & 7);
+  lds[buf][0][row * 8 + slot] = r.a[0];
+  lds[buf][0][(row + 32) * 8 + slot] = r.a[1];
+  lds[buf][1][row * 8 + slot] = r.b[0];
+  lds[buf][1][(row + 32) * 8 + slot] = r.b[1];
+}
+
+template <typename T>
+struct Mma;
+// bfloat16, v_mfma_f32_32x32x16_bf16: C += A[32 x 16] B[16 x 32], lane l supplying
+// A[l % 32][8 (l / 32) + e] and B[8 (l / 32) + e][l % 32], e < 8 — one 16-byte chunk of
+// each operand row. A stage is four of them.
+template <>
+struct Mma<__bf16> {
+  __device__ static void stage(f32x16& c, const u32x4* sa, const u32x4* sb, int lane) {
+    const int r = lane & 31, h = lane >> 5;
 #pragma unroll
-  for (int ks = 0; ks < kKB; ks += Mma<T>::kStep) Mma<T>::run(c, a_row + ks, b_col + ks, lane);
+    for (int q = 0; q < 4; ++q) {
+      const int slot = (2 * q + h) ^ (r & 7);
+      const u32x4 x = sa[r * 8 + slot], y = sb[r * 8 + slot];
+      c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(&x),
+                                                  *reinterpret_cast<const bf16x8*>(&y), c, 0,
+                                                  0, 0);
+    }
+  }
+};
+// float32, v_mfma_f32_32x32x2_f32: C += A[32 x 2] B[2 x 32], lane l supplying one element
+// of k-slot l / 32. The 32 k of a stage are dealt as: MFMA step q takes element q % 4 of
+// chunk 2 (q / 4) + l / 32 — A and B lanes agree on it, so each k enters exactly once.
+template <>
+struct Mma<float> {
+  __device__ static void stage(f32x16& c, const u32x4* sa, const u32x4* sb, int lane) {
+    const int r = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int slot = (2 * p + h) ^ (r & 7);
+      const u32x4 x = sa[r * 8 + slot], y = sb[r * 8 + slot];
+      const float xa[4] = {__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z),
+                           __uint_as_float(x.w)};
+      const float yb[4] = {__uint_as_float(y.x), __uint_as_float(y.y), __uint_as_float(y.z),
+                           __uint_as_float(y.w)};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) c = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[e], yb[e], c, 0, 0, 0);
+    }
+  }
+};
+
+// Runs stages [0, n) of a tile: src(s, a, lda, b, ldb) names stage s's operands;
+// after stage s, done(s, c) sees the accumulator (and may reset it). Every iteration
+// fetches a stage — past the end, the last one again — so that the loads in flight are
+// the same on every path and the wait before each LDS store lets kDepth - 1 stages stay
+// in flight.
+template <typename T, class Src, class Done>
+__device__ inline void tile_product(StageLds& lds, f32x16& c, int n, Src src, Done done) {
+  if (n <= 0) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wi = wave >> 1, wj = wave & 1;
+  StageRegs ring[kDepth];
+  auto fetch = [&](int s, StageRegs& r) {
+    const char *a, *b;
+    int64_t lda, ldb;
+    src(s < n ? s : n - 1, a, lda, b, ldb);
+    stage_load(r, a, lda, b, ldb);
+  };
+#pragma unroll
+  for (int j = 0; j < kDepth; ++j) fetch(j, ring[j]);
+  stage_store(lds, 0, ring[0]);
+  fetch(kDepth, ring[0]);
   __syncthreads();
+  for (int s0 = 0; s0 < n; s0 += kDepth) {
+#pragma unroll
+    for (int j = 0; j < kDepth; ++j) {
+      const int s = s0 + j;
+      if (s >= n) return;  // (not break: the next trip's waits assume a whole trip)
+      Mma<T>::stage(c, &lds[s & 1][0][wi * 32 * 8], &lds[s & 1][1][wj * 32 * 8], lane);
+      done(s, c);
+      const int next = (j + 1) % kDepth;  // static once the loop is unrolled
+      stage_store(lds, (s + 1) & 1, ring[next]);
+      fetch(s + 1 + kDepth, ring[next]);
+      __syncthreads();
+    }
+  }
 }
 
 // Everything a launch reads, by value.
@@ -149,55 +220,102 @@ __global__ __launch_bounds__(kThreads) void rate_init_kernel(RateArgs a) {
 // S (synapse types) is a template parameter: each lane keeps 16 x S targets.
 template <typename T, int S>
 __global__ __launch_bounds__(kThreads) void rate_step_kernel(RateArgs a) {
-  __shared__ __align__(16) T sA[kTile][kKB + kPad];
-  __shared__ __align__(16) T sB[kTile][kKB + kPad];
+  __shared__ StageLds lds;
   const wt_rate_tables& tb = a.tab;
   const wt_rate_operand& op = a.op;
   const wt_rate_io& io = a.io;
   const int64_t N = tb.N, B = io.B, T_ = io.T, t = a.t;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wi = wave >> 1, wj = wave & 1;
   const int64_t n0 = (int64_t)blockIdx.x * kTile, b0 = (int64_t)blockIdx.y * kTile;
-  const T* rin = static_cast<const T*>(op.rin) + (t & 1) * op.B_pad * op.K_rec_pad;
-  const T* X = static_cast<const T*>(op.X) + t * op.B_pad * op.K_ff_pad;
-  const T* W = static_cast<const T*>(op.W);
+  const int64_t n = n0 + wj * 32 + (lane & 31);
+  constexpr int kStageK = kStageBytes / (int)sizeof(T);
+  const int64_t Kp = op.K_rec_pad + op.K_ff_pad;
+  const int rec_stages = (int)(op.K_rec_pad / kStageK);
+  const char* rin_b = reinterpret_cast<const char*>(
+      static_cast<const T*>(op.rin) + ((t & 1) * op.B_pad + b0) * op.K_rec_pad);
+  const char* X_b = reinterpret_cast<const char*>(
+      static_cast<const T*>(op.X) + (t * op.B_pad + b0) * op.K_ff_pad);
+  const char* Wt_n = reinterpret_cast<const char*>(static_cast<const T*>(op.Wt) + n0 * Kp);
+  const int64_t ldr = op.K_rec_pad * (int64_t)sizeof(T), ldx = op.K_ff_pad * (int64_t)sizeof(T);
+  const int64_t ldw = Kp * (int64_t)sizeof(T);
 
   float target[16][S];
 #pragma unroll
   for (int v = 0; v < 16; ++v)
 #pragma unroll
     for (int s = 0; s < S; ++s) target[v][s] = 0.0f;
-  const int wi = wave >> 1, wj = wave & 1;
-  const int64_t n = n0 + wj * 32 + (lane & 31);
 
-  for (int g = 0; g < op.n_seg; ++g) {
-    const int64_t k0 = op.seg[g][0], k1 = op.seg[g][1], path = op.seg[g][2];
-    const bool input = op.seg[g][3] != 0;
-    f32x16 c = {};
-    for (int64_t k = k0; k < k1; k += kKB) {  // W rows are absolute; the operands' k is not
-      if (input)
-        kblock<T, true>(c, sA, sB, X + b0 * op.K_ff_pad, op.K_ff_pad, k - op.K_rec_pad,
-                        W + n0, op.N_pad, k, wave, lane);
-      else
-        kblock<T, true>(c, sA, sB, rin + b0 * op.K_rec_pad, op.K_rec_pad, k, W + n0, op.N_pad, k,
-                        wave, lane);
+  // k runs over the recurrent rows (the rates of the step), then the input rows (the
+  // step's input); at the end of each pathway's segment its activation a_k enters the
+  // targets, in pathway order.
+  int g = 0;
+  auto src = [&](int s, const char*& pa, int64_t& lda, const char*& pb, int64_t& ldb) {
+    if (s < rec_stages) {
+      pa = rin_b + (int64_t)s * kStageBytes;
+      lda = ldr;
+    } else {
+      pa = X_b + (int64_t)(s - rec_stages) * kStageBytes;
+      lda = ldx;
     }
-    if (n < N) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t b = b0 + wi * 32 + out_row(v, lane);
-        if (b >= B) continue;
-        if (io.A_saved) io.A_saved[((path * B + b) * T_ + t) * N + n] = c[v];
-#pragma unroll
-        for (int s = 0; s < S; ++s)
-          target[v][s] = target[v][s] + c[v] * tb.jump[(path * N + n) * S + s];
-      }
-    }
+    pb = Wt_n + (int64_t)s * kStageBytes;
+    ldb = ldw;
+  };
+  // every segment's kernel scale for this tile's 64 targets, staged in LDS before the
+  // product (the fold at a segment's end then issues no global load)
+  __shared__ float s_jump[kMaxSeg][S][kTile];
+  for (int i = threadIdx.x; i < op.n_seg * S * kTile; i += kThreads) {
+    const int seg = i / (S * kTile), s = (i / kTile) % S, col = i % kTile;
+    const int64_t tn = n0 + col;
+    s_jump[seg][s][col] = tn < N ? tb.jump[((int64_t)op.seg[seg][2] * N + tn) * S + s] : 0.0f;
   }
+  const int col = wj * 32 + (lane & 31);
+  auto done = [&](int s, f32x16& c) {
+    if ((int64_t)(s + 1) * kStageK != op.seg[g][1]) return;
+    const int64_t path = op.seg[g][2];
+    float jump[S];
+#pragma unroll
+    for (int q = 0; q < S; ++q) jump[q] = s_jump[g][q][col];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t b = b0 + wi * 32 + out_row(v, lane);
+      if (io.A_saved && n < N && b < B) io.A_saved[((path * B + b) * T_ + t) * N + n] = c[v];
+#pragma unroll
+      for (int q = 0; q < S; ++q) target[v][q] = target[v][q] + c[v] * jump[q];
+    }
+    c = f32x16{};
+    ++g;
+  };
+  f32x16 c = {};
+  tile_product<T>(lds, c, (int)(Kp / kStageK), src, done);
   if (n >= N) return;
   const float beta = tb.beta[n], theta = tb.theta[n], gain = tb.gain[n];
   const int code = tb.nonlinearity[n];
   const int32_t pos = op.rpos ? op.rpos[n] : -1;
   T* rin_next = static_cast<T*>(op.rin) + ((t + 1) & 1) * op.B_pad * op.K_rec_pad;
+  const bool last = t + 1 == T_;
+  // With the voltages saved, the voltage entering this step is the saved one (written by
+  // the previous step, or the first rates' launch), and the state v is written only
+  // after the last step. A current whose decay is 0 is its target: its state is neither
+  // read nor, before the last step, written.
+  float decay[S], sign[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    decay[s] = tb.decay[s];
+    sign[s] = tb.sign[s];
+  }
+  // every load of the state first (16 trials), then the update and the stores
+  float v_in[16], I_prev[16][S];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int64_t b = b0 + wi * 32 + out_row(v, lane);
+    const bool ok = b < B;
+    const int64_t el = (b * T_ + t) * N + n;
+    v_in[v] = !ok ? 0.0f : io.v_saved ? io.v_saved[el] : io.v[b * N + n];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+      I_prev[v][s] = ok && decay[s] != 0.0f ? io.I[(b * S + s) * N + n] : 0.0f;
+  }
 #pragma unroll
   for (int v = 0; v < 16; ++v) {
     const int64_t b = b0 + wi * 32 + out_row(v, lane);
@@ -208,20 +326,20 @@ __global__ __launch_bounds__(kThreads) void rate_step_kernel(RateArgs a) {
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       if (io.target_saved) io.target_saved[el * S + s] = target[v][s];
-      const float d = tb.decay[s];
-      I[s] = d * io.I[(b * S + s) * N + n] + (1.0f - d) * target[v][s];
-      io.I[(b * S + s) * N + n] = I[s];
-      I_syn = I_syn + I[s] * tb.sign[s];
+      const float d = decay[s];
+      I[s] = d * I_prev[v][s] + (1.0f - d) * target[v][s];
+      if (d != 0.0f || last) io.I[(b * S + s) * N + n] = I[s];
+      I_syn = I_syn + I[s] * sign[s];
     }
-    const float vv = beta * io.v[b * N + n] + (1.0f - beta) * I_syn;
-    io.v[b * N + n] = vv;
+    const float vv = beta * v_in[v] + (1.0f - beta) * I_syn;
+    if (!io.v_saved || last) io.v[b * N + n] = vv;
     if (io.track_v && (io.track_b < 0 || io.track_b == b)) {
       const int64_t row = ((io.track_b < 0 ? b : 0) * T_ + t) * N + n;
       io.track_v[row] = vv;
 #pragma unroll
       for (int s = 0; s < S; ++s) io.track_I[row * S + s] = I[s];
     }
-    if (t + 1 < T_) {
+    if (!last) {
       const float r = gain * nonlin(code, vv - theta);
       io.out[el + N] = r;
       if (pos >= 0) rin_next[b * op.K_rec_pad + pos] = to_storage<T>(r);
@@ -305,11 +423,11 @@ __global__ __launch_bounds__(kThreads) void rate_back_elem_kernel(RateBackArgs a
 }
 
 // Reverse product of step t: d_rate[b, neuron of row j] = sum_n dL/da_k[b, n] W[j, n] for
-// the recurrent rows j of pathway k (the rates' gradient through the recurrence).
+// the recurrent rows j of pathway k (the rates' gradient through the recurrence). W's
+// rows are k-contiguous along n: the tile product's second operand as it is.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void rate_back_gemm_kernel(RateBackArgs a) {
-  __shared__ __align__(16) T sA[kTile][kKB + kPad];
-  __shared__ __align__(16) T sB[kTile][kKB + kPad];
+  __shared__ StageLds lds;
   const wt_rate_operand& op = a.op;
   const wt_rate_back_io& io = a.io;
   const int64_t N = a.tab.N, B = io.B;
@@ -320,11 +438,20 @@ __global__ __launch_bounds__(kThreads) void rate_back_gemm_kernel(RateBackArgs a
   for (int g = 0; g < op.n_seg; ++g)
     if (!op.seg[g][3] && j0 >= op.seg[g][0] && j0 < op.seg[g][1]) path = op.seg[g][2];
   if (path < 0) return;
-  const T* gA = static_cast<const T*>(io.gA_op) + (path * op.B_pad + b0) * op.N_pad;
-  const T* W = static_cast<const T*>(op.W) + j0 * op.N_pad;
+  constexpr int kStageK = kStageBytes / (int)sizeof(T);
+  const char* gA = reinterpret_cast<const char*>(static_cast<const T*>(io.gA_op) +
+                                                 (path * op.B_pad + b0) * op.N_pad);
+  const char* Wj = reinterpret_cast<const char*>(static_cast<const T*>(op.W) + j0 * op.N_pad);
+  const int64_t ld = op.N_pad * (int64_t)sizeof(T);
   f32x16 c = {};
-  for (int64_t k = 0; k < op.N_pad; k += kKB)
-    kblock<T, false>(c, sA, sB, gA, op.N_pad, k, W, op.N_pad, k, wave, lane);
+  tile_product<T>(
+      lds, c, (int)(op.N_pad / kStageK),
+      [&](int s, const char*& pa, int64_t& lda, const char*& pb, int64_t& ldb) {
+        pa = gA + (int64_t)s * kStageBytes;
+        pb = Wj + (int64_t)s * kStageBytes;
+        lda = ldb = ld;
+      },
+      [](int, f32x16&) {});
   const int wi = wave >> 1, wj = wave & 1;
   const int64_t j = j0 + wj * 32 + (lane & 31);
   const int32_t neuron = op.src_of[j];
@@ -385,13 +512,17 @@ static bool operand_ok(const wt_rate_tables* tb, const wt_rate_operand* op, int6
   if (op->B_pad < B || op->B_pad % kTile || op->N_pad < tb->N || op->N_pad % kTile) return false;
   if (op->K_rec_pad % kTile || op->K_ff_pad % kTile || op->n_seg < 0 || op->n_seg > kMaxSeg)
     return false;
+  int64_t end = 0;  // segments tile [0, K_rec_pad + K_ff_pad) in order
   for (int64_t g = 0; g < op->n_seg; ++g) {
     const int32_t* s = op->seg[g];
+    if (s[0] != end) return false;
+    end = s[1];
     const int64_t lo = s[3] ? op->K_rec_pad : 0, hi = s[3] ? op->K_rec_pad + op->K_ff_pad : op->K_rec_pad;
     if (s[0] < lo || s[1] > hi || s[0] >= s[1] || s[0] % kTile || s[1] % kTile) return false;
     if (s[2] < 0 || s[2] >= tb->K || (!s[3] && s[2] >= tb->K_rec)) return false;
   }
-  return op->W && (op->K_rec_pad == 0 || (op->rin && op->rpos));
+  if (end != op->K_rec_pad + op->K_ff_pad) return false;
+  return op->W && op->Wt && (op->K_rec_pad == 0 || (op->rin && op->rpos));
 }
 
 }  // namespace rate

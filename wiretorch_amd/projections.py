@@ -6,8 +6,8 @@ caching mode tells the network what may be computed once:
 * ``"fixed"`` (``FrozenProjection``): weights fixed at construction;
 * ``"scaling_factors"`` (``ScalingFactorProjection``): a fixed connectome times one
   learnt factor, which the network applies to the synaptic kernel;
-* ``"weights"`` (``FullRankProjection``, ``LowRankProjection``): weights assembled from
-  parameters on every call.
+* ``"weights"`` (``FullRankProjection``, ``LowRankProjection``, ``SignedProjection``):
+  weights assembled from parameters on every call.
 
 Follows ``src/wiretorch/network_simulators/projections.py:34-216`` (the same four
 classes, parameterisations and caching modes) and ``:340-392``
@@ -140,6 +140,37 @@ class LowRankProjection(Projection):
         return torch.exp(self.U @ self.V) * self.mask
 
 
+class SignedProjection(Projection):
+    """Learnt per-connection weights of either sign: ``weights * mask``.
+
+    The reference's projections are all non-negative (log-parameterised,
+    ``projections.py:121-216``) and take the sign from the synapse type; a rate network
+    with a dense signed matrix (a random ``N(0, g^2/N)`` recurrent matrix and its Gaussian
+    input weights) learns the weights themselves. ``mask`` (default: every connection)
+    fixes which entries exist."""
+
+    def __init__(self, init_weights, mask=None):
+        w = _float32(init_weights)
+        if w.ndim != 2:
+            raise ValueError(f"init_weights must be 2D, got shape {tuple(w.shape)}")
+        super().__init__(*w.shape)
+        self.weights = nn.Parameter(w.clone())
+        if mask is not None:
+            m = _float32(mask)
+            if m.shape != w.shape:
+                raise ValueError(f"mask shape {tuple(m.shape)} != {tuple(w.shape)}")
+            self.register_buffer("mask", m)
+        else:
+            self.mask = None
+
+    @property
+    def caching_mode(self) -> str:
+        return "weights"
+
+    def forward(self) -> torch.Tensor:
+        return self.weights if self.mask is None else self.weights * self.mask
+
+
 def _members(types: np.ndarray, names: list[str]) -> dict[str, np.ndarray]:
     return {name: np.flatnonzero(types == i) for i, name in enumerate(names)}
 
@@ -181,4 +212,6 @@ def projection_mask(projection: Projection) -> np.ndarray:
         tensor = getattr(projection, name, None)
         if isinstance(tensor, torch.Tensor):
             return tensor.detach().cpu().numpy() != 0
+    if isinstance(projection, SignedProjection):
+        return np.ones((projection.n_source, projection.n_target), dtype=bool)
     raise TypeError(f"unknown Projection subclass {type(projection).__name__}")

@@ -28,6 +28,29 @@ TILE = 64
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1}
 #: What the last differentiable forward tracked (returned with its ``Run``).
 _LAST_TRACKED = None
+#: When a dict, each launch sequence appends a pair of events recorded on its stream
+#: just before and after it, under its name: ``"forward"`` (``wt_rate_forward``, T
+#: steps), ``"backward"`` (``wt_rate_backward``) and ``"grad_w"`` (the weight and input
+#: gradient products). ``bench.py`` times the kernels with them.
+LAUNCH_EVENTS: dict | None = None
+
+
+class _timed:
+    """Records a pair of events around a block into ``LAUNCH_EVENTS[name]``."""
+
+    def __init__(self, name):
+        self.name = name
+
+    def __enter__(self):
+        if LAUNCH_EVENTS is not None:
+            self.start = torch.cuda.Event(enable_timing=True)
+            self.start.record()
+
+    def __exit__(self, *exc):
+        if LAUNCH_EVENTS is not None and exc[0] is None:
+            stop = torch.cuda.Event(enable_timing=True)
+            stop.record()
+            LAUNCH_EVENTS.setdefault(self.name, []).append((self.start, stop))
 
 
 def _pad(n: int) -> int:
@@ -65,6 +88,7 @@ class _Operand:
         if len(self.seg) > 16:
             raise NotImplementedError(f"at most 16 pathways, got {len(self.seg)}")
         self.W = W.to(dtype).contiguous()
+        self.Wt = self.W.T.contiguous()  # the forward product reads W along k
 
     def inputs(self, x: torch.Tensor, B_pad: int) -> torch.Tensor:
         """``(T, B_pad, K_ff_pad)``: every step's input in operand order."""
@@ -77,6 +101,7 @@ class _Operand:
     def abi(self, rin, X, B_pad: int) -> _lib.RateOperand:
         op = _lib.RateOperand()
         op.W = self.W.data_ptr()
+        op.Wt = self.Wt.data_ptr()
         op.rin = _lib.ptr(rin)
         op.X = _lib.ptr(X) if self.K_ff_pad else None
         op.rpos = self.rpos.data_ptr()
@@ -149,8 +174,9 @@ def _forward(L: _Plan, x, v, I, track, track_b, saved):
                      _lib.ptr(tI), track_b, _lib.ptr(v_s), _lib.ptr(I_s), _lib.ptr(tgt_s),
                      _lib.ptr(A_s))
     stream = torch.cuda.current_stream(dev).cuda_stream
-    _lib.check(_lib.load().wt_rate_forward(L.tables(), L.op.abi(rin, X, L.B_pad), io, stream),
-               "wt_rate_forward")
+    with _timed("forward"):
+        _lib.check(_lib.load().wt_rate_forward(L.tables(), L.op.abi(rin, X, L.B_pad), io,
+                                               stream), "wt_rate_forward")
     tracked = {"v": tv, "I": tI} if track else None
     return out, tracked
 
@@ -220,32 +246,42 @@ class _RateRun(torch.autograd.Function):
             *[_lib.ptr(acc[k]) for k in ("theta", "gain", "beta", "decay", "scale")],
         )  # fmt: skip
         stream = torch.cuda.current_stream(dev).cuda_stream
-        _lib.check(_lib.load().wt_rate_backward(L.tables(), L.op.abi(rin, None, L.B_pad), io,
-                                                stream), "wt_rate_backward")
+        with _timed("backward"):
+            _lib.check(_lib.load().wt_rate_backward(L.tables(), L.op.abi(rin, None, L.B_pad),
+                                                    io, stream), "wt_rate_backward")
         grad_scale = acc["scale"].sum(dim=1)[:K] if want_scale else None
         grad_theta = acc["theta"].sum(0) if want_theta else None
         grad_gain = acc["gain"].sum(0) if want_gain else None
         grad_beta = acc["beta"].sum(0) if want_beta else None
         grad_decay = acc["decay"].sum(dim=(0, 2)) if want_decay else None
         # weights and inputs: plain products with dL/da
-        grad_w = [None] * len(weights)
-        rec_pathways = [(rows, W) for (rows, W) in zip(L.rows_rec, weights[:L.K_rec])]
-        for k, (rows, W) in enumerate(rec_pathways):
-            if w_needs[k]:
-                r_k = out[:, :, rows].reshape(B * T, -1)
-                grad_w[k] = r_k.T @ grad_A[k].reshape(B * T, N)
-        grad_x = torch.zeros_like(x, dtype=torch.float32) if want_x else None
-        for j, (rows, W) in enumerate(zip(L.rows_ff, weights[L.K_rec:])):
-            k = L.K_rec + j
-            g = grad_A[k].reshape(B * T, N)
-            if w_needs[k]:
-                grad_w[k] = x.detach().float()[:, :, rows].reshape(B * T, -1).T @ g
-            if want_x:
-                grad_x[:, :, rows] += (g @ W.detach().float().T).reshape(B, T, -1)
+        with _timed("grad_w"):
+            grad_w, grad_x = _weight_and_input_grads(L, out, x, grad_A, weights, w_needs,
+                                                     want_x)
         if grad_x is not None:
             grad_x = grad_x.to(x.dtype)
         return (None, None, None, None, None, grad_scale, grad_x, grad_theta, grad_gain,
                 grad_beta, grad_decay, *grad_w)
+
+
+def _weight_and_input_grads(L: _Plan, out, x, grad_A, weights, w_needs, want_x):
+    """``dL/dW_k = sum_{b,t} pre ⊗ dL/da_k`` (``pre``: the source rates, or the inputs) and
+    ``dL/dx = dL/da_k W_k^T`` per input pathway (``rate/engine.py:367-376``), float32."""
+    B, T, N = L.B, L.T, L.N
+    grad_w = [None] * len(weights)
+    for k, rows in enumerate(L.rows_rec):
+        if w_needs[k]:
+            r_k = out[:, :, rows].reshape(B * T, -1)
+            grad_w[k] = r_k.T @ grad_A[k].reshape(B * T, N)
+    grad_x = torch.zeros_like(x, dtype=torch.float32) if want_x else None
+    for j, (rows, W) in enumerate(zip(L.rows_ff, weights[L.K_rec:])):
+        k = L.K_rec + j
+        g = grad_A[k].reshape(B * T, N)
+        if w_needs[k]:
+            grad_w[k] = x.detach().float()[:, :, rows].reshape(B * T, -1).T @ g
+        if want_x:
+            grad_x[:, :, rows] += (g @ W.detach().float().T).reshape(B, T, -1)
+    return grad_w, grad_x
 
 
 def simulate(v, I, x, drive, p, *, probabilities=False, track=False, track_batch_idx=None,

@@ -34,7 +34,7 @@ from wiretorch_amd.network import (
     Physiology,
     conductance_kernel,
 )
-from wiretorch_amd.projections import FrozenProjection, FullRankProjection
+from wiretorch_amd.projections import FrozenProjection, FullRankProjection, SignedProjection
 
 E_L = -65.0
 G_L = 10.0
@@ -276,3 +276,50 @@ def rest_state(B: int, N: int, S: int, device="cpu"):
     g = torch.zeros((B, 2, S, N), device=device).permute(0, 3, 1, 2)
     counter = torch.zeros((B, N), dtype=torch.int32, device=device)
     return v, g, counter
+
+
+# ---------------------------------------------------------------------------------
+# Dense rate network (configuration 4)
+# ---------------------------------------------------------------------------------
+
+RATE_TAU_MEM = 10.0
+RATE_DT = 1.0
+
+
+def dense_rate(N=4096, n_in=64, B=256, T=1000, g2=1.5, dt=RATE_DT, seed=4, input_seed=0,
+               storage_dtype=torch.bfloat16, learnt=True) -> Workload:
+    """A dense recurrent rate network: one cell type ``r`` (``tau_mem`` 10 ms, tanh),
+    synapses of time constant 0 (the voltage form: each step's current is that step's
+    input), recurrent weights ``N(0, g2 / N)``, ``n_in`` Gaussian inputs (``N(0, 1)`` per
+    step) through weights ``N(0, 1 / n_in)``. ``learnt``: both matrices are
+    ``SignedProjection`` parameters (else fixed). ``dt`` 1 ms (the configuration leaves it
+    open; 0.1 of ``tau_mem``)."""
+    from wiretorch_amd.rate import RecurrentRateNetwork
+
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((N, N)) * np.sqrt(g2 / N)).astype(np.float32)
+    w_in = (rng.standard_normal((n_in, N)) * np.sqrt(1.0 / n_in)).astype(np.float32)
+    x = np.random.default_rng([seed, input_seed]).standard_normal((B, T, n_in))
+    x = x.astype(np.float32)
+    make = SignedProjection if learnt else FrozenProjection
+    cells = [dict(name="r", cell_id=0, tau_mem=RATE_TAU_MEM, nonlinearity="tanh")]
+    synapses = [dict(name="exc", synapse_id=0, cell_id=0, tau_syn=0.0, type="excitatory")]
+    model = RecurrentRateNetwork(
+        dt=float(dt), rec_projections={("r", "r"): make(w)},
+        ff_projections={("input", "r"): make(w_in)},
+        cell_type_indices=np.zeros(N, dtype=np.int64),
+        cell_type_indices_FF=np.zeros(n_in, dtype=np.int64), cell_params=cells,
+        cell_params_FF=[dict(name="input", cell_id=0)], synapse_params=synapses,
+        synapse_params_FF=[dict(synapses[0], name="exc_in")], batch_size=B,
+        storage_dtype=storage_dtype,
+    )  # fmt: skip
+    structure = dict(w=w, w_in=w_in)
+    return Workload("dense_rate", x, structure, model=model, N=N, S=len(model.registry))
+
+
+def config4(seed=4, T=1000, B=256) -> Workload:
+    """N 4,096 tanh rate neurons, dense bf16 recurrent weights ``N(0, 1.5/N)``, 64-dim
+    Gaussian input through dense 4096 x 64 weights, batch 256, forward + backward."""
+    wl = dense_rate(B=B, T=T, seed=seed)
+    wl.name = "config4"
+    return wl
