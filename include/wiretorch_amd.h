@@ -199,19 +199,20 @@ typedef struct {
   int64_t N, S, K, K_rec;
 } wt_rate_tables;
 
-/* The matrix operands, zero-padded to whole 64 x 64 tiles. K dimension: recurrent rows
- * [0, K_rec_pad) (neurons, in segment order), then input rows [K_rec_pad, +K_ff_pad).
- * seg[g] = {first row, end row, pathway k, 1 for an input segment}, whole tiles. */
+/* The recurrent product's operand, zero-padded to whole 64 x 64 tiles: rows [0,
+ * K_rec_pad) are the recurrent pathways' source neurons, each pathway a segment of whole
+ * tiles, seg[g] = {first row, end row, pathway k, 0}, in pathway order. (The input
+ * pathways' products x[:, :, rows] W_k come precomputed for the whole call, as
+ * wt_rate_io.A_ff.) */
 typedef struct {
-  const void* W;          /* (K_rec_pad + K_ff_pad, N_pad), float32 or bfloat16 */
-  const void* Wt;         /* (N_pad, K_rec_pad + K_ff_pad): W transposed, same dtype */
+  const void* W;          /* (K_rec_pad, N_pad), float32 or bfloat16 */
+  const void* Wt;         /* (N_pad, K_rec_pad): W transposed, same dtype */
   void* rin;              /* [2][B_pad][K_rec_pad] rates of the step (zero-initialised) */
-  const void* X;          /* [T][B_pad][K_ff_pad] input of every step, rows permuted */
   const int32_t* rpos;    /* (N,) recurrent row of each neuron, or -1 */
   const int32_t* src_of;  /* (K_rec_pad,) neuron of each recurrent row, or -1 */
   int32_t seg[16][4];
-  int64_t n_seg, B_pad, N_pad, K_rec_pad, K_ff_pad;
-  int64_t dtype;          /* 0 float32, 1 bfloat16 (what W, rin, X hold) */
+  int64_t n_seg, B_pad, N_pad, K_rec_pad;
+  int64_t dtype;          /* 0 float32, 1 bfloat16 (what W, Wt, rin hold) */
 } wt_rate_operand;
 
 typedef struct {
@@ -226,6 +227,8 @@ typedef struct {
   float* I_saved;       /* (B, T, N, S) currents entering each step, or null */
   float* target_saved;  /* (B, T, N, S) or null */
   float* A_saved;       /* (K, B, T, N) activations, or null */
+  const float* A_ff;    /* (K - K_rec, B, T, N) input pathways' activations, float32 (null
+                         * when K == K_rec) */
 } wt_rate_io;
 
 /* wt_rate_forward — T steps of a rate network: per step one fused launch (MFMA product

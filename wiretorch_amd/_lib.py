@@ -63,9 +63,9 @@ class RateTables(ctypes.Structure):
 
 class RateOperand(ctypes.Structure):
     _fields_ = [
-        ("W", P), ("Wt", P), ("rin", P), ("X", P), ("rpos", P), ("src_of", P),
+        ("W", P), ("Wt", P), ("rin", P), ("rpos", P), ("src_of", P),
         ("seg", (ctypes.c_int32 * 4) * 16), ("n_seg", I64), ("B_pad", I64), ("N_pad", I64),
-        ("K_rec_pad", I64), ("K_ff_pad", I64), ("dtype", I64),
+        ("K_rec_pad", I64), ("dtype", I64),
     ]  # fmt: skip
 
 
@@ -73,7 +73,7 @@ class RateIO(ctypes.Structure):
     _fields_ = [
         ("B", I64), ("T", I64), ("v", P), ("I", P), ("out", P), ("track_v", P),
         ("track_I", P), ("track_b", I64), ("v_saved", P), ("I_saved", P),
-        ("target_saved", P), ("A_saved", P),
+        ("target_saved", P), ("A_saved", P), ("A_ff", P),
     ]  # fmt: skip
 
 

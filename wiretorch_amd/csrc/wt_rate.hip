@@ -11,9 +11,11 @@
 //   * a segment's partial product is the pathway's activation a_k; at the end of the
 //     segment it enters the synaptic targets, target[s] += a_k * scale_k * made_k[s], in
 //     pathway order as the reference sums them.
-// Tiles: 64 x 64 outputs per workgroup of four waves, each wave a 32 x 32 MFMA block;
-// k-blocks of 32 staged in LDS. MFMA: v_mfma_f32_32x32x2_f32 (float32 storage) or
-// v_mfma_f32_32x32x16_bf16 (bfloat16 storage), accumulating in float32.
+// Tiles: 64 x 64 outputs per workgroup of four waves; stages of 128 bytes of k staged
+// in LDS, each wave multiplying the whole tile over a quarter of every stage, the four
+// partials added in wave order at the end of each pathway's segment. MFMA:
+// v_mfma_f32_32x32x2_f32 (float32 storage) or v_mfma_f32_32x32x16_bf16 (bfloat16
+// storage), accumulating in float32.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -70,10 +72,11 @@ __device__ inline int out_row(int v, int lane) { return 8 * (v >> 2) + 4 * (lane
 //
 // A stage is 8 KB per operand: thread t fetches the 16-byte chunk t % 8 of rows t / 8 and
 // 32 + t / 8, so eight consecutive threads read one row's 128 bytes. Stages are fetched
-// kDepth ahead into a ring of registers and stored to one of two LDS buffers; one
-// barrier per stage. In LDS, chunk c of row r sits in slot c ^ (r % 8) of its row: the
-// MFMA operand reads (one 16-byte chunk per lane, rows r..r+7 at one chunk) then fall in
-// eight different slots — no bank conflicts.
+// kDepth ahead into a ring of registers and stored to LDS. In LDS, chunk c of row r sits
+// in slot c ^ sw(r) of its row, sw(r) = (r % 8) ^ ((r / 8) % 2): an MFMA operand read
+// (one 16-byte chunk per lane, one chunk of rows r..r+15 per 16 lanes) then covers all
+// 64 banks (256 bytes: row parity selects the half, the slot the 16 bytes) — and with
+// 32 banks, each 8 lanes' rows fall in 8 different slots — no bank conflicts.
 // ---------------------------------------------------------------------------------
 
 constexpr int kStageBytes = 128;
@@ -98,91 +101,178 @@ __device__ inline void stage_load(StageRegs& r, const char* a, int64_t lda, cons
   r.b[1] = gload16(b + (row + 32) * ldb + off);
 }
 
-// LDS: [buffer][operand][row * 8 + slot] in 16-byte units.
-typedef u32x4 StageLds[2][2][512];
+// LDS: [buffer][operand][row * 8 + slot] in 16-byte units; three buffers.
+constexpr int kBuffers = 3;
+typedef u32x4 StageLds[kBuffers][2][512];
+
+__device__ inline int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 __device__ inline void stage_store(StageLds& lds, int buf, const StageRegs& r) {
-  const int t = threadIdx.x, row = t >> 3, slot = (t & 7) ^ (row & 7);
+  const int t = threadIdx.x, row = t >> 3, slot = (t & 7) ^ swz(row);  // swz(row + 32) == swz(row)
   lds[buf][0][row * 8 + slot] = r.a[0];
   lds[buf][0][(row + 32) * 8 + slot] = r.a[1];
   lds[buf][1][row * 8 + slot] = r.b[0];
   lds[buf][1][(row + 32) * 8 + slot] = r.b[1];
 }
 
+// Each of the four waves multiplies the whole 64 x 64 tile (2 x 2 blocks of 32 x 32)
+// over its own quarter of every stage's k — chunks 2w and 2w + 1 (16 bytes each) for
+// wave w — and keeps its partial sums; `reduce` adds the four partials of a block in
+// wave order. Per stage a wave reads 4 chunks per lane from LDS (not 8, as a 32 x 32
+// block over the whole stage would), which halves the LDS reads per flop.
+typedef f32x16 Acc[2][2];
+
+// A wave's operands of one stage: rows r and 32 + r of A and of Bt at its chunk.
+struct Frag {
+  u32x4 x[2], y[2];
+};
+
+__device__ inline Frag frag_load(const u32x4 (&buf)[2][512], int wave, int lane) {
+  const int r = lane & 31, chunk = 2 * wave + (lane >> 5);
+  const int slot = chunk ^ swz(r);
+  Frag f;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    f.x[i] = buf[0][(32 * i + r) * 8 + slot];
+    f.y[i] = buf[1][(32 * i + r) * 8 + slot];
+  }
+  return f;
+}
+
 template <typename T>
 struct Mma;
 // bfloat16, v_mfma_f32_32x32x16_bf16: C += A[32 x 16] B[16 x 32], lane l supplying
-// A[l % 32][8 (l / 32) + e] and B[8 (l / 32) + e][l % 32], e < 8 — one 16-byte chunk of
-// each operand row. A stage is four of them.
+// A[l % 32][8 (l / 32) + e] and B[8 (l / 32) + e][l % 32], e < 8: the 16 k of the
+// wave's two chunks.
 template <>
 struct Mma<__bf16> {
-  __device__ static void stage(f32x16& c, const u32x4* sa, const u32x4* sb, int lane) {
-    const int r = lane & 31, h = lane >> 5;
+  __device__ static void stage(Acc& c, const Frag& f) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int slot = (2 * q + h) ^ (r & 7);
-      const u32x4 x = sa[r * 8 + slot], y = sb[r * 8 + slot];
-      c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(&x),
-                                                  *reinterpret_cast<const bf16x8*>(&y), c, 0,
-                                                  0, 0);
-    }
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        c[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            *reinterpret_cast<const bf16x8*>(&f.x[i]), *reinterpret_cast<const bf16x8*>(&f.y[j]),
+            c[i][j], 0, 0, 0);
   }
 };
 // float32, v_mfma_f32_32x32x2_f32: C += A[32 x 2] B[2 x 32], lane l supplying one element
-// of k-slot l / 32. The 32 k of a stage are dealt as: MFMA step q takes element q % 4 of
-// chunk 2 (q / 4) + l / 32 — A and B lanes agree on it, so each k enters exactly once.
+// of k-slot l / 32: MFMA step e takes element e of chunk 2w + l / 32 — A and B lanes
+// agree on it, so each of the wave's 8 k enters exactly once.
 template <>
 struct Mma<float> {
-  __device__ static void stage(f32x16& c, const u32x4* sa, const u32x4* sb, int lane) {
-    const int r = lane & 31, h = lane >> 5;
+  __device__ static void stage(Acc& c, const Frag& f) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int slot = (2 * p + h) ^ (r & 7);
-      const u32x4 x = sa[r * 8 + slot], y = sb[r * 8 + slot];
-      const float xa[4] = {__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z),
-                           __uint_as_float(x.w)};
-      const float yb[4] = {__uint_as_float(y.x), __uint_as_float(y.y), __uint_as_float(y.z),
-                           __uint_as_float(y.w)};
+    for (int e = 0; e < 4; ++e)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) c = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[e], yb[e], c, 0, 0, 0);
-    }
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          c[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(f.x[i][e]),
+                                                         __uint_as_float(f.y[j][e]), c[i][j], 0,
+                                                         0, 0);
   }
 };
 
-// Runs stages [0, n) of a tile: src(s, a, lda, b, ldb) names stage s's operands;
-// after stage s, done(s, c) sees the accumulator (and may reset it). Every iteration
-// fetches a stage — past the end, the last one again — so that the loads in flight are
-// the same on every path and the wait before each LDS store lets kDepth - 1 stages stay
-// in flight.
-template <typename T, class Src, class Done>
-__device__ inline void tile_product(StageLds& lds, f32x16& c, int n, Src src, Done done) {
-  if (n <= 0) return;
+// LDS for `reduce`: [block][wave][v / 4][lane] in 16-byte units (64 KB).
+typedef u32x4 ReduceLds[4][4][4][64];
+
+// The sum over the four waves (in wave order) of block (w / 2, w % 2) of the tile, for
+// the wave w that owns it; every wave's partials are then zero. All four partials of a
+// block pass through LDS. A workgroup barrier inside: every wave calls it at the same
+// point.
+__device__ inline f32x16 reduce(Acc& c, ReduceLds& red, int wave, int lane) {
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk) {
+    const f32x16& p = c[blk >> 1][blk & 1];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      red[blk][wave][q][lane] = u32x4{__float_as_uint(p[4 * q]), __float_as_uint(p[4 * q + 1]),
+                                      __float_as_uint(p[4 * q + 2]), __float_as_uint(p[4 * q + 3])};
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) c[i][j] = f32x16{};
+  __syncthreads();
+  f32x16 sum = {};
+#pragma unroll
+  for (int w = 0; w < 4; ++w)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u32x4 x = red[wave][w][q][lane];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum[4 * q + e] = sum[4 * q + e] + __uint_as_float(x[e]);
+    }
+  return sum;
+}
+
+// Runs a tile's product over G segments of stages (count(g) >= 1 stages each; src(g, l,
+// a, lda, b, ldb) names stage l of segment g), calling fold(g, c) with the partial sums
+// after each segment (fold may reduce them).
+//
+// Pipeline: stage s + 2 is stored to LDS while the MFMAs of stage s run on operands read
+// from LDS during stage s - 1, and stage s + 1's operands are read meanwhile (three LDS
+// buffers, one barrier per stage); global loads run kDepth stages ahead of the store,
+// across segment ends. Each segment runs a whole number of kDepth-stage trips with no
+// exit inside: its stages past count(g) (at most kDepth - 1) load, store and synchronise
+// like the others — fetching a real stage again — but multiply zeros. The loads in
+// flight are then the same on every path, each store's wait lets kDepth - 1 stages stay
+// in flight, and the fold runs between trips, outside the unrolled loop.
+template <typename T, class Count, class Src, class Fold>
+__device__ inline void tile_product(StageLds& lds, Acc& c, int G, Count count, Src src,
+                                    Fold fold) {
+  if (G <= 0) return;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int wi = wave >> 1, wj = wave & 1;
   StageRegs ring[kDepth];
-  auto fetch = [&](int s, StageRegs& r) {
+  // fetch cursor over the padded stage sequence
+  int fg = 0, fl = 0, fn = count(0);
+  const int last_g = G - 1, last_l = count(G - 1) - 1;
+  auto fetch = [&](StageRegs& r) {
     const char *a, *b;
     int64_t lda, ldb;
-    src(s < n ? s : n - 1, a, lda, b, ldb);
+    if (fg < G)
+      src(fg, fl < fn ? fl : fn - 1, a, lda, b, ldb);
+    else
+      src(last_g, last_l, a, lda, b, ldb);
     stage_load(r, a, lda, b, ldb);
+    if (fg < G && ++fl == (fn + kDepth - 1) / kDepth * kDepth) {
+      fl = 0;
+      if (++fg < G) fn = count(fg);
+    }
   };
 #pragma unroll
-  for (int j = 0; j < kDepth; ++j) fetch(j, ring[j]);
+  for (int j = 0; j < kDepth; ++j) fetch(ring[j]);
   stage_store(lds, 0, ring[0]);
-  fetch(kDepth, ring[0]);
+  fetch(ring[0]);
+  stage_store(lds, 1, ring[1]);
+  fetch(ring[1]);
   __syncthreads();
-  for (int s0 = 0; s0 < n; s0 += kDepth) {
+  Frag cur = frag_load(lds[0], wave, lane);
+  int buf = 0;  // LDS buffer of the stage being multiplied
+  for (int g = 0; g < G; ++g) {
+    const int n = count(g), trips = (n + kDepth - 1) / kDepth;
+    for (int trip = 0; trip < trips; ++trip) {
 #pragma unroll
-    for (int j = 0; j < kDepth; ++j) {
-      const int s = s0 + j;
-      if (s >= n) return;  // (not break: the next trip's waits assume a whole trip)
-      Mma<T>::stage(c, &lds[s & 1][0][wi * 32 * 8], &lds[s & 1][1][wj * 32 * 8], lane);
-      done(s, c);
-      const int next = (j + 1) % kDepth;  // static once the loop is unrolled
-      stage_store(lds, (s + 1) & 1, ring[next]);
-      fetch(s + 1 + kDepth, ring[next]);
-      __syncthreads();
+      for (int j = 0; j < kDepth; ++j) {
+        const int l = trip * kDepth + j;
+        const int buf1 = buf == kBuffers - 1 ? 0 : buf + 1;
+        const int buf2 = buf1 == kBuffers - 1 ? 0 : buf1 + 1;
+        const Frag nxt = frag_load(lds[buf1], wave, lane);
+        if (l >= n) {  // a padding stage: A is zero
+#pragma unroll
+          for (int i = 0; i < 2; ++i) cur.x[i] = u32x4{0u, 0u, 0u, 0u};
+        }
+        Mma<T>::stage(c, cur);
+        const int slot = (j + 2) % kDepth;  // static once the loop is unrolled
+        stage_store(lds, buf2, ring[slot]);
+        fetch(ring[slot]);
+        __syncthreads();
+        cur = nxt;
+        buf = buf1;
+      }
     }
+    fold(g, c);
   }
 }
 
@@ -216,8 +306,9 @@ __global__ __launch_bounds__(kThreads) void rate_init_kernel(RateArgs a) {
     for (int64_t s = 0; s < S; ++s) io.I_saved[((b * T_) * N + n) * S + s] = io.I[(b * S + s) * N + n];
 }
 
-// Step t: a = [rin | X_t] W by segments, then the currents, voltages and next rates.
-// S (synapse types) is a template parameter: each lane keeps 16 x S targets.
+// Step t: a_k = r W_k for the recurrent pathways (segments of rin W), the input
+// pathways' a_k from A_ff, then the currents, voltages and next rates. S (synapse
+// types) is a template parameter: each lane keeps 16 x S targets.
 template <typename T, int S>
 __global__ __launch_bounds__(kThreads) void rate_step_kernel(RateArgs a) {
   __shared__ StageLds lds;
@@ -230,15 +321,11 @@ __global__ __launch_bounds__(kThreads) void rate_step_kernel(RateArgs a) {
   const int64_t n0 = (int64_t)blockIdx.x * kTile, b0 = (int64_t)blockIdx.y * kTile;
   const int64_t n = n0 + wj * 32 + (lane & 31);
   constexpr int kStageK = kStageBytes / (int)sizeof(T);
-  const int64_t Kp = op.K_rec_pad + op.K_ff_pad;
-  const int rec_stages = (int)(op.K_rec_pad / kStageK);
   const char* rin_b = reinterpret_cast<const char*>(
       static_cast<const T*>(op.rin) + ((t & 1) * op.B_pad + b0) * op.K_rec_pad);
-  const char* X_b = reinterpret_cast<const char*>(
-      static_cast<const T*>(op.X) + (t * op.B_pad + b0) * op.K_ff_pad);
-  const char* Wt_n = reinterpret_cast<const char*>(static_cast<const T*>(op.Wt) + n0 * Kp);
-  const int64_t ldr = op.K_rec_pad * (int64_t)sizeof(T), ldx = op.K_ff_pad * (int64_t)sizeof(T);
-  const int64_t ldw = Kp * (int64_t)sizeof(T);
+  const char* Wt_n =
+      reinterpret_cast<const char*>(static_cast<const T*>(op.Wt) + n0 * op.K_rec_pad);
+  const int64_t ld = op.K_rec_pad * (int64_t)sizeof(T);
 
   float target[16][S];
 #pragma unroll
@@ -246,23 +333,9 @@ __global__ __launch_bounds__(kThreads) void rate_step_kernel(RateArgs a) {
 #pragma unroll
     for (int s = 0; s < S; ++s) target[v][s] = 0.0f;
 
-  // k runs over the recurrent rows (the rates of the step), then the input rows (the
-  // step's input); at the end of each pathway's segment its activation a_k enters the
-  // targets, in pathway order.
-  int g = 0;
-  auto src = [&](int s, const char*& pa, int64_t& lda, const char*& pb, int64_t& ldb) {
-    if (s < rec_stages) {
-      pa = rin_b + (int64_t)s * kStageBytes;
-      lda = ldr;
-    } else {
-      pa = X_b + (int64_t)(s - rec_stages) * kStageBytes;
-      lda = ldx;
-    }
-    pb = Wt_n + (int64_t)s * kStageBytes;
-    ldb = ldw;
-  };
-  // every segment's kernel scale for this tile's 64 targets, staged in LDS before the
-  // product (the fold at a segment's end then issues no global load)
+  // k runs over the recurrent pathways' segments in order; at the end of each segment its
+  // activation a_k enters the targets. Every segment's kernel scale for this tile's 64 targets, staged in LDS before the
+  // product (the fold then issues no global load)
   __shared__ float s_jump[kMaxSeg][S][kTile];
   for (int i = threadIdx.x; i < op.n_seg * S * kTile; i += kThreads) {
     const int seg = i / (S * kTile), s = (i / kTile) % S, col = i % kTile;
@@ -270,29 +343,64 @@ __global__ __launch_bounds__(kThreads) void rate_step_kernel(RateArgs a) {
     s_jump[seg][s][col] = tn < N ? tb.jump[((int64_t)op.seg[seg][2] * N + tn) * S + s] : 0.0f;
   }
   const int col = wj * 32 + (lane & 31);
-  auto done = [&](int s, f32x16& c) {
-    if ((int64_t)(s + 1) * kStageK != op.seg[g][1]) return;
+  auto count = [&](int g) { return (int)((op.seg[g][1] - op.seg[g][0]) / kStageK); };
+  auto src = [&](int g, int l, const char*& pa, int64_t& lda, const char*& pb, int64_t& ldb) {
+    const int64_t off = (op.seg[g][0] / kStageK + l) * (int64_t)kStageBytes;
+    pa = rin_b + off;
+    pb = Wt_n + off;
+    lda = ldb = ld;
+  };
+  __shared__ ReduceLds red;
+  auto fold = [&](int g, Acc& c) {
     const int64_t path = op.seg[g][2];
+    const f32x16 act = reduce(c, red, wave, lane);  // a_k of this wave's 32 x 32 block
     float jump[S];
 #pragma unroll
     for (int q = 0; q < S; ++q) jump[q] = s_jump[g][q][col];
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int64_t b = b0 + wi * 32 + out_row(v, lane);
-      if (io.A_saved && n < N && b < B) io.A_saved[((path * B + b) * T_ + t) * N + n] = c[v];
+      if (io.A_saved && n < N && b < B) io.A_saved[((path * B + b) * T_ + t) * N + n] = act[v];
 #pragma unroll
-      for (int q = 0; q < S; ++q) target[v][q] = target[v][q] + c[v] * jump[q];
+      for (int q = 0; q < S; ++q) target[v][q] = target[v][q] + act[v] * jump[q];
     }
-    c = f32x16{};
-    ++g;
   };
-  f32x16 c = {};
-  tile_product<T>(lds, c, (int)(Kp / kStageK), src, done);
+  Acc c = {};
+  tile_product<T>(lds, c, (int)op.n_seg, count, src, fold);
   if (n >= N) return;
+  // The state update of the lane's 16 trials, in three phases — every load, then the
+  // arithmetic in registers, then every store — so that no store sits between two loads
+  // (the pointers do not alias).
+  bool ok[16];
+  int64_t el[16];  // (b, t, n) in the (B, T, N) arrays
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int64_t b = b0 + wi * 32 + out_row(v, lane);
+    ok[v] = b < B;
+    el[v] = ((ok[v] ? b : 0) * T_ + t) * N + n;
+  }
+  // the input pathways' activations, after the recurrent ones (pathway order)
+  for (int64_t k = tb.K_rec; k < tb.K; ++k) {
+    const float* __restrict__ A = io.A_ff + (k - tb.K_rec) * B * T_ * N;
+    float act[16], jump[S];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) act[v] = ok[v] ? A[el[v]] : 0.0f;
+#pragma unroll
+    for (int q = 0; q < S; ++q) jump[q] = tb.jump[(k * N + n) * S + q];
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+#pragma unroll
+      for (int q = 0; q < S; ++q) target[v][q] = target[v][q] + act[v] * jump[q];
+    if (io.A_saved) {
+      float* __restrict__ As = io.A_saved + k * B * T_ * N;
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        if (ok[v]) As[el[v]] = act[v];
+    }
+  }
   const float beta = tb.beta[n], theta = tb.theta[n], gain = tb.gain[n];
   const int code = tb.nonlinearity[n];
   const int32_t pos = op.rpos ? op.rpos[n] : -1;
-  T* rin_next = static_cast<T*>(op.rin) + ((t + 1) & 1) * op.B_pad * op.K_rec_pad;
   const bool last = t + 1 == T_;
   // With the voltages saved, the voltage entering this step is the saved one (written by
   // the previous step, or the first rates' launch), and the state v is written only
@@ -304,49 +412,67 @@ __global__ __launch_bounds__(kThreads) void rate_step_kernel(RateArgs a) {
     decay[s] = tb.decay[s];
     sign[s] = tb.sign[s];
   }
-  // every load of the state first (16 trials), then the update and the stores
-  float v_in[16], I_prev[16][S];
+  const float* __restrict__ v_saved_in = io.v_saved;
+  const float* __restrict__ v_state_in = io.v;
+  const float* __restrict__ I_in = io.I;
+  float vv[16], I[16][S];
 #pragma unroll
   for (int v = 0; v < 16; ++v) {
     const int64_t b = b0 + wi * 32 + out_row(v, lane);
-    const bool ok = b < B;
-    const int64_t el = (b * T_ + t) * N + n;
-    v_in[v] = !ok ? 0.0f : io.v_saved ? io.v_saved[el] : io.v[b * N + n];
+    vv[v] = !ok[v] ? 0.0f : v_saved_in ? v_saved_in[el[v]] : v_state_in[b * N + n];
 #pragma unroll
     for (int s = 0; s < S; ++s)
-      I_prev[v][s] = ok && decay[s] != 0.0f ? io.I[(b * S + s) * N + n] : 0.0f;
+      I[v][s] = ok[v] && decay[s] != 0.0f ? I_in[(b * S + s) * N + n] : 0.0f;
   }
+  float r[16];
 #pragma unroll
   for (int v = 0; v < 16; ++v) {
-    const int64_t b = b0 + wi * 32 + out_row(v, lane);
-    if (b >= B) continue;
-    const int64_t el = (b * T_ + t) * N + n;
-    float I[S];
     float I_syn = 0.0f;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      if (io.target_saved) io.target_saved[el * S + s] = target[v][s];
       const float d = decay[s];
-      I[s] = d * I_prev[v][s] + (1.0f - d) * target[v][s];
-      if (d != 0.0f || last) io.I[(b * S + s) * N + n] = I[s];
-      I_syn = I_syn + I[s] * sign[s];
+      I[v][s] = d * I[v][s] + (1.0f - d) * target[v][s];
+      I_syn = I_syn + I[v][s] * sign[s];
     }
-    const float vv = beta * v_in[v] + (1.0f - beta) * I_syn;
-    if (!io.v_saved || last) io.v[b * N + n] = vv;
-    if (io.track_v && (io.track_b < 0 || io.track_b == b)) {
-      const int64_t row = ((io.track_b < 0 ? b : 0) * T_ + t) * N + n;
-      io.track_v[row] = vv;
+    vv[v] = beta * vv[v] + (1.0f - beta) * I_syn;
+    r[v] = gain * nonlin(code, vv[v] - theta);
+  }
+  float* __restrict__ out = io.out;
+  float* __restrict__ v_saved_out = io.v_saved;
+  float* __restrict__ v_state = io.v;
+  float* __restrict__ I_state = io.I;
+  T* __restrict__ rin_next = static_cast<T*>(op.rin) + ((t + 1) & 1) * op.B_pad * op.K_rec_pad;
 #pragma unroll
-      for (int s = 0; s < S; ++s) io.track_I[row * S + s] = I[s];
-    }
+  for (int v = 0; v < 16; ++v) {
+    if (!ok[v]) continue;
+    const int64_t b = b0 + wi * 32 + out_row(v, lane);
     if (!last) {
-      const float r = gain * nonlin(code, vv - theta);
-      io.out[el + N] = r;
-      if (pos >= 0) rin_next[b * op.K_rec_pad + pos] = to_storage<T>(r);
-      if (io.v_saved) io.v_saved[el + N] = vv;
-      if (io.I_saved)
+      out[el[v] + N] = r[v];
+      if (pos >= 0) rin_next[b * op.K_rec_pad + pos] = to_storage<T>(r[v]);
+      if (v_saved_out) v_saved_out[el[v] + N] = vv[v];
+    }
+    if (!v_saved_out || last) v_state[b * N + n] = vv[v];
 #pragma unroll
-        for (int s = 0; s < S; ++s) io.I_saved[(el + N) * S + s] = I[s];
+    for (int s = 0; s < S; ++s)
+      if (decay[s] != 0.0f || last) I_state[(b * S + s) * N + n] = I[v][s];
+  }
+  // what is saved or tracked (not on the plain forward path)
+  if (io.target_saved || io.I_saved || io.track_v) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      if (!ok[v]) continue;
+      const int64_t b = b0 + wi * 32 + out_row(v, lane);
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        if (io.target_saved) io.target_saved[el[v] * S + s] = target[v][s];
+        if (io.I_saved && !last) io.I_saved[(el[v] + N) * S + s] = I[v][s];
+      }
+      if (io.track_v && (io.track_b < 0 || io.track_b == b)) {
+        const int64_t row = ((io.track_b < 0 ? b : 0) * T_ + t) * N + n;
+        io.track_v[row] = vv[v];
+#pragma unroll
+        for (int s = 0; s < S; ++s) io.track_I[row * S + s] = I[v][s];
+      }
     }
   }
 }
@@ -370,7 +496,11 @@ __global__ __launch_bounds__(kThreads) void rate_back_elem_kernel(RateBackArgs a
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= B * N) return;
   const int64_t b = idx / N, n = idx - b * N;
-  float lv = io.lam_v[idx];
+  // every pointer below addresses its own array (no aliasing): the loads of a phase can
+  // all be in flight before its stores
+  float* __restrict__ lam_v = io.lam_v;
+  float* __restrict__ lam_I = io.lam_I;
+  float lv = lam_v[idx];
   if (a.t_rate >= 0) {  // (C): v_u enters r_u; lv holds beta dL/dv_{u+1} already
     const int64_t u = a.t_rate;
     const int64_t el = (b * T_ + u) * N + n;
@@ -387,7 +517,15 @@ __global__ __launch_bounds__(kThreads) void rate_back_elem_kernel(RateBackArgs a
     const int64_t t = a.t;
     const int64_t el = (b * T_ + t) * N + n;
     const float beta = tb.beta[n];
-    float dtarget[kMaxS];
+    // a current whose decay is 0 passes no adjoint back in time: lam_I stays 0, unread
+    float dtarget[kMaxS], lamI[kMaxS], decay[kMaxS], sign[kMaxS];
+#pragma unroll
+    for (int s = 0; s < kMaxS; ++s) {
+      if (s >= S) break;
+      decay[s] = tb.decay[s];
+      sign[s] = tb.sign[s];
+      lamI[s] = decay[s] != 0.0f ? lam_I[(b * S + s) * N + n] : 0.0f;
+    }
     float I_next_syn = 0.0f;
 #pragma unroll
     for (int s = 0; s < kMaxS; ++s) {
@@ -395,31 +533,53 @@ __global__ __launch_bounds__(kThreads) void rate_back_elem_kernel(RateBackArgs a
       if (io.acc_beta) {
         const float I_next =
             t + 1 < T_ ? io.I_saved[(el + N) * S + s] : io.I_final[(b * S + s) * N + n];
-        I_next_syn = I_next_syn + I_next * tb.sign[s];
+        I_next_syn = I_next_syn + I_next * sign[s];
       }
-      const float dI = io.lam_I[(b * S + s) * N + n] + lv * (1.0f - beta) * tb.sign[s];
-      const float d = tb.decay[s];
-      dtarget[s] = dI * (1.0f - d);
-      io.lam_I[(b * S + s) * N + n] = dI * d;
+      const float dI = lamI[s] + lv * (1.0f - beta) * sign[s];
+      dtarget[s] = dI * (1.0f - decay[s]);
+      lamI[s] = dI * decay[s];
       if (io.acc_decay)
         io.acc_decay[(b * S + s) * N + n] += dI * (io.I_saved[el * S + s] - io.target_saved[el * S + s]);
     }
     if (io.acc_beta) io.acc_beta[idx] += lv * (io.v_saved[el] - I_next_syn);
-    for (int64_t k = 0; k < K; ++k) {
-      float g = 0.0f;
-      for (int64_t s = 0; s < S; ++s) g = g + dtarget[s] * tb.jump[(k * N + n) * S + s];
-      io.grad_A[((k * B + b) * T_ + t) * N + n] = g;
-      if (k < tb.K_rec)
-        static_cast<T*>(io.gA_op)[(k * a.op.B_pad + b) * a.op.N_pad + n] = to_storage<T>(g);
-      if (io.acc_scale) {
-        float m = 0.0f;
-        for (int64_t s = 0; s < S; ++s) m = m + dtarget[s] * tb.made[k * S + s];
-        io.acc_scale[(k * B + b) * N + n] += m * io.A_saved[((k * B + b) * T_ + t) * N + n];
+    // dL/da_k, eight pathways at a time: their kernel scales first, then the stores
+    float* __restrict__ grad_A = io.grad_A;
+    T* __restrict__ gA_op = static_cast<T*>(io.gA_op);
+    for (int64_t k0 = 0; k0 < K; k0 += 8) {
+      float g[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        g[i] = 0.0f;
+        if (k0 + i >= K) continue;
+#pragma unroll
+        for (int s = 0; s < kMaxS; ++s) {
+          if (s >= S) break;
+          g[i] = g[i] + dtarget[s] * tb.jump[((k0 + i) * N + n) * S + s];
+        }
       }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int64_t k = k0 + i;
+        if (k >= K) break;
+        grad_A[((k * B + b) * T_ + t) * N + n] = g[i];
+        if (k < tb.K_rec) gA_op[(k * a.op.B_pad + b) * a.op.N_pad + n] = to_storage<T>(g[i]);
+      }
+      if (io.acc_scale) {
+        for (int64_t k = k0; k < K && k < k0 + 8; ++k) {
+          float m = 0.0f;
+          for (int64_t s = 0; s < S; ++s) m = m + dtarget[s] * tb.made[k * S + s];
+          io.acc_scale[(k * B + b) * N + n] += m * io.A_saved[((k * B + b) * T_ + t) * N + n];
+        }
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < kMaxS; ++s) {
+      if (s >= S) break;
+      if (decay[s] != 0.0f) lam_I[(b * S + s) * N + n] = lamI[s];
     }
     lv = lv * beta;  // dL/dv_t before its rate's term
   }
-  io.lam_v[idx] = lv;
+  lam_v[idx] = lv;
 }
 
 // Reverse product of step t: d_rate[b, neuron of row j] = sum_n dL/da_k[b, n] W[j, n] for
@@ -443,15 +603,17 @@ __global__ __launch_bounds__(kThreads) void rate_back_gemm_kernel(RateBackArgs a
                                                  (path * op.B_pad + b0) * op.N_pad);
   const char* Wj = reinterpret_cast<const char*>(static_cast<const T*>(op.W) + j0 * op.N_pad);
   const int64_t ld = op.N_pad * (int64_t)sizeof(T);
-  f32x16 c = {};
+  __shared__ ReduceLds red;
+  Acc acc = {};
   tile_product<T>(
-      lds, c, (int)(op.N_pad / kStageK),
-      [&](int s, const char*& pa, int64_t& lda, const char*& pb, int64_t& ldb) {
-        pa = gA + (int64_t)s * kStageBytes;
-        pb = Wj + (int64_t)s * kStageBytes;
+      lds, acc, 1, [&](int) { return (int)(op.N_pad / kStageK); },
+      [&](int, int l, const char*& pa, int64_t& lda, const char*& pb, int64_t& ldb) {
+        pa = gA + (int64_t)l * kStageBytes;
+        pb = Wj + (int64_t)l * kStageBytes;
         lda = ldb = ld;
       },
-      [](int, f32x16&) {});
+      [](int, Acc&) {});
+  const f32x16 c = reduce(acc, red, wave, lane);
   const int wi = wave >> 1, wj = wave & 1;
   const int64_t j = j0 + wj * 32 + (lane & 31);
   const int32_t neuron = op.src_of[j];
@@ -510,19 +672,16 @@ static hipError_t backward_impl(const RateBackArgs& base, hipStream_t stream) {
 static bool operand_ok(const wt_rate_tables* tb, const wt_rate_operand* op, int64_t B) {
   if (op->dtype != 0 && op->dtype != 1) return false;
   if (op->B_pad < B || op->B_pad % kTile || op->N_pad < tb->N || op->N_pad % kTile) return false;
-  if (op->K_rec_pad % kTile || op->K_ff_pad % kTile || op->n_seg < 0 || op->n_seg > kMaxSeg)
-    return false;
-  int64_t end = 0;  // segments tile [0, K_rec_pad + K_ff_pad) in order
+  if (op->K_rec_pad % kTile || op->n_seg < 0 || op->n_seg > kMaxSeg) return false;
+  int64_t end = 0;  // segments tile [0, K_rec_pad) in order, one per recurrent pathway
   for (int64_t g = 0; g < op->n_seg; ++g) {
     const int32_t* s = op->seg[g];
-    if (s[0] != end) return false;
+    if (s[0] != end || s[1] <= s[0] || s[1] % kTile || s[3] != 0) return false;
+    if (s[2] < 0 || s[2] >= tb->K_rec) return false;
     end = s[1];
-    const int64_t lo = s[3] ? op->K_rec_pad : 0, hi = s[3] ? op->K_rec_pad + op->K_ff_pad : op->K_rec_pad;
-    if (s[0] < lo || s[1] > hi || s[0] >= s[1] || s[0] % kTile || s[1] % kTile) return false;
-    if (s[2] < 0 || s[2] >= tb->K || (!s[3] && s[2] >= tb->K_rec)) return false;
   }
-  if (end != op->K_rec_pad + op->K_ff_pad) return false;
-  return op->W && op->Wt && (op->K_rec_pad == 0 || (op->rin && op->rpos));
+  if (end != op->K_rec_pad) return false;
+  return op->K_rec_pad == 0 || (op->W && op->Wt && op->rin && op->rpos);
 }
 
 }  // namespace rate
@@ -536,7 +695,7 @@ extern "C" int wt_rate_forward(const wt_rate_tables* tab, const wt_rate_operand*
   if (tab->S < 1 || tab->S > kMaxS || tab->K < 0 || tab->K_rec < 0 || tab->K_rec > tab->K)
     return hipErrorInvalidValue;
   if (!operand_ok(tab, op, io->B)) return hipErrorInvalidValue;
-  if (op->K_ff_pad > 0 && !op->X) return hipErrorInvalidValue;
+  if (tab->K > tab->K_rec && !io->A_ff) return hipErrorInvalidValue;
   if ((io->track_v != nullptr) != (io->track_I != nullptr)) return hipErrorInvalidValue;
   if (io->B * tab->N == 0 || io->T == 0) return hipSuccess;
   RateArgs a = {};

@@ -2,11 +2,13 @@
 ``rate/engine.py`` (and of ``rate/dynamics.simulate``, ``rate/dynamics.py:109-160``),
 running ``wt_rate_forward`` / ``wt_rate_backward`` of ``libwiretorch_amd.so``.
 
-Per call the pathways' weights are laid out as one zero-padded operand (recurrent rows
-first, then input rows, every pathway a segment of whole 64-row tiles), cached while the
-weight tensors are unchanged. ``p.storage_dtype`` selects what the products multiply in:
-float32 (``v_mfma_f32_32x32x2_f32``) or bfloat16 (``v_mfma_f32_32x32x16_bf16``); state
-and accumulation stay float32.
+Per call the recurrent pathways' weights are laid out as one zero-padded operand (every
+pathway a segment of whole 64-row tiles, and its transpose), cached while the weight
+tensors are unchanged; the input pathways' activations ``x[:, :, rows] @ W_k`` are one
+product for the whole call, before the steps, as in the reference. ``p.storage_dtype``
+selects what the products multiply in: float32 (``v_mfma_f32_32x32x2_f32``) or bfloat16
+(``v_mfma_f32_32x32x16_bf16``, and operands rounded to bfloat16 for the input product);
+state and accumulation stay float32.
 
 Gradients (``_RateRun``, the counterpart of ``rate/engine.py:336-383``) flow to the
 inputs, every pathway's weights and kernel scale, and ``theta``, ``gain``, ``beta`` and
@@ -58,15 +60,14 @@ def _pad(n: int) -> int:
 
 
 class _Operand:
-    """The padded weight operand of one drive and what indexes it."""
+    """The padded recurrent weight operand of one drive and what indexes it."""
 
-    def __init__(self, recurrent, feedforward, N: int, dtype, device):
+    def __init__(self, recurrent, N: int, dtype, device):
         self.N, self.N_pad, self.dtype = N, _pad(N), dtype
         rec_sizes = [_pad(rows.numel()) for rows, _ in recurrent]
-        ff_sizes = [_pad(rows.numel()) for rows, _ in feedforward]
-        self.K_rec_pad, self.K_ff_pad = sum(rec_sizes), sum(ff_sizes)
+        self.K_rec_pad = sum(rec_sizes)
         self.seg = []
-        W = torch.zeros((self.K_rec_pad + self.K_ff_pad, self.N_pad), device=device)
+        W = torch.zeros((self.K_rec_pad, self.N_pad), device=device)
         self.rpos = torch.full((N,), -1, dtype=torch.int32, device=device)
         self.src_of = torch.full((max(self.K_rec_pad, 1),), -1, dtype=torch.int32, device=device)
         start = 0
@@ -78,32 +79,16 @@ class _Operand:
             self.src_of[start:start + n_k] = rows.to(torch.int32)
             self.seg.append((start, start + size, k, 0))
             start += size
-        self.ff_cols = []  # (column offset in the input operand, rows)
-        for k, ((rows, Wk), size) in enumerate(zip(feedforward, ff_sizes)):
-            n_k = rows.numel()
-            W[start:start + n_k, :N] = Wk.detach().float()
-            self.ff_cols.append((start - self.K_rec_pad, rows.long()))
-            self.seg.append((start, start + size, len(recurrent) + k, 1))
-            start += size
         if len(self.seg) > 16:
-            raise NotImplementedError(f"at most 16 pathways, got {len(self.seg)}")
+            raise NotImplementedError(f"at most 16 recurrent pathways, got {len(self.seg)}")
         self.W = W.to(dtype).contiguous()
         self.Wt = self.W.T.contiguous()  # the forward product reads W along k
 
-    def inputs(self, x: torch.Tensor, B_pad: int) -> torch.Tensor:
-        """``(T, B_pad, K_ff_pad)``: every step's input in operand order."""
-        B, T, _ = x.shape
-        X = torch.zeros((T, B_pad, self.K_ff_pad), dtype=self.dtype, device=x.device)
-        for off, rows in self.ff_cols:
-            X[:, :B, off:off + rows.numel()] = x.detach()[:, :, rows].transpose(0, 1).to(self.dtype)
-        return X
-
-    def abi(self, rin, X, B_pad: int) -> _lib.RateOperand:
+    def abi(self, rin, B_pad: int) -> _lib.RateOperand:
         op = _lib.RateOperand()
-        op.W = self.W.data_ptr()
-        op.Wt = self.Wt.data_ptr()
+        op.W = self.W.data_ptr() if self.K_rec_pad else None
+        op.Wt = self.Wt.data_ptr() if self.K_rec_pad else None
         op.rin = _lib.ptr(rin)
-        op.X = _lib.ptr(X) if self.K_ff_pad else None
         op.rpos = self.rpos.data_ptr()
         op.src_of = self.src_of.data_ptr()
         for g, s in enumerate(self.seg):
@@ -111,16 +96,33 @@ class _Operand:
                 op.seg[g][c] = s[c]
         op.n_seg = len(self.seg)
         op.B_pad, op.N_pad = B_pad, self.N_pad
-        op.K_rec_pad, op.K_ff_pad = self.K_rec_pad, self.K_ff_pad
+        op.K_rec_pad = self.K_rec_pad
         op.dtype = DTYPE_CODES[self.dtype]
         return op
 
 
 def _operand(drive, N: int, dtype, device) -> _Operand:
-    tensors = [t for pair in drive.recurrent + drive.feedforward for t in pair]
+    tensors = [t for pair in drive.recurrent for t in pair]
     key = ("rate_operand", N, str(dtype), str(device)) + _key(*tensors)
-    return _cached(key, tuple(tensors),
-                   lambda: _Operand(drive.recurrent, drive.feedforward, N, dtype, device))
+    return _cached(key, tuple(tensors), lambda: _Operand(drive.recurrent, N, dtype, device))
+
+
+def _input_activations(L, x) -> torch.Tensor | None:
+    """``(K_ff, B, T, N)`` float32: ``x[:, :, rows] @ W_k`` per input pathway, one product
+    for the whole call as the reference computes it (``network.py:142-157``); with a
+    reduced-precision storage dtype the operands are rounded to it and multiplied in
+    float32."""
+    if not L.K_ff:
+        return None
+    B, T, N = L.B, L.T, L.N
+    A = torch.empty((L.K_ff, B, T, N), device=L.device)
+    for j, (rows, W) in enumerate(L.feedforward):
+        xr = x.detach()[:, :, rows].reshape(B * T, -1).float()
+        Wr = W.detach().float()
+        if L.op.dtype != torch.float32:
+            xr, Wr = xr.to(L.op.dtype).float(), Wr.to(L.op.dtype).float()
+        torch.matmul(xr, Wr, out=A[j].view(B * T, N))
+    return A
 
 
 class _Plan:
@@ -139,6 +141,7 @@ class _Plan:
             raise NotImplementedError(f"at most 8 synapse types, got {self.S}")
         self.K_rec, self.K_ff = len(drive.recurrent), len(drive.feedforward)
         self.K = self.K_rec + self.K_ff
+        self.feedforward = drive.feedforward
         self.B_pad = _pad(self.B)
         self.op = _operand(drive, self.N, p.storage_dtype, self.device)
         f = lambda t: t.detach().to(device=self.device, dtype=torch.float32).contiguous()
@@ -168,14 +171,14 @@ def _forward(L: _Plan, x, v, I, track, track_b, saved):
     tv = torch.empty((Bt, T, N), device=dev) if track else None
     tI = torch.empty((Bt, T, N, S), device=dev) if track else None
     rin = torch.zeros((2, L.B_pad, max(L.op.K_rec_pad, 1)), dtype=L.op.dtype, device=dev)
-    X = L.op.inputs(x, L.B_pad) if L.op.K_ff_pad else None
+    A_ff = _input_activations(L, x)
     v_s, I_s, tgt_s, A_s = saved if saved is not None else (None,) * 4
     io = _lib.RateIO(B, T, v.data_ptr(), I.data_ptr(), out.data_ptr(), _lib.ptr(tv),
                      _lib.ptr(tI), track_b, _lib.ptr(v_s), _lib.ptr(I_s), _lib.ptr(tgt_s),
-                     _lib.ptr(A_s))
+                     _lib.ptr(A_s), _lib.ptr(A_ff))
     stream = torch.cuda.current_stream(dev).cuda_stream
     with _timed("forward"):
-        _lib.check(_lib.load().wt_rate_forward(L.tables(), L.op.abi(rin, X, L.B_pad), io,
+        _lib.check(_lib.load().wt_rate_forward(L.tables(), L.op.abi(rin, L.B_pad), io,
                                                stream), "wt_rate_forward")
     tracked = {"v": tv, "I": tI} if track else None
     return out, tracked
@@ -247,7 +250,7 @@ class _RateRun(torch.autograd.Function):
         )  # fmt: skip
         stream = torch.cuda.current_stream(dev).cuda_stream
         with _timed("backward"):
-            _lib.check(_lib.load().wt_rate_backward(L.tables(), L.op.abi(rin, None, L.B_pad),
+            _lib.check(_lib.load().wt_rate_backward(L.tables(), L.op.abi(rin, L.B_pad),
                                                     io, stream), "wt_rate_backward")
         grad_scale = acc["scale"].sum(dim=1)[:K] if want_scale else None
         grad_theta = acc["theta"].sum(0) if want_theta else None
