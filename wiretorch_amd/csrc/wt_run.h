@@ -3,8 +3,8 @@
 //
 // Registers and LDS, per workgroup of 1024 threads:
 //   * each thread owns up to MAXI (trial, neuron) items; their v, conductances and
-//     refractory counters stay in VGPRs for the whole launch, with one packed
-//     descriptor each (target within the range, trial within the group, type row);
+//     refractory counters stay in VGPRs for the whole launch (an item's trial, target
+//     and type row are recomputed from its index each step: see item_at);
 //   * LDS holds the int64 activation accumulators [K][tpg][range_n], the workgroup's
 //     own fired bits of the next step, the parameter table (one 64-byte row per distinct
 //     neuron type) and the step's event list.
@@ -69,9 +69,9 @@ __device__ inline ArgPtr kargs() {
   return p;
 }
 
-// A value the compiler cannot see through: what is derived from an item's descriptor
-// is recomputed each step instead of hoisted out of the time loop (which would keep
-// every item's addresses live in registers for the whole launch).
+// A value the compiler cannot see through: what is derived from an item's index is
+// recomputed each step instead of hoisted out of the time loop (which would keep every
+// item's addresses live in registers for the whole launch).
 __device__ inline uint32_t opaque(uint32_t x) {
   asm volatile("" : "+v"(x));
   return x;
@@ -274,6 +274,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   __shared__ int32_t s_nev;
   __shared__ int32_t s_nfired;
   __shared__ uint32_t s_fired[kRunBlock];  // this step's fired sources: j | trial << 24
+  __shared__ uint8_t s_type_of[kMaxItemsPerWg];  // type row of each target of the range
   __shared__ typename BlockScan::storage_type s_scan;
 
   // Sizes in 32 bits (the host checks that they fit); offsets into (B, T, N) arrays
@@ -329,25 +330,35 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     }
   }
 
-  // Registers: the owned items' state and descriptors (target within the range in bits
-  // 0-15, trial within the group in 16-23, row of the type table in 24-31). A thread's
-  // item i is item threadIdx.x + i * kRunBlock of the workgroup; past the last item the
-  // descriptor is 0 and the state zeros, so every lane may compute (only writes check).
+  for (int32_t ln = threadIdx.x; ln < nr; ln += blockDim.x)
+    s_type_of[ln] = (uint8_t)A.tab.type_of[lo + ln];
+  // Item it = threadIdx.x + i * kRunBlock of the workgroup is (trial q, target ln) with
+  // it = q * nr + ln: q = floor(it * ceil(2^32 / nr) / 2^32), exact for it, nr < 2^16.
+  const uint32_t magic = nr > 0 ? (uint32_t)(0xffffffffull / (uint32_t)nr + 1u) : 0u;
+  struct Item {
+    bool valid;
+    uint32_t q, ln;
+  };
+  auto item_at = [&](uint32_t it) {
+    const bool valid = it < items;
+    const uint32_t q = valid ? __umulhi(it, magic) : 0u;
+    return Item{valid, q, valid ? it - q * (uint32_t)nr : 0u};
+  };
+
+  // Registers: the owned items' state. A thread's item i is item threadIdx.x +
+  // i * kRunBlock of the workgroup; past the last item the state is zeros, so every
+  // lane may compute (only writes check).
   float v[MAXI], gr[MAXI][S], gd[MAXI][S];
   int32_t counter[MAXI];
-  uint32_t desc[MAXI];
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) {
-    const uint32_t it = threadIdx.x + (uint32_t)i * kRunBlock;
-    desc[i] = 0;
+    const Item m = item_at(threadIdx.x + (uint32_t)i * kRunBlock);
     v[i] = 0.0f;
     counter[i] = 0;
 #pragma unroll
     for (int s = 0; s < S; ++s) gr[i][s] = gd[i][s] = 0.0f;
-    if (it < items) {
-      const uint32_t q = it / (uint32_t)nr, ln = it - q * (uint32_t)nr;
-      const int64_t n = lo + ln, b = g + (int64_t)q * groups;
-      desc[i] = ln | (q << 16) | (((uint32_t)A.tab.type_of[n] & 0xffu) << 24);
+    if (m.valid) {
+      const int64_t n = lo + m.ln, b = g + (int64_t)m.q * groups;
       v[i] = A.io.v[b * N + n];
       counter[i] = refractory ? A.io.counter[b * N + n] : 0;
 #pragma unroll
@@ -370,10 +381,10 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) {
-    const uint32_t d = desc[i];
-    if (threadIdx.x + (uint32_t)i * kRunBlock >= items) continue;
-    const uint32_t ln = d & 0xffffu, q = (d >> 16) & 0xffu;
-    const float* row = s_types + (d >> 24) * kRow;
+    const Item m = item_at(threadIdx.x + (uint32_t)i * kRunBlock);
+    if (!m.valid) continue;
+    const uint32_t ln = m.ln, q = m.q;
+    const float* row = s_types + s_type_of[ln] * kRow;
     const float theta = row[0];
     float r_hold, held;
     const float s0 = spike_step(v[i], theta, counter[i], (int32_t)row[4], refractory,
@@ -447,10 +458,10 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
         // a wave skips item i only when none of its lanes holds one (a uniform branch:
         // the state is then updated in place on every path)
         if (wave_base + (uint32_t)i * kRunBlock >= items) continue;
-        const bool valid = opaque(threadIdx.x + (uint32_t)i * kRunBlock) < items;
-        const uint32_t d = opaque(desc[i]);
-        const uint32_t ln = d & 0xffffu, q = (d >> 16) & 0xffu;
-        const float* row = s_types + (d >> 24) * kRow;
+        const Item m = item_at(opaque(threadIdx.x + (uint32_t)i * kRunBlock));
+        const bool valid = m.valid;
+        const uint32_t ln = m.ln, q = m.q;
+        const float* row = s_types + s_type_of[ln] * kRow;
         const int64_t out = step_base + (int64_t)((uint64_t)q * trial_stride) + ln;
         const int64_t b = EXTRA ? g + (int64_t)q * groups : 0;
         const int64_t n = lo + ln;
@@ -666,10 +677,10 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   // The activations of the last step enter the conductances that leave the chunk.
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) {
-    const uint32_t d = desc[i];
-    if (threadIdx.x + (uint32_t)i * kRunBlock >= items || T == 0) continue;
-    const uint32_t ln = d & 0xffffu, q = (d >> 16) & 0xffu;
-    const float* row = s_types + (d >> 24) * kRow;
+    const Item m = item_at(threadIdx.x + (uint32_t)i * kRunBlock);
+    if (!m.valid || T == 0) continue;
+    const uint32_t ln = m.ln, q = m.q;
+    const float* row = s_types + s_type_of[ln] * kRow;
     const int64_t n = lo + ln, b = g + (int64_t)q * groups;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
@@ -703,10 +714,9 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   // write the state back
 #pragma unroll
   for (int i = 0; i < MAXI; ++i) {
-    const uint32_t d = desc[i];
-    if (threadIdx.x + (uint32_t)i * kRunBlock >= items) continue;
-    const uint32_t ln = d & 0xffffu, q = (d >> 16) & 0xffu;
-    const int64_t n = lo + ln, b = g + (int64_t)q * groups;
+    const Item m = item_at(threadIdx.x + (uint32_t)i * kRunBlock);
+    if (!m.valid) continue;
+    const int64_t n = lo + m.ln, b = g + (int64_t)m.q * groups;
     A.io.v[b * N + n] = v[i];
     if (refractory) A.io.counter[b * N + n] = counter[i];
 #pragma unroll

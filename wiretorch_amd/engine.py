@@ -224,7 +224,7 @@ def geometry(B: int, N: int, K: int, n_cu: int, max_lds: int) -> tuple[int, int,
     groups = max(1, min(MAX_GROUPS, B))
     tpg = -(-B // groups)
     limit = max(1, n_cu // groups)
-    budget = max_lds - 46 * 1024  # static: event lists, type table, own bits
+    budget = max_lds - 54 * 1024  # static: event lists, type tables, own bits
 
     def fits(R):
         range_n = -(-(-(-N // R)) // 32) * 32
