@@ -443,6 +443,54 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     }
     __syncthreads();
 
+    // ---------------- events of step t, listed before the update ----------------
+    // The fired bits of the preloaded words are compacted into s_fired (source | trial
+    // << 24); bits past its capacity stay in rest[u], to be handled after the update.
+    // Then one thread per listed source, and per listed input, issues its range lookups
+    // (and pathway) into registers: their latency passes during the update.
+    uint32_t rest[MAXI];
+#pragma unroll
+    for (int u = 0; u < MAXI; ++u) {
+      rest[u] = 0u;
+      uint32_t bits = pre[u];
+      if (!bits) continue;
+      const uint32_t w = threadIdx.x + (uint32_t)u * blockDim.x;
+      const uint32_t q = w / (uint32_t)total_words, wl = w - q * (uint32_t)total_words;
+      const uint32_t j0 =
+          (wl / (uint32_t)words) * (uint32_t)range_n + (wl % (uint32_t)words) * 32;
+      int pos = atomicAdd(&s_nfired, __builtin_popcount(bits));
+      while (bits) {
+        const uint32_t bit = __builtin_ctz(bits);
+        bits &= bits - 1;
+        if (pos < kRunBlock)
+          s_fired[pos] = (j0 + bit) | (q << 24);
+        else
+          rest[u] |= 1u << bit;
+        ++pos;
+      }
+    }
+    __syncthreads();
+    int64_t re0 = 0, re1 = 0, ie0 = 0, ie1 = 0;
+    int32_t rk = -1, ik = -1;
+    uint32_t rj = 0;
+    {
+      ArgPtr P = kargs();
+      const int n_list = s_nfired < kRunBlock ? s_nfired : kRunBlock;
+      if ((int)threadIdx.x < n_list) {
+        rj = s_fired[opaque(threadIdx.x)];  // (an address recomputed, not kept live)
+        const int64_t* sp = P->rec.split + (int64_t)(rj & 0xffffffu) * (R + 1) + r;
+        re0 = gload(sp);
+        re1 = gload(sp + 1);
+        rk = gload(P->rec.pathway + (rj & 0xffffffu));
+      }
+      if ((int)(threadIdx.x % kInCap) < in_c && in_c <= kInCap) {
+        const int64_t* sp = P->ff.split + (int64_t)in_j * (R + 1) + r;
+        ie0 = gload(sp);
+        ie1 = gload(sp + 1);
+        ik = gload(P->ff.pathway + in_j);
+      }
+    }
+
     // ---------------- (A) integrate step t for the owned neurons ----------------
     // (step 0 has no previous activations to inject: its own instance of the loop)
     auto update = [&](auto inject_tag) {
@@ -559,45 +607,38 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       }
     }
 
-    // ---------------- events of step t ----------------
-    // (1) The fired bits are compacted into s_fired (source | trial << 24); sources past
-    // its capacity, and inputs of rows with more than kInCap of them, are listed here by
-    // the thread that finds them. Every read of this step's bitmap happens before the
-    // arrival at the barrier.
+    // ---------------- events of step t, after the update ----------------
+    // (1) What the list could not hold — fired sources past its capacity and in words
+    // beyond the preload, inputs of rows with more than kInCap of them — is appended by
+    // the thread that holds it (an event past the event list's capacity is pushed at
+    // once: the update has already read the accumulator). Every read of this step's
+    // bitmap happens before the arrival at the barrier.
     {
       ArgPtr P = kargs();
       const int64_t* rec_split = P->rec.split;
       const int32_t* rec_path = P->rec.pathway;
-      auto fired = [&](uint32_t w, uint32_t bits) {
+      auto direct = [&](uint32_t w, uint32_t bits) {
         const uint32_t q = w / (uint32_t)total_words, wl = w - q * (uint32_t)total_words;
         const uint32_t j0 =
             (wl / (uint32_t)words) * (uint32_t)range_n + (wl % (uint32_t)words) * 32;
-        int pos = atomicAdd(&s_nfired, __builtin_popcount(bits));
         while (bits) {
           const uint32_t j = j0 + __builtin_ctz(bits);
           bits &= bits - 1;
-          if (pos < kRunBlock) {
-            s_fired[pos] = j | (q << 24);
-          } else {
-            const int32_t k = gload(rec_path + j);
-            const int64_t* sp = rec_split + (int64_t)j * (R + 1) + r;
-            if (k >= 0)
-              append_event(EL, acc, P->rec.targets, P->rec.weights, 0, gload(sp),
-                           gload(sp + 1), k * acc_stride + (int64_t)q * range_n, lo, 1.0f,
-                           fx);
-          }
-          ++pos;
+          const int32_t k = gload(rec_path + j);
+          const int64_t* sp = rec_split + (int64_t)j * (R + 1) + r;
+          if (k >= 0)
+            append_event(EL, acc, P->rec.targets, P->rec.weights, 0, gload(sp), gload(sp + 1),
+                         k * acc_stride + (int64_t)q * range_n, lo, 1.0f, fx);
         }
       };
       if (recurrent) {
 #pragma unroll
         for (int u = 0; u < MAXI; ++u)
-          if (pre[u]) fired(threadIdx.x + (uint32_t)u * blockDim.x, pre[u]);
-        // words beyond the preload (only when the bitmap outgrows the registers)
+          if (rest[u]) direct(threadIdx.x + (uint32_t)u * blockDim.x, rest[u]);
         for (int64_t w = threadIdx.x + (int64_t)MAXI * blockDim.x; w < group_words;
              w += blockDim.x) {
           const uint32_t bits = load_agent(in_bits + w);
-          if (bits) fired((uint32_t)w, bits);
+          if (bits) direct((uint32_t)w, bits);
         }
       }
       if (has_ff) {
@@ -626,29 +667,9 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       __syncthreads();
     }
     tick(s_time, 2);
-    // (2) One thread per listed fired source and per prefetched input: every range
-    // lookup in flight together, then the events appended.
+    // (2) The listed sources and inputs, whose lookups were issued before the update.
     {
       ArgPtr P = kargs();
-      const int n_list = s_nfired < kRunBlock ? s_nfired : kRunBlock;
-      const bool has_rec = (int)threadIdx.x < n_list;
-      const bool has_in = (int)(threadIdx.x % kInCap) < in_c && in_c <= kInCap;
-      int64_t re0 = 0, re1 = 0, ie0 = 0, ie1 = 0;
-      int32_t rk = -1, ik = -1;
-      uint32_t rj = 0;
-      if (has_rec) {
-        rj = s_fired[threadIdx.x];
-        const int64_t* sp = P->rec.split + (int64_t)(rj & 0xffffffu) * (R + 1) + r;
-        re0 = gload(sp);
-        re1 = gload(sp + 1);
-        rk = gload(P->rec.pathway + (rj & 0xffffffu));
-      }
-      if (has_in) {
-        const int64_t* sp = P->ff.split + (int64_t)in_j * (R + 1) + r;
-        ie0 = gload(sp);
-        ie1 = gload(sp + 1);
-        ik = gload(P->ff.pathway + in_j);
-      }
       if (rk >= 0)
         append_event(EL, acc, P->rec.targets, P->rec.weights, 0, re0, re1,
                      rk * acc_stride + (int64_t)(rj >> 24) * range_n, lo, 1.0f, fx);
