@@ -488,98 +488,174 @@ struct RateBackArgs {
   int32_t t_rate;  // step of (C), or -1 for none
 };
 
-template <typename T>
+// V consecutive neurons of one trial per thread (V = 4: 16-byte loads and stores, when N
+// is a multiple of 4 and every array is 16-byte aligned; V = 1 otherwise).
+template <int V>
+struct Vec {
+  float x[V];
+};
+template <int V>
+__device__ inline Vec<V> ldv(const float* p) {
+  Vec<V> r;
+  if constexpr (V == 4) {
+    const float4 q = *reinterpret_cast<const float4*>(p);
+    r.x[0] = q.x; r.x[1] = q.y; r.x[2] = q.z; r.x[3] = q.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i) r.x[i] = p[i];
+  }
+  return r;
+}
+template <int V>
+__device__ inline void stv(float* p, const float (&x)[V]) {
+  if constexpr (V == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i) p[i] = x[i];
+  }
+}
+
+template <typename T, int S, int V>
 __global__ __launch_bounds__(kThreads) void rate_back_elem_kernel(RateBackArgs a) {
   const wt_rate_tables& tb = a.tab;
   const wt_rate_back_io& io = a.io;
-  const int64_t N = tb.N, S = tb.S, K = tb.K, B = io.B, T_ = io.T;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t N = tb.N, K = tb.K, B = io.B, T_ = io.T;
+  const int64_t idx = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * V;  // (b, n) flat
   if (idx >= B * N) return;
-  const int64_t b = idx / N, n = idx - b * N;
-  // every pointer below addresses its own array (no aliasing): the loads of a phase can
-  // all be in flight before its stores
+  const int64_t b = idx / N, n = idx - b * N;  // n .. n + V - 1, one trial
+  const bool rate = a.t_rate >= 0, adj = a.t >= 0;
+  const int64_t u = a.t_rate, t = a.t;
+  const int64_t el_u = (b * T_ + u) * N + n, el_t = (b * T_ + t) * N + n;
+  // Every load first — none of them depends on another, and the arrays do not alias —
+  // then the arithmetic, then the stores: one round trip to memory per thread.
   float* __restrict__ lam_v = io.lam_v;
   float* __restrict__ lam_I = io.lam_I;
-  float lv = lam_v[idx];
-  if (a.t_rate >= 0) {  // (C): v_u enters r_u; lv holds beta dL/dv_{u+1} already
-    const int64_t u = a.t_rate;
-    const int64_t el = (b * T_ + u) * N + n;
-    const float dr = io.grad_out[el] + (io.d_rate ? io.d_rate[b * tb.N + n] : 0.0f);
-    const float x = io.v_saved[el] - tb.theta[n];
-    const int code = tb.nonlinearity[n];
-    const float gf = dr * tb.gain[n];
-    const float fp = nonlin_grad(code, x);
-    lv = lv + gf * fp;
-    if (io.acc_theta) io.acc_theta[idx] -= gf * fp;
-    if (io.acc_gain) io.acc_gain[idx] += dr * nonlin(code, x);
+  const float* __restrict__ grad_out = io.grad_out;
+  const float* __restrict__ d_rate = io.d_rate;
+  const float* __restrict__ v_saved = io.v_saved;
+  Vec<V> lv = ldv<V>(lam_v + idx), dr = {}, vs = {};
+  if (rate) {
+    dr = ldv<V>(grad_out + el_u);
+    if (d_rate) {
+      const Vec<V> d = ldv<V>(d_rate + b * N + n);
+#pragma unroll
+      for (int i = 0; i < V; ++i) dr.x[i] = dr.x[i] + d.x[i];
+    }
+    vs = ldv<V>(v_saved + el_u);
   }
-  if (a.t >= 0) {  // (A) of step t: v_{t+1} = beta v_t + (1 - beta) sum_s sign_s I_{t+1,s}
-    const int64_t t = a.t;
-    const int64_t el = (b * T_ + t) * N + n;
-    const float beta = tb.beta[n];
-    // a current whose decay is 0 passes no adjoint back in time: lam_I stays 0, unread
-    float dtarget[kMaxS], lamI[kMaxS], decay[kMaxS], sign[kMaxS];
+  const Vec<V> theta = ldv<V>(tb.theta + n), gain = ldv<V>(tb.gain + n),
+               beta = ldv<V>(tb.beta + n);
+  int code[V];
 #pragma unroll
-    for (int s = 0; s < kMaxS; ++s) {
-      if (s >= S) break;
-      decay[s] = tb.decay[s];
-      sign[s] = tb.sign[s];
-      lamI[s] = decay[s] != 0.0f ? lam_I[(b * S + s) * N + n] : 0.0f;
+  for (int i = 0; i < V; ++i) code[i] = tb.nonlinearity[n + i];
+  float decay[S], sign[S], lamI[S][V];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    decay[s] = tb.decay[s];
+    sign[s] = tb.sign[s];
+  }
+#pragma unroll
+  for (int s = 0; s < S; ++s) {  // a current whose decay is 0 passes no adjoint back in time
+    const Vec<V> l = adj && decay[s] != 0.0f ? ldv<V>(lam_I + (b * S + s) * N + n) : Vec<V>{};
+#pragma unroll
+    for (int i = 0; i < V; ++i) lamI[s][i] = l.x[i];
+  }
+  constexpr int kChunk = 2;
+  float jump[kChunk][V][S];  // jump[k][n + i][s], S * V consecutive floats per pathway
+  auto load_jump = [&](int64_t k0) {
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c)
+#pragma unroll
+      for (int i = 0; i < V; ++i)
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+          jump[c][i][s] = adj && k0 + c < K ? tb.jump[((k0 + c) * N + n + i) * S + s] : 0.0f;
+  };
+  load_jump(0);
+
+  float lvx[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) lvx[i] = lv.x[i];
+  if (rate) {  // (C): v_u enters r_u; lv holds beta dL/dv_{u+1} already
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float x = vs.x[i] - theta.x[i];
+      const float gf = dr.x[i] * gain.x[i];
+      const float fp = nonlin_grad(code[i], x);
+      lvx[i] = lvx[i] + gf * fp;
+      if (io.acc_theta) io.acc_theta[idx + i] -= gf * fp;
+      if (io.acc_gain) io.acc_gain[idx + i] += dr.x[i] * nonlin(code[i], x);
     }
-    float I_next_syn = 0.0f;
+  }
+  if (adj) {  // (A) of step t: v_{t+1} = beta v_t + (1 - beta) sum_s sign_s I_{t+1,s}
+    float dtarget[S][V];
 #pragma unroll
-    for (int s = 0; s < kMaxS; ++s) {
-      if (s >= S) break;
-      if (io.acc_beta) {
-        const float I_next =
-            t + 1 < T_ ? io.I_saved[(el + N) * S + s] : io.I_final[(b * S + s) * N + n];
-        I_next_syn = I_next_syn + I_next * sign[s];
+    for (int i = 0; i < V; ++i) {
+      float I_next_syn = 0.0f;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        if (io.acc_beta) {
+          const float I_next = t + 1 < T_ ? io.I_saved[(el_t + i + N) * S + s]
+                                          : io.I_final[(b * S + s) * N + n + i];
+          I_next_syn = I_next_syn + I_next * sign[s];
+        }
+        const float dI = lamI[s][i] + lvx[i] * (1.0f - beta.x[i]) * sign[s];
+        dtarget[s][i] = dI * (1.0f - decay[s]);
+        lamI[s][i] = dI * decay[s];
+        if (io.acc_decay)
+          io.acc_decay[(b * S + s) * N + n + i] +=
+              dI * (io.I_saved[(el_t + i) * S + s] - io.target_saved[(el_t + i) * S + s]);
       }
-      const float dI = lamI[s] + lv * (1.0f - beta) * sign[s];
-      dtarget[s] = dI * (1.0f - decay[s]);
-      lamI[s] = dI * decay[s];
-      if (io.acc_decay)
-        io.acc_decay[(b * S + s) * N + n] += dI * (io.I_saved[el * S + s] - io.target_saved[el * S + s]);
+      if (io.acc_beta) io.acc_beta[idx + i] += lvx[i] * (v_saved[el_t + i] - I_next_syn);
     }
-    if (io.acc_beta) io.acc_beta[idx] += lv * (io.v_saved[el] - I_next_syn);
-    // dL/da_k, eight pathways at a time: their kernel scales first, then the stores
+    // dL/da_k = sum_s dtarget_s jump_k[s], kChunk pathways at a time
     float* __restrict__ grad_A = io.grad_A;
     T* __restrict__ gA_op = static_cast<T*>(io.gA_op);
-    for (int64_t k0 = 0; k0 < K; k0 += 8) {
-      float g[8];
+    for (int64_t k0 = 0; k0 < K; k0 += kChunk) {
+      if (k0 > 0) load_jump(k0);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        g[i] = 0.0f;
-        if (k0 + i >= K) continue;
-#pragma unroll
-        for (int s = 0; s < kMaxS; ++s) {
-          if (s >= S) break;
-          g[i] = g[i] + dtarget[s] * tb.jump[((k0 + i) * N + n) * S + s];
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int64_t k = k0 + i;
+      for (int c = 0; c < kChunk; ++c) {
+        const int64_t k = k0 + c;
         if (k >= K) break;
-        grad_A[((k * B + b) * T_ + t) * N + n] = g[i];
-        if (k < tb.K_rec) gA_op[(k * a.op.B_pad + b) * a.op.N_pad + n] = to_storage<T>(g[i]);
-      }
-      if (io.acc_scale) {
-        for (int64_t k = k0; k < K && k < k0 + 8; ++k) {
-          float m = 0.0f;
-          for (int64_t s = 0; s < S; ++s) m = m + dtarget[s] * tb.made[k * S + s];
-          io.acc_scale[(k * B + b) * N + n] += m * io.A_saved[((k * B + b) * T_ + t) * N + n];
+        float g[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          g[i] = 0.0f;
+#pragma unroll
+          for (int s = 0; s < S; ++s) g[i] = g[i] + dtarget[s][i] * jump[c][i][s];
+        }
+        stv<V>(grad_A + ((k * B + b) * T_ + t) * N + n, g);
+        if (k < tb.K_rec) {
+          T* dst = gA_op + (k * a.op.B_pad + b) * a.op.N_pad + n;
+#pragma unroll
+          for (int i = 0; i < V; ++i) dst[i] = to_storage<T>(g[i]);
+        }
+        if (io.acc_scale) {
+          float m[V];
+#pragma unroll
+          for (int i = 0; i < V; ++i) {
+            m[i] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < S; ++s) m[i] = m[i] + dtarget[s][i] * tb.made[k * S + s];
+            io.acc_scale[(k * B + b) * N + n + i] +=
+                m[i] * io.A_saved[((k * B + b) * T_ + t) * N + n + i];
+          }
         }
       }
     }
 #pragma unroll
-    for (int s = 0; s < kMaxS; ++s) {
-      if (s >= S) break;
-      if (decay[s] != 0.0f) lam_I[(b * S + s) * N + n] = lamI[s];
-    }
-    lv = lv * beta;  // dL/dv_t before its rate's term
+    for (int s = 0; s < S; ++s)
+      if (decay[s] != 0.0f) {
+        float l[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) l[i] = lamI[s][i];
+        stv<V>(lam_I + (b * S + s) * N + n, l);
+      }
+#pragma unroll
+    for (int i = 0; i < V; ++i) lvx[i] = lvx[i] * beta.x[i];  // dL/dv_t before its rate's term
   }
-  lam_v[idx] = lv;
+  stv<V>(lam_v + idx, lvx);
 }
 
 // Reverse product of step t: d_rate[b, neuron of row j] = sum_n dL/da_k[b, n] W[j, n] for
@@ -656,13 +732,30 @@ template <typename T>
 static hipError_t backward_impl(const RateBackArgs& base, hipStream_t stream) {
   RateBackArgs a = base;
   const int64_t BN = a.io.B * a.tab.N;
-  const dim3 egrid((unsigned)((BN + kThreads - 1) / kThreads));
+  const dim3 egrid_1((unsigned)((BN + kThreads - 1) / kThreads));
+  const dim3 egrid_4((unsigned)((BN / 4 + kThreads - 1) / kThreads));
   const dim3 ggrid((unsigned)(a.op.K_rec_pad / kTile), (unsigned)(a.op.B_pad / kTile));
   const bool rec = a.tab.K_rec > 0 && a.op.K_rec_pad > 0;
+  void (*elem)(RateBackArgs) = nullptr;
+  // four neurons per thread when every (., N) row and array is 16-byte aligned
+  auto al = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  const wt_rate_back_io& q = a.io;
+  const bool v4 = a.tab.N % 4 == 0 && al(q.grad_out) && al(q.v_saved) && al(q.lam_v) &&
+                  al(q.lam_I) && al(q.grad_A) && (!q.d_rate || al(q.d_rate)) &&
+                  al(a.tab.theta) && al(a.tab.gain) && al(a.tab.beta);
+  const int vw = v4 ? 4 : 1;
+  switch (a.tab.S * 8 + vw) {
+#define WT_ELEM(SS)                                                     \
+    case SS * 8 + 1: elem = rate_back_elem_kernel<T, SS, 1>; break; \
+    case SS * 8 + 4: elem = rate_back_elem_kernel<T, SS, 4>; break;
+    WT_ELEM(1) WT_ELEM(2) WT_ELEM(3) WT_ELEM(4) WT_ELEM(5) WT_ELEM(6) WT_ELEM(7) WT_ELEM(8)
+#undef WT_ELEM
+    default: return hipErrorInvalidValue;
+  }
   for (int64_t t = a.io.T - 1; t >= -1; --t) {
     a.t = (int32_t)t;
     a.t_rate = t + 1 < a.io.T ? (int32_t)(t + 1) : -1;
-    hipLaunchKernelGGL(rate_back_elem_kernel<T>, egrid, dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL(elem, vw == 4 ? egrid_4 : egrid_1, dim3(kThreads), 0, stream, a);
     if (t >= 0 && rec)
       hipLaunchKernelGGL(rate_back_gemm_kernel<T>, ggrid, dim3(kThreads), 0, stream, a);
   }
