@@ -1,7 +1,7 @@
 """Benchmark: neuron-steps/s and synaptic events/s of the fly-scale conductance-LIF
 forward on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2|4]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1|2|3|4]
 
 A step is one forward call of the hot path over one batch of synthetic input: 8 trials
 x 2000 time steps (dt 0.1 ms) of a 140k-neuron, ~50M-synapse network from rest, with
@@ -9,8 +9,13 @@ the input resident in HBM. Prints one JSON line (see the keys below), including 
 roofline of the dominant kernel (``wt_cond_run``, timed with HIP events on its stream)
 and the CPU baseline (the oracle, on a bounded slice of the same workload).
 
-``--config 4`` measures the dense rate network instead (configuration 4, the matrix-core
-path): a step is one forward + backward of 256 trials x 1000 steps of 4096 tanh rate
+``--config 1`` measures configuration 1 the same way (10,000 neurons, ~2M synapses, 32
+trials x 5,000 steps, through the network API). ``--config 3`` measures the training
+step: forward + backward of 64 trials x 500 steps of configuration 3's network (learnt
+per-synapse weights, tau_mem and theta), the loss a squared error of 20 ms-binned rates;
+its roofline is that of the part (forward, backward, weight gradient) with the largest
+share of the step. ``--config 4`` measures the dense rate network (configuration 4, the
+matrix-core path): a step is one forward + backward of 256 trials x 1000 steps of 4096 tanh rate
 neurons with bf16 weights, from rest, with a linear read-out's squared error as the loss;
 the roofline is that of the kernel with the largest share of the step, against the
 matrix cores' dense peak in its arithmetic type.
@@ -92,6 +97,171 @@ def cpu_baseline(wl, steps):
         "sample": f"oracle on the first {steps} of {wl.x.shape[1]} steps, all {B} trials "
                   f"({dt:.1f} s)",
     }
+
+
+def er_events(wl, spikes, x):
+    """Delivered events of an Erdős–Rényi workload: spikes x out-degree, recurrent and
+    input, over all trials and steps."""
+    out_rec = torch.from_numpy((wl.structure["w"] != 0).sum(1)).to(spikes.device, torch.float64)
+    out_ff = torch.from_numpy((wl.structure["w_in"] != 0).sum(1)).to(x.device, torch.float64)
+    return float(spikes.double().sum(dim=(0, 1)) @ out_rec
+                 + (x != 0).double().sum(dim=(0, 1)) @ out_ff)
+
+
+def _part_ms(events):
+    return {k: float(np.mean([a.elapsed_time(b) for a, b in v])) for k, v in events.items()}
+
+
+def _er_cpu_baseline(model, x_np, steps, train):
+    """The oracle on the first ``steps`` steps of the same workload (all trials), on a
+    CPU copy of the benchmarked network."""
+    import copy
+
+    import oracle.dynamics as oracle_engine
+
+    engine_module, model._engine = model._engine, None  # (a module does not copy)
+    try:
+        cpu_model = copy.deepcopy(model).cpu()
+    finally:
+        model._engine = engine_module
+    model = cpu_model
+    model._engine = oracle_engine
+    x = torch.from_numpy(x_np[:, :steps]).float()
+    B, N = x.shape[0], model.n_neurons
+    model.reset_state()
+    t0 = time.perf_counter()
+    if train:
+        model.zero_grad(set_to_none=True)
+        spikes = model(x)
+        dt = float(model.dt)
+        target = torch.from_numpy(synthetic.gamma_targets(3, N, max(1, int(steps * dt // 20))))
+        synthetic.binned_rate_loss(spikes, target, dt).backward()
+    else:
+        with torch.no_grad():
+            model(x)
+    elapsed = time.perf_counter() - t0
+    what = "forward + backward" if train else "forward"
+    return {
+        "value": B * N * steps / elapsed,
+        "unit": "neuron-steps/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"oracle {what} of the first {steps} of {x_np.shape[1]} steps, all {B} "
+                  f"trials ({elapsed:.1f} s)",
+    }
+
+
+def _line(value, ms_per_step, args, dtype, config, roofline, cpu, **extra):
+    line = {
+        "metric": METRIC, "value": value, "unit": "neuron-steps/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+        "data": "synthetic", **extra, "config": config, "roofline": roofline,
+        "cpu_baseline": cpu,
+    }  # fmt: skip
+    print(json.dumps(line), flush=True)
+
+
+def bench_config1(args):
+    dev = torch.device("cuda:0")
+    T = args.T if args.T != 2000 else 5000
+    wl = synthetic.config1(T=T)
+    model = wl.model.to(dev)
+    x = torch.from_numpy(wl.x).float().to(dev)
+    B, N = x.shape[0], wl.N
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            model.reset_state()
+            model(x)
+        torch.cuda.synchronize()
+        engine.PART_EVENTS = {}
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            model.reset_state()
+            spikes = model(x)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    parts, engine.PART_EVENTS = _part_ms(engine.PART_EVENTS), None
+    ms_per_step = wall * 1e3 / args.steps
+    events = er_events(wl, spikes, x)
+    S = wl.S
+    bytes_per_launch = algorithmic_bytes(B, T, N, S, events)
+    achieved = bytes_per_launch / (parts["forward"] / 1e3) / 1e9
+    rate_hz = float(spikes.mean()) / 0.1e-3
+    print(f"# config1: kernel {parts['forward']:.3f} ms, wall {ms_per_step:.3f} ms/step, "
+          f"rate {rate_hz:.2f} Hz", file=sys.stderr, flush=True)
+    cpu = _er_cpu_baseline(model, wl.x, args.cpu_steps, False) if args.cpu_steps > 0 else None
+    _line(B * N * T / (ms_per_step / 1e3), ms_per_step, args, "f32",
+          {"workload": "config1: mid-size conductance-LIF forward", "neurons": N,
+           "synapses": int((wl.structure["w"] != 0).sum()), "batch": B, "time_steps": T,
+           "dt_ms": 0.1, "parallelism": "single GPU"},
+          {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "wt_cond_run",
+           "kernel_ms": parts["forward"], "algorithmic_bytes_per_launch": bytes_per_launch},
+          cpu, synaptic_events_per_s=events / (ms_per_step / 1e3), mean_rate_hz=rate_hz)
+
+
+def bench_config3(args):
+    dev = torch.device("cuda:0")
+    T = args.T if args.T != 2000 else 500
+    wl = synthetic.config3(T=T)
+    model = wl.model.to(dev)
+    x = torch.from_numpy(wl.x).float().to(dev)
+    B, N, S = x.shape[0], wl.N, wl.S
+    dt = float(model.dt)
+    target = torch.from_numpy(synthetic.gamma_targets(3, N, max(1, int(T * dt // 20)))).to(dev)
+
+    def step():
+        model.reset_state()
+        model.zero_grad(set_to_none=True)
+        spikes = model(x)
+        synthetic.binned_rate_loss(spikes, target, dt).backward()
+        return spikes
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    engine.PART_EVENTS = {}
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        spikes = step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    parts, engine.PART_EVENTS = _part_ms(engine.PART_EVENTS), None
+    ms_per_step = wall * 1e3 / args.steps
+    events = er_events(wl, spikes.detach(), x)
+    K = 3  # pathways: recurrent E, recurrent I, input
+    n_edges = int((wl.structure["w"] != 0).sum() + (wl.structure["w_in"] != 0).sum())
+    # algorithmic bytes: the forward moves the state and saves v, G, held, A; the backward
+    # reads what was saved (and the spikes and dL/ds) and writes dL/dA; the weight
+    # gradient reads dL/dA of each delivered event's target (and its index) and writes
+    # one gradient per synapse
+    nbytes = {
+        "forward": T * (B * N * (8 + 16 * S + 8 + 4 + 4 + 4 * S + 1 + 4 * K) + 24 * N)
+                   + 8 * events,
+        "backward": T * B * N * (4 + 4 + 4 + 4 * S + 1 + 4 * K + 4 * K),
+        "weight_gradient": 8 * events + 4 * n_edges,
+    }
+    dominant = max(parts, key=parts.get)
+    achieved = nbytes[dominant] / (parts[dominant] / 1e3) / 1e9
+    rate_hz = float(spikes.detach().mean()) * 1000.0 / dt
+    print(f"# config3: wall {ms_per_step:.2f} ms/step; " + ", ".join(
+        f"{k} {v:.2f} ms ({nbytes[k] / (v / 1e3) / 1e9:.0f} GB/s)" for k, v in parts.items())
+        + f"; rate {rate_hz:.1f} Hz", file=sys.stderr, flush=True)
+    cpu = _er_cpu_baseline(model, wl.x, args.cpu_steps, True) if args.cpu_steps > 0 else None
+    _line(B * N * T / (ms_per_step / 1e3), ms_per_step, args, "f32",
+          {"workload": "config3: conductance-LIF training step (BPTT, surrogate gradient)",
+           "neurons": N, "synapses": int((wl.structure["w"] != 0).sum()), "batch": B,
+           "time_steps": T, "dt_ms": dt, "learnt": "per-synapse weights, tau_mem, theta",
+           "loss": "MSE of 20 ms-binned rates vs gamma(2, 5 Hz) targets",
+           "parallelism": "single GPU"},
+          {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+           "kernel": {"forward": "wt_cond_run", "backward": "wt_cond_scan_backward",
+                      "weight_gradient": "wt_weight_gradient"}[dominant],
+           "kernel_ms": parts[dominant], "algorithmic_bytes_per_launch": nbytes[dominant],
+           "per_part_ms": parts},
+          cpu, synaptic_events_per_s=events / (ms_per_step / 1e3), mean_rate_hz=rate_hz)
 
 
 def rate_cpu_baseline(wl, steps):
@@ -224,7 +394,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--cpu-steps", type=int, default=int(os.environ.get("BENCH_CPU_STEPS", 400)))
     ap.add_argument("--T", type=int, default=2000)
-    ap.add_argument("--config", type=int, choices=(2, 4), default=2)
+    ap.add_argument("--config", type=int, choices=(1, 2, 3, 4), default=2)
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run one device-to-device copy of this many bytes (the "
                          "reference kernel for calibrating rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -241,10 +411,19 @@ def main():
         print("bench.py runs on one GPU only: this build has no multi-GPU path "
               "(the hot path runs on a single GPU)", file=sys.stderr)
         sys.exit(2)
+    default_cpu = "--cpu-steps" not in sys.argv and "BENCH_CPU_STEPS" not in os.environ
     if args.config == 4:
-        if "--cpu-steps" not in sys.argv and "BENCH_CPU_STEPS" not in os.environ:
+        if default_cpu:
             args.cpu_steps = 100
         return bench_config4(args)
+    if args.config == 1:
+        if default_cpu:
+            args.cpu_steps = 50
+        return bench_config1(args)
+    if args.config == 3:
+        if default_cpu:
+            args.cpu_steps = 5
+        return bench_config3(args)
     dev = torch.device("cuda:0")
     t_build = time.perf_counter()
     wl = synthetic.fly_scale(T=args.T, device=dev)

@@ -282,7 +282,21 @@ int wt_weight_gradient(const wt_side* side, const int64_t* edge_src, int64_t n_e
                        const float* grad_A, int64_t B, int64_t T, int64_t N,
                        int64_t pathway_offset, float* grad_w, wt_stream_t stream);
 
-/* wt_device_info — compute units of the current device (for the geometry). */
+/* wt_weight_gradient_by_target — the same sums (in a fixed order of their own: a
+ * wave's 64 lanes over consecutive events, then a tree), grouped by (pathway, target)
+ * row: grad_A (n_pathways, BT, N) is the side's dL/da, first transposed into rows
+ * (n_pathways * N, BT) f32 (caller's scratch, overwritten), row k * N + n = dL/da_k over
+ * b*T+t for target n; the incoming synapses of row kn are in_edge[in_indptr[kn] ..
+ * in_indptr[kn+1]-1] (edge indices, each edge in the row of its source's pathway). One
+ * workgroup per row reads it once into LDS. Every edge listed is overwritten; edges
+ * listed in no row are left alone. Replaces: as wt_weight_gradient. */
+int wt_weight_gradient_by_target(const int64_t* edge_src, int64_t n_edges,
+                                 const int64_t* in_indptr, const int64_t* in_edge,
+                                 int64_t n_pathways, int64_t N, const int64_t* ev_indptr,
+                                 const int64_t* ev_bt, const float* ev_val,
+                                 const float* grad_A, int64_t BT, float* rows, float* grad_w,
+                                 wt_stream_t stream);
+
 int wt_device_info(int64_t* n_cu, int64_t* max_lds_bytes);
 
 #ifdef __cplusplus

@@ -110,6 +110,8 @@ SIGNATURES = {
     "wt_edge_sources": (ctypes.c_int, [P, I64, P, P]),
     "wt_weight_gradient": (ctypes.c_int, [ctypes.POINTER(Side), P, I64, P, P, P, P, I64,
                                           I64, I64, I64, P, P]),
+    "wt_weight_gradient_by_target": (ctypes.c_int, [P, I64, P, P, I64, I64, P, P, P, P, I64,
+                                                    P, P, P]),
     "wt_device_info": (ctypes.c_int, [ctypes.POINTER(I64), ctypes.POINTER(I64)]),
 }  # fmt: skip
 

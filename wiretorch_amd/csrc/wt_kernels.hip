@@ -100,6 +100,112 @@ __global__ void weight_gradient_kernel(wt_side side, const int64_t* edge_src, in
   grad_w[e] = sum;
 }
 
+// The same sums, grouped by (pathway, target): workgroup kn = k * N + n holds the
+// target's dL/da_k over every (trial, step), row kn of grad_A_T (k, n, b*T+t), in LDS —
+// read once, contiguously — and each wave takes one incoming synapse at a time: its 64
+// lanes read 64 consecutive events of the synapse's source (one coalesced load) and add
+// the row's entries; the lanes' partial sums are then added in a fixed tree (the sum is
+// deterministic). Rows longer than the LDS chunk are taken a chunk at a time, each
+// synapse's running sum kept in grad_w.
+constexpr int kWgBlock = 1024;
+constexpr int64_t kWgChunk = 32768;  // floats of a row in LDS (128 KB)
+
+// dL/da (K, BT, N) -> rows (K * N, BT), through 64 x 64 LDS tiles (coalesced both ways).
+__global__ __launch_bounds__(256) void transpose_rows_kernel(const float* src, float* dst,
+                                                             int64_t BT, int64_t N) {
+  __shared__ float tile[64][65];
+  const int64_t k = blockIdx.z, n0 = (int64_t)blockIdx.x * 64, bt0 = (int64_t)blockIdx.y * 64;
+  const float* s = src + k * BT * N;
+  float* d = dst + k * N * BT;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t bt = bt0 + r, n = n0 + tx;
+    if (bt < BT && n < N) tile[r][tx] = s[bt * N + n];
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t n = n0 + r, bt = bt0 + tx;
+    if (bt < BT && n < N) d[n * BT + bt] = tile[tx][r];
+  }
+}
+
+__global__ __launch_bounds__(kWgBlock) void weight_gradient_target_kernel(
+    const int64_t* in_indptr, const int64_t* in_edge, const int64_t* edge_src,
+    const int64_t* ev_indptr, const int64_t* ev_bt, const float* ev_val,
+    const float* grad_A_T, int64_t BT, float* grad_w) {
+  extern __shared__ float row[];
+  const int64_t kn = blockIdx.x;
+  const int64_t e0 = in_indptr[kn], e1 = in_indptr[kn + 1];
+  if (e0 == e1) return;  // uniform
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, n_waves = blockDim.x >> 6;
+  const float* src = grad_A_T + kn * BT;
+  const bool vec = (BT & 3) == 0 && ((uintptr_t)grad_A_T & 15) == 0;
+  for (int64_t c0 = 0; c0 < BT; c0 += kWgChunk) {
+    const int64_t len = BT - c0 < kWgChunk ? BT - c0 : kWgChunk;
+    __syncthreads();  // the previous chunk is no longer read
+    if (vec) {
+      const float4* s4 = reinterpret_cast<const float4*>(src + c0);
+      float4* r4 = reinterpret_cast<float4*>(row);
+      const int64_t n4 = len >> 2;
+      int64_t i = threadIdx.x;
+      for (; i + 3 * kWgBlock < n4; i += 4 * kWgBlock) {  // four loads in flight
+        const float4 a = s4[i], b = s4[i + kWgBlock], c = s4[i + 2 * kWgBlock],
+                     d = s4[i + 3 * kWgBlock];
+        r4[i] = a;
+        r4[i + kWgBlock] = b;
+        r4[i + 2 * kWgBlock] = c;
+        r4[i + 3 * kWgBlock] = d;
+      }
+      for (; i < n4; i += kWgBlock) r4[i] = s4[i];
+    } else {
+      for (int64_t i = threadIdx.x; i < len; i += blockDim.x) row[i] = src[c0 + i];
+    }
+    __syncthreads();
+    for (int64_t ei = e0 + wave; ei < e1; ei += n_waves) {
+      const int64_t e = in_edge[ei], j = edge_src[e];
+      int64_t i0 = ev_indptr[j];
+      const int64_t i1 = ev_indptr[j + 1];
+      if (c0 > 0) {  // the first event at or past the chunk (events ascend in b*T+t)
+        int64_t lo = i0, hi = i1;
+        while (lo < hi) {
+          const int64_t mid = (lo + hi) >> 1;
+          if (ev_bt[mid] < c0) lo = mid + 1; else hi = mid;
+        }
+        i0 = lo;
+      }
+      float part = 0.0f;
+      int64_t i = i0 + lane;
+      for (; i + 192 < i1; i += 256) {  // four events per lane in flight
+        int64_t bt[4];
+        float val[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          bt[u] = ev_bt[i + 64 * u] - c0;
+          val[u] = ev_val[i + 64 * u];
+        }
+        bool past = false;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (bt[u] >= len) past = true;
+          if (!past) part += val[u] * row[bt[u]];
+        }
+        if (past) {  // this lane's later events are past the chunk too
+          i = i1;
+          break;
+        }
+      }
+      for (; i < i1; i += 64) {
+        const int64_t bt = ev_bt[i] - c0;
+        if (bt >= len) break;
+        part += ev_val[i] * row[bt];
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
+      if (lane == 0) grad_w[e] = (c0 > 0 ? grad_w[e] : 0.0f) + part;
+    }
+  }
+}
+
 __global__ void edge_source_kernel(const int64_t* indptr, int64_t n_src, int64_t* edge_src) {
   const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= n_src) return;
@@ -354,6 +460,37 @@ extern "C" int wt_weight_gradient(const wt_side* side, const int64_t* edge_src, 
   hipLaunchKernelGGL(weight_gradient_kernel, dim3((unsigned)((n_edges + block - 1) / block)),
                      dim3(block), 0, (hipStream_t)stream, *side, edge_src, n_edges, ev_indptr,
                      ev_bt, ev_val, grad_A, B * T, N, pathway_offset, grad_w);
+  return hipGetLastError();
+}
+
+extern "C" int wt_weight_gradient_by_target(const int64_t* edge_src, int64_t n_edges,
+                                            const int64_t* in_indptr, const int64_t* in_edge,
+                                            int64_t n_pathways, int64_t N,
+                                            const int64_t* ev_indptr, const int64_t* ev_bt,
+                                            const float* ev_val, const float* grad_A,
+                                            int64_t BT, float* rows, float* grad_w,
+                                            wt_stream_t stream) {
+  if (n_edges < 0 || n_pathways < 0 || N < 0 || BT < 0) return hipErrorInvalidValue;
+  const int64_t n_rows = n_pathways * N;
+  if (n_edges == 0 || n_rows == 0) return hipSuccess;
+  if (!edge_src || !in_indptr || !in_edge || !ev_indptr || !ev_bt || !ev_val || !grad_A ||
+      !rows || !grad_w || BT == 0)
+    return hipErrorInvalidValue;
+  if (n_rows > 0x7fffffff || (N + 63) / 64 > 0x7fffffff || (BT + 63) / 64 > 65535 ||
+      n_pathways > 65535)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(transpose_rows_kernel,
+                     dim3((unsigned)((N + 63) / 64), (unsigned)((BT + 63) / 64),
+                          (unsigned)n_pathways),
+                     dim3(256), 0, (hipStream_t)stream, grad_A, rows, BT, N);
+  const int64_t chunk = BT < kWgChunk ? BT : kWgChunk;
+  const hipError_t e = hipFuncSetAttribute((const void*)weight_gradient_target_kernel,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)(chunk * sizeof(float)));
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(weight_gradient_target_kernel, dim3((unsigned)n_rows), dim3(kWgBlock),
+                     (size_t)chunk * sizeof(float), (hipStream_t)stream, in_indptr, in_edge,
+                     edge_src, ev_indptr, ev_bt, ev_val, rows, BT, grad_w);
   return hipGetLastError();
 }
 

@@ -46,6 +46,29 @@ MAX_TYPES = 256
 #: When a list, every ``wt_cond_run`` launch appends a pair of events recorded on its
 #: stream just before and after it (``bench.py`` times the kernel with them).
 LAUNCH_EVENTS: list | None = None
+#: When a dict, each part of a call appends a pair of events recorded on its stream just
+#: before and after it, under its name: ``"forward"`` (``wt_cond_run``), ``"backward"``
+#: (``wt_cond_scan_backward`` / ``wt_cond_recurrent_backward``) and
+#: ``"weight_gradient"`` (the events listing and ``wt_weight_gradient``).
+PART_EVENTS: dict | None = None
+
+
+class _timed:
+    """Records a pair of events around a block into ``PART_EVENTS[name]``."""
+
+    def __init__(self, name):
+        self.name = name
+
+    def __enter__(self):
+        if PART_EVENTS is not None:
+            self.start = torch.cuda.Event(enable_timing=True)
+            self.start.record()
+
+    def __exit__(self, *exc):
+        if PART_EVENTS is not None and exc[0] is None:
+            stop = torch.cuda.Event(enable_timing=True)
+            stop.record()
+            PART_EVENTS.setdefault(self.name, []).append((self.start, stop))
 #: When a list, launches run ``wt_cond_run_timed`` and append the per-workgroup phase
 #: ticks ``(groups * R, 5)`` (profiling only).
 PHASE_TIMING: list | None = None
@@ -68,6 +91,7 @@ class _Side:
     max_in_sum: float = 0.0
     _split: dict = field(default_factory=dict)
     _edge_src: torch.Tensor | None = None
+    _by_target: dict = field(default_factory=dict)
 
     @property
     def n_src(self) -> int:
@@ -102,6 +126,22 @@ class _Side:
             )
             self._edge_src = out
         return self._edge_src
+
+    def by_target(self, N: int, n_pathways: int, stream):
+        """``(in_indptr, in_edge)``: the edges grouped by (pathway, target) row
+        ``k * N + n``, in source order within a row (edges of no pathway left out)."""
+        key = (N, n_pathways)
+        if key not in self._by_target:
+            c = self.conn
+            edge_src = self.edge_src(stream)
+            k = c.pathway[edge_src]
+            row = torch.where(k >= 0, k * N + c.targets.long(), n_pathways * N)
+            in_edge = torch.argsort(row, stable=True)
+            counts = torch.bincount(row, minlength=n_pathways * N + 1)[: n_pathways * N]
+            in_indptr = torch.zeros(n_pathways * N + 1, dtype=torch.int64, device=c.device)
+            in_indptr[1:] = torch.cumsum(counts, 0)
+            self._by_target[key] = (in_indptr, in_edge)
+        return self._by_target[key]
 
     def abi(self, R: int, range_n: int, stream, weights: torch.Tensor | None = None) -> _lib.Side:
         c = self.conn
@@ -413,8 +453,9 @@ def _launch(L: _Plan, x, scale, v, g, counter, spikes, prob, saved, tracked,
                                          ticks.data_ptr(), L.stream), "wt_cond_run_timed")
         PHASE_TIMING.append(ticks)
     else:
-        _lib.check(lib.wt_cond_run(tab, rec, ff, geo, io, scratch.data_ptr(), L.stream),
-                   "wt_cond_run")
+        with _timed("forward"):
+            _lib.check(lib.wt_cond_run(tab, rec, ff, geo, io, scratch.data_ptr(), L.stream),
+                       "wt_cond_run")
     if LAUNCH_EVENTS is not None:
         stop.record()
         LAUNCH_EVENTS.append((start, stop))
@@ -489,20 +530,23 @@ class _Run(torch.autograd.Function):
             rec = L.rec.abi(R, range_n, L.stream, rec_w)
             scratch = torch.empty(int(lib.wt_cond_recurrent_backward_scratch_bytes(S, L.K_rec, B, N)),
                                   dtype=torch.uint8, device=dev)
-            _lib.check(lib.wt_cond_recurrent_backward(tab, rec, io, scratch.data_ptr(), L.stream),
-                       "wt_cond_recurrent_backward")
+            with _timed("backward"):
+                _lib.check(lib.wt_cond_recurrent_backward(tab, rec, io, scratch.data_ptr(),
+                                                          L.stream), "wt_cond_recurrent_backward")
         else:
-            _lib.check(lib.wt_cond_scan_backward(tab, io, L.stream), "wt_cond_scan_backward")
+            with _timed("backward"):
+                _lib.check(lib.wt_cond_scan_backward(tab, io, L.stream), "wt_cond_scan_backward")
         grad_scale = partial.sum(dim=1) if want_scale else None
         dims = [0] * 5 + [(0, 2), (0, 3), (0, 3)]
         grad_phys = [t.sum(d) if t is not None else None for t, d in zip(phys, dims)]
         grad_w = [None] * len(weights)
-        if any(w_needs[:n_rec_w]):
-            grad_w[:n_rec_w] = _weight_grads(L, L.rec, spikes, grad_A, 0, weights[:n_rec_w],
-                                             w_needs[:n_rec_w])
-        if any(w_needs[n_rec_w:]):
-            grad_w[n_rec_w:] = _weight_grads(L, L.ff, x.detach().float(), grad_A, L.K_rec,
-                                             weights[n_rec_w:], w_needs[n_rec_w:])
+        with _timed("weight_gradient"):
+            if any(w_needs[:n_rec_w]):
+                grad_w[:n_rec_w] = _weight_grads(L, L.rec, spikes, grad_A, 0,
+                                                 weights[:n_rec_w], w_needs[:n_rec_w])
+            if any(w_needs[n_rec_w:]):
+                grad_w[n_rec_w:] = _weight_grads(L, L.ff, x.detach().float(), grad_A, L.K_rec,
+                                                 weights[n_rec_w:], w_needs[n_rec_w:])
         grad_x = _input_grad(L, x, grad_A, weights[n_rec_w:]) if want_x else None
         return (None, None, grad_scale, grad_x, None, None, None, *grad_w, *grad_phys)
 
@@ -545,19 +589,25 @@ def _events(activity: torch.Tensor):
 
 
 def _weight_grads(L: _Plan, side: _Side, activity, grad_A, k0, weights, needs):
-    """Gradients of a side's weight tensors from the event-driven support gradient."""
+    """Gradients of a side's weight tensors from the event-driven support gradient:
+    ``wt_weight_gradient_by_target`` over dL/da transposed to (pathway, target) rows."""
     c = side.conn
     indptr, bt, value = _events(activity)
-    grad_e = torch.empty(c.n_edges, device=L.device)
+    grad_e = torch.zeros(c.n_edges, device=L.device)
     edge_src = side.edge_src(L.stream)
-    groups, R, range_n = L.geo
-    abi = side.abi(R, range_n, L.stream)
-    _lib.check(
-        _lib.load().wt_weight_gradient(abi, edge_src.data_ptr(), c.n_edges, indptr.data_ptr(),
-                                       bt.data_ptr(), value.data_ptr(), grad_A.data_ptr(), L.B,
-                                       L.T, L.N, k0, grad_e.data_ptr(), L.stream),
-        "wt_weight_gradient",
-    )  # fmt: skip
+    n_path = int(c.n_pathways)
+    if c.n_edges and n_path:
+        in_indptr, in_edge = side.by_target(L.N, n_path, L.stream)
+        BT = L.B * L.T
+        rows = torch.empty((n_path * L.N, BT), device=L.device)
+        gA = grad_A[k0: k0 + n_path]
+        _lib.check(
+            _lib.load().wt_weight_gradient_by_target(
+                edge_src.data_ptr(), c.n_edges, in_indptr.data_ptr(), in_edge.data_ptr(),
+                n_path, L.N, indptr.data_ptr(), bt.data_ptr(), value.data_ptr(),
+                gA.data_ptr(), BT, rows.data_ptr(), grad_e.data_ptr(), L.stream),
+            "wt_weight_gradient_by_target",
+        )  # fmt: skip
     if side.row_local is None:  # compressed side: the gradient of its weights
         return [grad_e if needs[0] else None]
     out = []

@@ -160,6 +160,40 @@ def config1(seed=1, T=5000, B=32) -> Workload:
     return wl
 
 
+def config3(seed=3, T=500, B=64, dt=1.0) -> Workload:
+    """The training step's network: N 10,000 (80/20), ER p = 0.02 with per-synapse learnt
+    weights (``FullRankProjection`` on the connectome), learnt per-type ``tau_mem`` and
+    ``theta``, fast-sigmoid surrogate of slope 10, 500 inputs at 5-20 Hz, batch 64,
+    T 500. dt is 1 ms (the configuration leaves it open): 500 ms, 25 bins of 20 ms for
+    the rate loss (``binned_rate_loss``)."""
+    rates = np.random.default_rng([seed, 99]).uniform(5.0, 20.0, 500)
+    half = {k: 0.5 * v for k, v in PAIR_SCALE.items()}  # in-degree 200
+    wl = er_network(N=10_000, frac_e=0.8, p=0.02, n_in=500, p_in=0.04, in_scale=8.0,
+                    rates_hz=rates, B=B, T=T, dt=dt, seed=seed, pair_scale=half,
+                    learnt=True, learn={"tau_mem": True, "theta": True},
+                    surrgrad_scale=10.0)
+    wl.name = "config3"
+    return wl
+
+
+def gamma_targets(seed: int, N: int, n_bins: int, shape=2.0, scale_hz=5.0) -> np.ndarray:
+    """Target rates (Hz) per (bin, neuron), drawn from gamma(shape, scale)."""
+    rng = np.random.default_rng([seed, 7])
+    return rng.gamma(shape, scale_hz, (n_bins, N)).astype(np.float32)
+
+
+def binned_rate_loss(spikes: torch.Tensor, target_hz: torch.Tensor, dt_ms: float,
+                     bin_ms: float = 20.0) -> torch.Tensor:
+    """Mean squared error between firing rates binned in ``bin_ms`` (Hz, averaged over the
+    batch) and ``target_hz`` (n_bins, N); steps past the last whole bin are dropped."""
+    B, T, N = spikes.shape
+    per_bin = int(round(bin_ms / dt_ms))
+    n_bins = T // per_bin
+    rates = spikes[:, : n_bins * per_bin].reshape(B, n_bins, per_bin, N).mean(dim=(0, 2))
+    rates = rates * (1000.0 / dt_ms)
+    return ((rates - target_hz[:n_bins]) ** 2).mean()
+
+
 # ---------------------------------------------------------------------------------
 # Fly scale (configuration 2)
 # ---------------------------------------------------------------------------------
