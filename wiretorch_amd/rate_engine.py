@@ -107,6 +107,15 @@ def _operand(drive, N: int, dtype, device) -> _Operand:
     return _cached(key, tuple(tensors), lambda: _Operand(drive.recurrent, N, dtype, device))
 
 
+def _columns(t: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
+    """``t[..., rows]`` — ``t`` itself (no copy) when ``rows`` are all of its columns in
+    order."""
+    n = t.shape[-1]
+    if rows.numel() == n and bool((rows == torch.arange(n, device=rows.device)).all()):
+        return t
+    return t[..., rows]
+
+
 def _input_activations(L, x) -> torch.Tensor | None:
     """``(K_ff, B, T, N)`` float32: ``x[:, :, rows] @ W_k`` per input pathway, one product
     for the whole call as the reference computes it (``network.py:142-157``); with a
@@ -117,7 +126,7 @@ def _input_activations(L, x) -> torch.Tensor | None:
     B, T, N = L.B, L.T, L.N
     A = torch.empty((L.K_ff, B, T, N), device=L.device)
     for j, (rows, W) in enumerate(L.feedforward):
-        xr = x.detach()[:, :, rows].reshape(B * T, -1).float()
+        xr = _columns(x.detach(), rows).reshape(B * T, -1).float()
         Wr = W.detach().float()
         if L.op.dtype != torch.float32:
             xr, Wr = xr.to(L.op.dtype).float(), Wr.to(L.op.dtype).float()
@@ -274,14 +283,14 @@ def _weight_and_input_grads(L: _Plan, out, x, grad_A, weights, w_needs, want_x):
     grad_w = [None] * len(weights)
     for k, rows in enumerate(L.rows_rec):
         if w_needs[k]:
-            r_k = out[:, :, rows].reshape(B * T, -1)
+            r_k = _columns(out, rows).reshape(B * T, -1)
             grad_w[k] = r_k.T @ grad_A[k].reshape(B * T, N)
     grad_x = torch.zeros_like(x, dtype=torch.float32) if want_x else None
     for j, (rows, W) in enumerate(zip(L.rows_ff, weights[L.K_rec:])):
         k = L.K_rec + j
         g = grad_A[k].reshape(B * T, N)
         if w_needs[k]:
-            grad_w[k] = x.detach().float()[:, :, rows].reshape(B * T, -1).T @ g
+            grad_w[k] = _columns(x.detach().float(), rows).reshape(B * T, -1).T @ g
         if want_x:
             grad_x[:, :, rows] += (g @ W.detach().float().T).reshape(B, T, -1)
     return grad_w, grad_x
