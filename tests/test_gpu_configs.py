@@ -3,6 +3,10 @@
 
 * Configuration 1 (forward, dt 0.1 ms): spike raster identical to the oracle's over the
   first 200 steps, voltages within 1e-5 relative — the bar of configuration 0.
+* Dense firing (a strongly driven configuration-3 network at 70 Hz, 16 trials, two per
+  workgroup): most steps list more fired sources per workgroup than its event list
+  holds (1,024), some more than twice that, so they are pushed in two or three rounds;
+  forward and training step to the bars of configurations 1 and 3.
 * Configuration 3 (training step: per-synapse learnt weights, learnt per-type tau_mem and
   theta, fast-sigmoid surrogate of slope 10, squared error of 20 ms-binned rates against
   gamma(2, 5 Hz) targets, dt 1 ms): over 100 steps, the same raster, the loss within 1e-5
@@ -62,6 +66,52 @@ def test_config3_training_step_matches_oracle():
     s_ref, l_ref, g_ref = _training_step(wl, x, target, oracle_engine, "cpu")
     s_gpu, l_gpu, g_gpu = _training_step(wl, x, target, engine, DEV)
     assert s_ref.sum() > 0
+    differs = (s_gpu != s_ref).any(axis=(0, 2))
+    assert not differs.any(), f"rasters differ from step {int(np.argmax(differs))}"
+    np.testing.assert_allclose(l_gpu, l_ref, rtol=1e-5)
+    assert g_ref.keys() == g_gpu.keys() and len(g_ref) == 6
+    for key, value in g_ref.items():
+        scale = np.abs(value).max()
+        assert scale > 0, key
+        np.testing.assert_allclose(g_gpu[key], value, rtol=0, atol=1e-4 * scale, err_msg=key)
+
+
+def _dense_workload():
+    rates = np.random.default_rng([5, 99]).uniform(20.0, 40.0, 500)
+    return synthetic.er_network(N=10_000, frac_e=0.8, p=0.02, n_in=500, p_in=0.04,
+                                in_scale=20.0, rates_hz=rates, B=16, T=40, dt=1.0, seed=5,
+                                learnt=True, learn={"tau_mem": True, "theta": True},
+                                surrgrad_scale=10.0)
+
+
+def _fired_per_workgroup_step(spikes):
+    """Sources fired per (group, step): every workgroup of a group lists the fired sources
+    of all the group's trials (trial b in group b % groups)."""
+    B, T, N = spikes.shape
+    groups, _, _ = engine.geometry(B, N, 2, 256, 160 * 1024)
+    return spikes.reshape(-1, groups, T, N).sum(axis=(0, 3))
+
+
+def test_dense_firing_forward_matches_oracle():
+    wl = _dense_workload()
+    x = torch.from_numpy(wl.x).float()
+    s_ref, v_ref = _forward(wl.model, x, oracle_engine)
+    per = _fired_per_workgroup_step(s_ref)
+    assert per.max() > 2 * 1024 and (per > 1024).mean() > 0.5, per.max()
+    wl.model.to(DEV)
+    s_gpu, v_gpu = _forward(wl.model, x.to(DEV), engine)
+    differs = (s_gpu != s_ref).any(axis=(0, 2))
+    assert not differs.any(), f"rasters differ from step {int(np.argmax(differs))}"
+    np.testing.assert_allclose(v_gpu, v_ref, rtol=1e-5, atol=1e-5 * 65)
+
+
+def test_dense_firing_training_step_matches_oracle():
+    wl = _dense_workload()
+    x = torch.from_numpy(wl.x).float()
+    target = torch.from_numpy(synthetic.gamma_targets(5, wl.N, 2))
+    s_ref, l_ref, g_ref = _training_step(wl, x, target, oracle_engine, "cpu")
+    assert _fired_per_workgroup_step(s_ref).max() > 2 * 1024
+    s_gpu, l_gpu, g_gpu = _training_step(wl, x, target, engine, DEV)
     differs = (s_gpu != s_ref).any(axis=(0, 2))
     assert not differs.any(), f"rasters differ from step {int(np.argmax(differs))}"
     np.testing.assert_allclose(l_gpu, l_ref, rtol=1e-5)

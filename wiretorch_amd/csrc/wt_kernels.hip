@@ -272,14 +272,16 @@ static int64_t run_tpg_max(const wt_geometry* geo, int64_t B) {
 // (fired bitmaps, the input lists) is written before it is read.
 static int64_t scratch_zeroed(const wt_geometry* geo) { return 256 + geo->groups * 128; }
 
-// Fired bitmaps: two buffers of [groups][tpg_max][R * words] words.
+// Fired bitmaps: three buffers of [groups][tpg_max][R * words] words (step t in buffer
+// t % 3: a workgroup still reads step t's bits after it has arrived at the barrier that
+// lets the others publish step t+1's).
 static int64_t bitmap_words(const wt_geometry* geo, int64_t B) {
   return geo->groups * run_tpg_max(geo, B) * geo->R * (geo->range_n / 32);
 }
 
 extern "C" int64_t wt_cond_run_scratch_bytes(const wt_geometry* geo, int64_t B, int64_t T) {
   int64_t bytes = scratch_zeroed(geo);
-  bytes += 2 * bitmap_words(geo, B) * 4;                  // fired bitmaps
+  bytes += 3 * bitmap_words(geo, B) * 4;                  // fired bitmaps
   bytes = (bytes + 255) / 256 * 256;
   bytes += B * T * 4;                                     // input counts
   bytes += B * T * kInCap * 8;                            // input indices and values
@@ -322,7 +324,7 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
   a.barrier = reinterpret_cast<uint32_t*>(base + 256);
   a.bitmap = reinterpret_cast<uint32_t*>(base + scratch_zeroed(geo));
   a.tpg_max = tpg;
-  int64_t off = scratch_zeroed(geo) + 2 * bitmap_words(geo, io->B) * 4;
+  int64_t off = scratch_zeroed(geo) + 3 * bitmap_words(geo, io->B) * 4;
   off = (off + 255) / 256 * 256;
   int32_t* in_count = reinterpret_cast<int32_t*>(base + off);
   off += io->B * io->T * 4;

@@ -203,6 +203,21 @@ __device__ inline void append_event(const EventList& L, double* acc, const int32
   }
 }
 
+// An event into the list if it has room; false (and nothing else done) if it has not —
+// the caller keeps the event for the next round.
+__device__ inline bool try_append(const EventList& L, int side_id, int64_t e0, int64_t e1,
+                                  int64_t row, int64_t lo, float value) {
+  if (e1 <= e0) return true;
+  const int pos = atomicAdd(L.n, 1);
+  if (pos >= kRunBlock) return false;
+  L.e0[pos] = e0;
+  L.count[pos] = (int32_t)(e1 - e0);
+  L.row[pos] = (int32_t)(row - lo);
+  L.value[pos] = value;
+  L.side[pos] = (uint8_t)side_id;
+  return true;
+}
+
 // Every listed synapse, spread evenly over the workgroup (four per thread per round,
 // loads issued before the atomics), added to the accumulator. L.count holds the
 // exclusive prefix of the entries' edge counts.
@@ -261,6 +276,7 @@ __device__ inline void run_events(const EventList& L, int m, int32_t total, doub
 // the whole launch.
 template <int S, int MAXI, bool EXTRA, bool REFR>
 __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
+  static_assert(MAXI <= 8, "the overflow note holds one bit per preloaded word");
   extern __shared__ __align__(16) double acc[];  // [K][tpg][range_n]
   __shared__ __align__(16) float s_types[kMaxLdsTypes * kRow];
   __shared__ uint32_t s_bits[kMaxOwnWords];  // [tpg][words]: the next step's own spikes
@@ -410,9 +426,9 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     ++phase;
   }
 
-  for (int32_t t = 0; t < T; ++t) {
+  for (int32_t t = 0, buf = 0; t < T; ++t, buf = buf == 2 ? 0 : buf + 1) {
     const bool more = t + 1 < T;
-    const uint32_t* in_bits = group_bits + (t & 1) * buffer_words;
+    const uint32_t* in_bits = group_bits + buf * buffer_words;  // step t: buffer t % 3
     // ---- the group's fired bits of step t: complete once every workgroup arrived ----
     if (recurrent) {
       if (!barrier_wait(my_barrier, phase * (uint32_t)R, A.err, &s_flag)) return;
@@ -445,28 +461,32 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
 
     // ---------------- events of step t, listed before the update ----------------
     // The fired bits of the preloaded words are compacted into s_fired (source | trial
-    // << 24); bits past its capacity stay in rest[u], to be handled after the update.
+    // << 24); the bits past its capacity are noted in rest and read again from the
+    // bitmap after the update.
     // Then one thread per listed source, and per listed input, issues its range lookups
     // (and pathway) into registers: their latency passes during the update.
-    uint32_t rest[MAXI];
+    // rest: bit u (u < 8) — every fired bit of preloaded word u is past the list's
+    // capacity; bits 8-15 = u + 1 and bits 16-23 = k for the word whose k lowest fired
+    // bits were listed and whose others were not (at most one per workgroup).
+    uint32_t rest = 0u;
 #pragma unroll
     for (int u = 0; u < MAXI; ++u) {
-      rest[u] = 0u;
       uint32_t bits = pre[u];
       if (!bits) continue;
       const uint32_t w = threadIdx.x + (uint32_t)u * blockDim.x;
       const uint32_t q = w / (uint32_t)total_words, wl = w - q * (uint32_t)total_words;
       const uint32_t j0 =
           (wl / (uint32_t)words) * (uint32_t)range_n + (wl % (uint32_t)words) * 32;
-      int pos = atomicAdd(&s_nfired, __builtin_popcount(bits));
-      while (bits) {
-        const uint32_t bit = __builtin_ctz(bits);
+      const int n = __builtin_popcount(bits);
+      int pos = atomicAdd(&s_nfired, n);
+      if (pos >= kRunBlock) {
+        rest |= 1u << u;
+        continue;
+      }
+      if (pos + n > kRunBlock) rest |= (uint32_t)(u + 1) << 8 | (uint32_t)(kRunBlock - pos) << 16;
+      for (; bits && pos < kRunBlock; ++pos) {
+        s_fired[pos] = (j0 + __builtin_ctz(bits)) | (q << 24);
         bits &= bits - 1;
-        if (pos < kRunBlock)
-          s_fired[pos] = (j0 + bit) | (q << 24);
-        else
-          rest[u] |= 1u << bit;
-        ++pos;
       }
     }
     __syncthreads();
@@ -600,7 +620,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     // ---------------- publish step t+1's spikes ----------------
     const bool publish = recurrent && more;
     if (publish) {
-      uint32_t* out_bits = group_bits + ((t + 1) & 1) * buffer_words;
+      uint32_t* out_bits = group_bits + (buf == 2 ? 0 : buf + 1) * buffer_words;
       for (int64_t w = threadIdx.x; w < tpg * words; w += blockDim.x) {
         const int64_t q = w / words;
         store_agent(out_bits + q * total_words + r * words + (w - q * words), s_bits[w]);
@@ -608,37 +628,33 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     }
 
     // ---------------- events of step t, after the update ----------------
-    // (1) What the list could not hold — fired sources past its capacity and in words
-    // beyond the preload, inputs of rows with more than kInCap of them — is appended by
-    // the thread that holds it (an event past the event list's capacity is pushed at
-    // once: the update has already read the accumulator). Every read of this step's
-    // bitmap happens before the arrival at the barrier.
+    // (1) Fired sources in bitmap words beyond the preload, and inputs of rows with more
+    // than kInCap of them, are appended by the thread that finds them (an event past the
+    // list's capacity is pushed at once: the update has already read the accumulator).
+    // Step t's bitmap stays readable after the arrival at the barrier: the others write
+    // step t+1's bits into the next of three buffers, and step t+2's only once this
+    // workgroup has arrived again.
     {
       ArgPtr P = kargs();
       const int64_t* rec_split = P->rec.split;
       const int32_t* rec_path = P->rec.pathway;
-      auto direct = [&](uint32_t w, uint32_t bits) {
-        const uint32_t q = w / (uint32_t)total_words, wl = w - q * (uint32_t)total_words;
-        const uint32_t j0 =
-            (wl / (uint32_t)words) * (uint32_t)range_n + (wl % (uint32_t)words) * 32;
-        while (bits) {
-          const uint32_t j = j0 + __builtin_ctz(bits);
-          bits &= bits - 1;
-          const int32_t k = gload(rec_path + j);
-          const int64_t* sp = rec_split + (int64_t)j * (R + 1) + r;
-          if (k >= 0)
-            append_event(EL, acc, P->rec.targets, P->rec.weights, 0, gload(sp), gload(sp + 1),
-                         k * acc_stride + (int64_t)q * range_n, lo, 1.0f, fx);
-        }
-      };
       if (recurrent) {
-#pragma unroll
-        for (int u = 0; u < MAXI; ++u)
-          if (rest[u]) direct(threadIdx.x + (uint32_t)u * blockDim.x, rest[u]);
         for (int64_t w = threadIdx.x + (int64_t)MAXI * blockDim.x; w < group_words;
              w += blockDim.x) {
-          const uint32_t bits = load_agent(in_bits + w);
-          if (bits) direct((uint32_t)w, bits);
+          uint32_t bits = load_agent(in_bits + w);
+          const uint32_t q = (uint32_t)w / (uint32_t)total_words;
+          const uint32_t wl = (uint32_t)w - q * (uint32_t)total_words;
+          const uint32_t j0 =
+              (wl / (uint32_t)words) * (uint32_t)range_n + (wl % (uint32_t)words) * 32;
+          while (bits) {
+            const uint32_t j = j0 + __builtin_ctz(bits);
+            bits &= bits - 1;
+            const int32_t k = gload(rec_path + j);
+            const int64_t* sp = rec_split + (int64_t)j * (R + 1) + r;
+            if (k >= 0)
+              append_event(EL, acc, P->rec.targets, P->rec.weights, 0, gload(sp),
+                           gload(sp + 1), k * acc_stride + (int64_t)q * range_n, lo, 1.0f, fx);
+          }
         }
       }
       if (has_ff) {
@@ -667,28 +683,72 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       __syncthreads();
     }
     tick(s_time, 2);
-    // (2) The listed sources and inputs, whose lookups were issued before the update.
+    // (2) The listed sources and inputs (their lookups issued before the update), then
+    // the fired sources the list could not hold (rest), in rounds of at most kRunBlock
+    // events: each round appends what fits, scans and pushes it. A round that could not
+    // take every event leaves the list's count past its capacity — read by every thread
+    // after the round's barrier — and the events not taken for the next round. (Sparse
+    // firing takes one round.)
     {
       ArgPtr P = kargs();
-      if (rk >= 0)
-        append_event(EL, acc, P->rec.targets, P->rec.weights, 0, re0, re1,
-                     rk * acc_stride + (int64_t)(rj >> 24) * range_n, lo, 1.0f, fx);
-      if (ik >= 0)
-        append_event(EL, acc, P->ff.targets, P->ff.weights, 1, ie0, ie1,
-                     (P->tab.K_rec * tpg + (int64_t)(threadIdx.x / kInCap)) * range_n +
-                         ik * acc_stride,
-                     lo, in_v, fx);
-    }
-    __syncthreads();
-    {
-      const int m = s_nev < kRunBlock ? s_nev : kRunBlock;
-      if (m > 0) {  // m is uniform: every thread takes part in the scan
-        const int tid = threadIdx.x;
-        int32_t c = tid < m ? s_count[tid] : 0, total;
-        BlockScan().exclusive_scan(c, c, 0, total, s_scan);
-        if (tid < m) s_count[tid] = c;
+      bool rec_pending = rk >= 0, in_pending = ik >= 0;
+      uint32_t rest_bits[MAXI];
+#pragma unroll
+      for (int u = 0; u < MAXI; ++u) {
+        rest_bits[u] = 0u;
+        const bool whole = (rest >> u) & 1u, split = ((rest >> 8) & 0xffu) == (uint32_t)(u + 1);
+        if (whole || split) {
+          rest_bits[u] = load_agent(in_bits + threadIdx.x + (uint32_t)u * blockDim.x);
+          if (split)
+            for (uint32_t k = (rest >> 16) & 0xffu; k > 0; --k) rest_bits[u] &= rest_bits[u] - 1;
+        }
+      }
+      for (;;) {
+        if (rec_pending)
+          rec_pending = !try_append(EL, 0, re0, re1,
+                                    rk * acc_stride + (int64_t)(rj >> 24) * range_n, lo, 1.0f);
+        if (in_pending)
+          in_pending = !try_append(EL, 1, ie0, ie1,
+                                   (P->tab.K_rec * tpg + (int64_t)(threadIdx.x / kInCap)) *
+                                           range_n + ik * acc_stride,
+                                   lo, in_v);
+        bool full = false;
+#pragma unroll
+        for (int u = 0; u < MAXI; ++u) {
+          if (full || !rest_bits[u]) continue;
+          const uint32_t w = threadIdx.x + (uint32_t)u * blockDim.x;
+          const uint32_t q = w / (uint32_t)total_words, wl = w - q * (uint32_t)total_words;
+          const uint32_t j0 =
+              (wl / (uint32_t)words) * (uint32_t)range_n + (wl % (uint32_t)words) * 32;
+          while (rest_bits[u]) {
+            const uint32_t j = j0 + __builtin_ctz(rest_bits[u]);
+            const int32_t k = gload(P->rec.pathway + j);
+            if (k >= 0) {
+              const int64_t* sp = P->rec.split + (int64_t)j * (R + 1) + r;
+              if (!try_append(EL, 0, gload(sp), gload(sp + 1),
+                              k * acc_stride + (int64_t)q * range_n, lo, 1.0f)) {
+                full = true;
+                break;
+              }
+            }
+            rest_bits[u] &= rest_bits[u] - 1;
+          }
+        }
         __syncthreads();
-        run_events(EL, m, total, acc, lo, fx);
+        const int n_ev = s_nev;
+        const int m = n_ev < kRunBlock ? n_ev : kRunBlock;
+        if (m > 0) {  // m is uniform: every thread takes part in the scan
+          const int tid = threadIdx.x;
+          int32_t c = tid < m ? s_count[tid] : 0, total;
+          BlockScan().exclusive_scan(c, c, 0, total, s_scan);
+          if (tid < m) s_count[tid] = c;
+          __syncthreads();
+          run_events(EL, m, total, acc, lo, fx);
+        }
+        if (n_ev <= kRunBlock) break;  // uniform: every event of the step was taken
+        __syncthreads();  // the list is consumed
+        if (threadIdx.x == 0) s_nev = 0;
+        __syncthreads();
       }
     }
     __syncthreads();  // the accumulator is complete for the next update
