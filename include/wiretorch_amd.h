@@ -123,10 +123,11 @@ int wt_cond_run(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
 
 /* wt_cond_run_timed — wt_cond_run with per-workgroup wall-clock ticks (100 MHz) of each
  * phase of the step loop, as seen by the workgroup's first thread, added to
- * timing[wg * 5 + phase], phases: its own neuron update, the wait for the rest of the
- * workgroup's update, publication + event listing + barrier arrival, barrier wait,
- * range lookups + scan + synapse push. For profiling; no counterpart in the reference.
- * timing: (groups * R * 5) u64. */
+ * timing[wg * 8 + phase], phases: 0 bitmap and input loads + clears, 1 listing of the
+ * fired sources, 2 range lookups + its own neuron update, 3 the wait for the rest of the
+ * workgroup's update, 4 publication + unlisted events + barrier arrival, 5 barrier wait,
+ * 6 appends to the event list, 7 scan + synapse push (+ further rounds). For profiling;
+ * no counterpart in the reference. timing: (groups * R * 8) u64. */
 int wt_cond_run_timed(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
                       const wt_geometry* geo, const wt_run_io* io, void* scratch,
                       uint64_t* timing, wt_stream_t stream);

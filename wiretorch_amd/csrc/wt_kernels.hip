@@ -351,7 +351,8 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
   if (qe != hipSuccess) return qe;
   const size_t static_lds = kRunBlock * (8 + 4 + 4 + 4 + 1 + 4) +
                             sizeof(BlockScan::storage_type) + (kPhases + 1) * 8 + 64 +
-                            kMaxLdsTypes * kRow * 4 + kMaxOwnWords * 4 + kMaxItemsPerWg;
+                            kMaxLdsTypes * kRow * 4 + kMaxOwnWords * 4 + kMaxItemsPerWg +
+                            kBuckets * (2 + 8);
   if (lds + static_lds > (size_t)max_lds) return hipErrorInvalidValue;
   if (ff->n_src > 0 && io->x) {
     const int64_t rows = io->B * io->T;

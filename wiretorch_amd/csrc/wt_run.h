@@ -48,7 +48,7 @@ struct RunArgs {
 // Phases timed by wt_cond_run_timed (thread 0's view): its own update, the wait for the
 // rest of the workgroup's update, publication + event compaction + arrival, the barrier
 // wait, range lookups + scan + synapse push.
-constexpr int kPhases = 5;
+constexpr int kPhases = 8;
 constexpr int kInCap = 64;  // inputs listed per (trial, step); denser rows are scanned
 constexpr int kMaxLdsTypes = 256;
 constexpr int kTypeCols = 6;  // global table: theta, U_reset, E_L, C_m, beta, n_ref; scale[K]
@@ -56,6 +56,7 @@ constexpr int kTypeCols = 6;  // global table: theta, U_reset, E_L, C_m, beta, n
 constexpr int kRow = 16;
 constexpr int kMaxItemsPerWg = 8 * kRunBlock;        // trials x range per workgroup
 constexpr int kMaxOwnWords = kMaxItemsPerWg / 32;    // the workgroup's own fired bits
+constexpr int kBuckets = 256;  // 64-edge buckets of a scanned event list with a direct entry map
 
 using BlockScan = rocprim::block_scan<int32_t, kRunBlock,
                                       rocprim::block_scan_algorithm::using_warp_scan>;
@@ -184,7 +185,10 @@ struct EventList {
   int32_t* row;
   float* value;
   uint8_t* side;
-  int32_t* n;      // entries appended (may exceed the capacity: the rest ran serially)
+  int32_t* n;      // entries appended; past the capacity, events pushed at once by
+                   // append_event or left for another round
+  int16_t* first;  // [kBuckets] after the scan: the entry holding edge 64 b
+  uint64_t* heads; // [kBuckets] after the scan: bit f % 64 of word f / 64 where an entry starts
 };
 
 __device__ inline void append_event(const EventList& L, double* acc, const int32_t* targets,
@@ -203,24 +207,52 @@ __device__ inline void append_event(const EventList& L, double* acc, const int32
   }
 }
 
-// An event into the list if it has room; false (and nothing else done) if it has not —
-// the caller keeps the event for the next round.
-__device__ inline bool try_append(const EventList& L, int side_id, int64_t e0, int64_t e1,
-                                  int64_t row, int64_t lo, float value) {
-  if (e1 <= e0) return true;
-  const int pos = atomicAdd(L.n, 1);
-  if (pos >= kRunBlock) return false;
+// Entry pos of the event list: a source whose edges [e0, e1) land on `row` (absolute).
+__device__ inline void put_event(const EventList& L, int pos, int side_id, int64_t e0,
+                                 int64_t e1, int64_t row, int64_t lo, float value) {
   L.e0[pos] = e0;
   L.count[pos] = (int32_t)(e1 - e0);
   L.row[pos] = (int32_t)(row - lo);
   L.value[pos] = value;
   L.side[pos] = (uint8_t)side_id;
-  return true;
+}
+
+// Exclusive prefix of n (0 <= n < 2^BITS) over the lanes of the wave below this one, and
+// the wave's total, from one ballot per bit. Every lane of the wave takes part.
+template <int BITS>
+__device__ inline uint32_t wave_prefix(uint32_t n, uint32_t& total) {
+  uint32_t below = 0, all = 0;
+#pragma unroll
+  for (int b = 0; b < BITS; ++b) {
+    const uint64_t m = __ballot((n >> b) & 1u);
+    below += __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                       __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u)) << b;
+    all += (uint32_t)__builtin_popcountll(m) << b;
+  }
+  total = all;
+  return below;
+}
+
+template <int M>
+__device__ inline bool rest_any(const uint32_t (&bits)[M]) {
+  uint32_t any = 0;
+#pragma unroll
+  for (int u = 0; u < M; ++u) any |= bits[u];
+  return any != 0;
+}
+
+// The wave's first position of `total` consecutive ones taken from an LDS counter: one
+// atomic per wave. Every lane of the wave takes part; all receive the same base.
+__device__ inline int wave_reserve(int32_t* counter, uint32_t total) {
+  int base = 0;
+  if (__lane_id() == 0 && total != 0) base = atomicAdd(counter, (int)total);
+  return __builtin_amdgcn_readfirstlane(base);
 }
 
 // Every listed synapse, spread evenly over the workgroup (four per thread per round,
-// loads issued before the atomics), added to the accumulator. L.count holds the
-// exclusive prefix of the entries' edge counts.
+// loads issued before the atomics), added to the accumulator. After the scan L.count
+// holds the exclusive prefix of the entries' edge counts, L.e0 each entry's first edge
+// minus its prefix, and L.first / L.heads the entry map of the first kBuckets buckets.
 __device__ inline void run_events(const EventList& L, int m, int32_t total, double* acc,
                                   int64_t lo, Fixed fx) {
   ArgPtr P = kargs();
@@ -229,31 +261,42 @@ __device__ inline void run_events(const EventList& L, int m, int32_t total, doub
   const float* const rec_w = P->rec.weights;
   const float* const ff_w = P->ff.weights;
   const int stride = blockDim.x;
+  const int nb = (total + 63) >> 6;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint64_t upto = (2ull << lane) - 1ull;  // bucket positions 0 .. lane
   for (int32_t base = threadIdx.x; base < total; base += 4 * stride) {
     // three passes, so that all eight loads are in flight together: locate each edge's
-    // entry (LDS), load the edges (HBM), add them (LDS atomics)
+    // entry (LDS), load the edges (HBM), add them (LDS atomics).
+    // A wave's 64 edges at u are 64-edge bucket b = (base + u * stride) / 64 (stride is a
+    // multiple of 64): lane l's entry is the bucket's first entry plus the entries that
+    // start at bucket positions 1 .. l. Past the map, a binary search over the prefixes.
+    int a[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int32_t f = base + u * stride, b = f >> 6;
+      if (b >= nb) {
+        a[u] = 0;  // no edge of the wave here
+      } else if (b < kBuckets) {
+        a[u] = L.first[b] + __builtin_popcountll(L.heads[b] & upto & ~1ull);
+      } else {
+        int lo2 = L.first[kBuckets - 1], z = m;
+        while (z - lo2 > 1) {
+          const int mid = (lo2 + z) >> 1;
+          if (L.count[mid] <= f) lo2 = mid; else z = mid;
+        }
+        a[u] = lo2;
+      }
+    }
     int64_t e[4];
     int32_t rows[4];
     float val[4];
     bool input[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int32_t f = base + u * stride;
-      e[u] = 0;
-      rows[u] = 0;
-      val[u] = 0.0f;
-      input[u] = false;
-      if (f < total) {
-        int a = 0, z = m;  // entry a with prefix[a] <= f < prefix[a + 1]
-        while (z - a > 1) {
-          const int mid = (a + z) >> 1;
-          if (L.count[mid] <= f) a = mid; else z = mid;
-        }
-        e[u] = L.e0[a] + (f - L.count[a]);
-        input[u] = L.side[a] != 0;
-        val[u] = L.value[a];
-        rows[u] = L.row[a];  // may be negative: rows are relative to the range start
-      }
+      e[u] = L.e0[a[u]] + (base + u * stride);  // e0 holds the entry's first edge - prefix
+      input[u] = L.side[a[u]] != 0;
+      val[u] = L.value[a[u]];
+      rows[u] = L.row[a[u]];  // may be negative: rows are relative to the range start
     }
     int32_t tgt[4];
     float w[4];
@@ -316,7 +359,9 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   const bool has_ff = A.ff.n_src > 0;
   const float dt = *A.tab.dt;
   const Fixed fx{ldexpf(1.0f, (int)A.geo.frac_bits), ldexp(1.0, -(int)A.geo.frac_bits)};
-  const EventList EL{s_e0, s_count, s_row, s_value, s_side, &s_nev};
+  __shared__ int16_t s_first[kBuckets];
+  __shared__ uint64_t s_heads[kBuckets];
+  const EventList EL{s_e0, s_count, s_row, s_value, s_side, &s_nev, s_first, s_heads};
   Synapses<S> syn;
   load_synapses<S>(A.tab, syn);
   uint64_t made = 0;  // bit k * S + s: pathway k drives synapse type s
@@ -433,7 +478,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     if (recurrent) {
       if (!barrier_wait(my_barrier, phase * (uint32_t)R, A.err, &s_flag)) return;
     }
-    tick(s_time, 3);
+    tick(s_time, 5);
     uint32_t pre[MAXI];
 #pragma unroll
     for (int u = 0; u < MAXI; ++u) {
@@ -458,6 +503,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       s_nfired = 0;
     }
     __syncthreads();
+    tick(s_time, 0);
 
     // ---------------- events of step t, listed before the update ----------------
     // The fired bits of the preloaded words are compacted into s_fired (source | trial
@@ -472,24 +518,29 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
 #pragma unroll
     for (int u = 0; u < MAXI; ++u) {
       uint32_t bits = pre[u];
+      if (__ballot(bits != 0u) == 0) continue;  // uniform over the wave
+      const uint32_t n = __builtin_popcount(bits);
+      uint32_t total;
+      const uint32_t below = wave_prefix<6>(n, total);
+      int pos = wave_reserve(&s_nfired, total) + (int)below;
       if (!bits) continue;
       const uint32_t w = threadIdx.x + (uint32_t)u * blockDim.x;
       const uint32_t q = w / (uint32_t)total_words, wl = w - q * (uint32_t)total_words;
       const uint32_t j0 =
           (wl / (uint32_t)words) * (uint32_t)range_n + (wl % (uint32_t)words) * 32;
-      const int n = __builtin_popcount(bits);
-      int pos = atomicAdd(&s_nfired, n);
       if (pos >= kRunBlock) {
         rest |= 1u << u;
         continue;
       }
-      if (pos + n > kRunBlock) rest |= (uint32_t)(u + 1) << 8 | (uint32_t)(kRunBlock - pos) << 16;
+      if (pos + (int)n > kRunBlock)
+        rest |= (uint32_t)(u + 1) << 8 | (uint32_t)(kRunBlock - pos) << 16;
       for (; bits && pos < kRunBlock; ++pos) {
         s_fired[pos] = (j0 + __builtin_ctz(bits)) | (q << 24);
         bits &= bits - 1;
       }
     }
     __syncthreads();
+    tick(s_time, 1);
     int64_t re0 = 0, re1 = 0, ie0 = 0, ie1 = 0;
     int32_t rk = -1, ik = -1;
     uint32_t rj = 0;
@@ -613,9 +664,9 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       update(std::false_type{});
     else
       update(std::true_type{});
-    tick(s_time, 0);
+    tick(s_time, 2);
     __syncthreads();  // the accumulator is read and cleared; the next bits are complete
-    tick(s_time, 1);
+    tick(s_time, 3);
 
     // ---------------- publish step t+1's spikes ----------------
     const bool publish = recurrent && more;
@@ -682,7 +733,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     } else {
       __syncthreads();
     }
-    tick(s_time, 2);
+    tick(s_time, 4);
     // (2) The listed sources and inputs (their lookups issued before the update), then
     // the fired sources the list could not hold (rest), in rounds of at most kRunBlock
     // events: each round appends what fits, scans and pushes it. A round that could not
@@ -691,68 +742,161 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     // firing takes one round.)
     {
       ArgPtr P = kargs();
-      bool rec_pending = rk >= 0, in_pending = ik >= 0;
+      bool rec_pending = rk >= 0 && re1 > re0, in_pending = ik >= 0 && ie1 > ie0;
       uint32_t rest_bits[MAXI];
 #pragma unroll
-      for (int u = 0; u < MAXI; ++u) {
-        rest_bits[u] = 0u;
-        const bool whole = (rest >> u) & 1u, split = ((rest >> 8) & 0xffu) == (uint32_t)(u + 1);
-        if (whole || split) {
-          rest_bits[u] = load_agent(in_bits + threadIdx.x + (uint32_t)u * blockDim.x);
+      for (int u = 0; u < MAXI; ++u) rest_bits[u] = 0u;
+      if (rest) {  // every word read at once (an index past the group's words is clamped)
+#pragma unroll
+        for (int u = 0; u < MAXI; ++u) {
+          const int64_t w = threadIdx.x + (int64_t)u * blockDim.x;
+          rest_bits[u] = load_agent(in_bits + (w < group_words ? w : group_words - 1));
+        }
+#pragma unroll
+        for (int u = 0; u < MAXI; ++u) {
+          const bool whole = (rest >> u) & 1u;
+          const bool split = ((rest >> 8) & 0xffu) == (uint32_t)(u + 1);
+          if (!whole && !split) rest_bits[u] = 0u;
           if (split)
             for (uint32_t k = (rest >> 16) & 0xffu; k > 0; --k) rest_bits[u] &= rest_bits[u] - 1;
         }
       }
       for (;;) {
-        if (rec_pending)
-          rec_pending = !try_append(EL, 0, re0, re1,
-                                    rk * acc_stride + (int64_t)(rj >> 24) * range_n, lo, 1.0f);
-        if (in_pending)
-          in_pending = !try_append(EL, 1, ie0, ie1,
-                                   (P->tab.K_rec * tpg + (int64_t)(threadIdx.x / kInCap)) *
-                                           range_n + ik * acc_stride,
-                                   lo, in_v);
-        bool full = false;
-#pragma unroll
-        for (int u = 0; u < MAXI; ++u) {
-          if (full || !rest_bits[u]) continue;
-          const uint32_t w = threadIdx.x + (uint32_t)u * blockDim.x;
-          const uint32_t q = w / (uint32_t)total_words, wl = w - q * (uint32_t)total_words;
-          const uint32_t j0 =
-              (wl / (uint32_t)words) * (uint32_t)range_n + (wl % (uint32_t)words) * 32;
-          while (rest_bits[u]) {
-            const uint32_t j = j0 + __builtin_ctz(rest_bits[u]);
-            const int32_t k = gload(P->rec.pathway + j);
-            if (k >= 0) {
-              const int64_t* sp = P->rec.split + (int64_t)j * (R + 1) + r;
-              if (!try_append(EL, 0, gload(sp), gload(sp + 1),
-                              k * acc_stride + (int64_t)q * range_n, lo, 1.0f)) {
-                full = true;
-                break;
-              }
+        // the listed source and input of each thread: one reservation per wave
+        {
+          uint32_t total;
+          const uint32_t below = wave_prefix<2>((uint32_t)rec_pending + in_pending, total);
+          int pos = wave_reserve(EL.n, total) + (int)below;
+          if (rec_pending) {
+            if (pos < kRunBlock) {
+              put_event(EL, pos, 0, re0, re1, rk * acc_stride + (int64_t)(rj >> 24) * range_n,
+                        lo, 1.0f);
+              rec_pending = false;
             }
-            rest_bits[u] &= rest_bits[u] - 1;
+            ++pos;
+          }
+          if (in_pending && pos < kRunBlock) {
+            put_event(EL, pos, 1, ie0, ie1,
+                      (P->tab.K_rec * tpg + (int64_t)(threadIdx.x / kInCap)) * range_n +
+                          ik * acc_stride,
+                      lo, in_v);
+            in_pending = false;
           }
         }
+        // the unlisted fired sources, up to kTake per thread at a time with their lookups
+        // in flight together, while the wave has any and the list has room
+        // (a list already full takes nothing more this round: its count, which only
+        // grows, then calls for another)
+        while (__ballot(rest_any(rest_bits)) != 0 &&
+               __builtin_amdgcn_readfirstlane(*EL.n) < kRunBlock) {
+          constexpr int kTake = 4;
+          uint32_t src[kTake], trial[kTake];
+          bool has[kTake];
+          {
+            uint32_t left[MAXI];
+#pragma unroll
+            for (int u = 0; u < MAXI; ++u) left[u] = rest_bits[u];
+#pragma unroll
+            for (int c = 0; c < kTake; ++c) {
+              has[c] = false;
+              src[c] = 0;
+              trial[c] = 0;
+#pragma unroll
+              for (int u = 0; u < MAXI; ++u) {
+                if (has[c] || !left[u]) continue;
+                const uint32_t w = threadIdx.x + (uint32_t)u * blockDim.x;
+                const uint32_t q = w / (uint32_t)total_words, wl = w - q * (uint32_t)total_words;
+                src[c] = (wl / (uint32_t)words) * (uint32_t)range_n +
+                         (wl % (uint32_t)words) * 32 + __builtin_ctz(left[u]);
+                trial[c] = q;
+                left[u] &= left[u] - 1;
+                has[c] = true;
+              }
+            }
+          }
+          int32_t kk[kTake];
+          int64_t f0[kTake], f1[kTake];
+#pragma unroll
+          for (int c = 0; c < kTake; ++c) {
+            kk[c] = -1;
+            f0[c] = f1[c] = 0;
+            if (has[c]) {
+              const int64_t* sp = P->rec.split + (int64_t)src[c] * (R + 1) + r;
+              kk[c] = gload(P->rec.pathway + src[c]);
+              f0[c] = gload(sp);
+              f1[c] = gload(sp + 1);
+            }
+          }
+          uint32_t n = 0;
+#pragma unroll
+          for (int c = 0; c < kTake; ++c) n += (has[c] && kk[c] >= 0 && f1[c] > f0[c]) ? 1u : 0u;
+          uint32_t total;
+          const uint32_t below = wave_prefix<3>(n, total);
+          const int base = wave_reserve(EL.n, total);
+          int pos = base + (int)below;
+          // taken sources are consumed in order up to the first event without room
+          int consumed = 0;
+          bool stop = false;
+#pragma unroll
+          for (int c = 0; c < kTake; ++c) {
+            if (!has[c] || stop) continue;
+            if (kk[c] >= 0 && f1[c] > f0[c]) {
+              if (pos >= kRunBlock) {
+                stop = true;
+                continue;
+              }
+              put_event(EL, pos, 0, f0[c], f1[c],
+                        kk[c] * acc_stride + (int64_t)trial[c] * range_n, lo, 1.0f);
+              ++pos;
+            }
+            ++consumed;
+          }
+#pragma unroll
+          for (int c = 0; c < kTake; ++c) {
+            if (c >= consumed) continue;
+            bool done = false;
+#pragma unroll
+            for (int u = 0; u < MAXI; ++u) {
+              if (done || !rest_bits[u]) continue;
+              rest_bits[u] &= rest_bits[u] - 1;
+              done = true;
+            }
+          }
+          if (base + (int)total >= kRunBlock) break;  // uniform: the list is full
+        }
+        // the entry map is cleared for this round's scan (its last reader, the previous
+        // round's push, is behind a barrier; its next writer after the one below)
+        for (int w = threadIdx.x; w < kBuckets; w += blockDim.x) s_heads[w] = 0;
         __syncthreads();
+        tick(s_time, 6);
         const int n_ev = s_nev;
         const int m = n_ev < kRunBlock ? n_ev : kRunBlock;
         if (m > 0) {  // m is uniform: every thread takes part in the scan
           const int tid = threadIdx.x;
           int32_t c = tid < m ? s_count[tid] : 0, total;
+          const int32_t cnt = c;
           BlockScan().exclusive_scan(c, c, 0, total, s_scan);
-          if (tid < m) s_count[tid] = c;
+          if (tid < m) {  // entry tid holds edges [c, c + cnt) of the round, cnt > 0
+            s_count[tid] = c;
+            s_e0[tid] -= c;
+            for (int32_t b = (c + 63) >> 6; b < kBuckets && (b << 6) < c + cnt; ++b)
+              s_first[b] = (int16_t)tid;
+            if (c < kBuckets * 64)
+              atomicOr((unsigned long long*)&s_heads[c >> 6], 1ull << (c & 63));
+          }
           __syncthreads();
           run_events(EL, m, total, acc, lo, fx);
         }
-        if (n_ev <= kRunBlock) break;  // uniform: every event of the step was taken
+        if (n_ev < kRunBlock) break;  // uniform: every event of the step was taken
+        // (a full list may leave events: n_ev == kRunBlock takes one more, possibly empty,
+        // round)
         __syncthreads();  // the list is consumed
         if (threadIdx.x == 0) s_nev = 0;
         __syncthreads();
       }
     }
     __syncthreads();  // the accumulator is complete for the next update
-    tick(s_time, 4);
+    tick(s_time, 7);
   }
 
   // The activations of the last step enter the conductances that leave the chunk.

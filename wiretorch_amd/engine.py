@@ -70,8 +70,10 @@ class _timed:
             stop.record()
             PART_EVENTS.setdefault(self.name, []).append((self.start, stop))
 #: When a list, launches run ``wt_cond_run_timed`` and append the per-workgroup phase
-#: ticks ``(groups * R, 5)`` (profiling only).
+#: ticks ``(groups * R, 8)`` (profiling only; the phases are listed with the entry point).
 PHASE_TIMING: list | None = None
+#: Phase slots per workgroup that ``wt_cond_run_timed`` writes.
+PHASES = 8
 
 
 # =====================================================================
@@ -448,7 +450,7 @@ def _launch(L: _Plan, x, scale, v, g, counter, spikes, prob, saved, tracked,
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
     if PHASE_TIMING is not None:
-        ticks = torch.zeros((groups * R, 5), dtype=torch.int64, device=L.device)
+        ticks = torch.zeros((groups * R, PHASES), dtype=torch.int64, device=L.device)
         _lib.check(lib.wt_cond_run_timed(tab, rec, ff, geo, io, scratch.data_ptr(),
                                          ticks.data_ptr(), L.stream), "wt_cond_run_timed")
         PHASE_TIMING.append(ticks)
