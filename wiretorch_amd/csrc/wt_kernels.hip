@@ -349,11 +349,29 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
   if (qe == hipSuccess)
     qe = hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   if (qe != hipSuccess) return qe;
-  const size_t static_lds = kRunBlock * (8 + 4 + 4 + 4 + 1 + 4) +
-                            sizeof(BlockScan::storage_type) + (kPhases + 1) * 8 + 64 +
-                            kMaxLdsTypes * kRow * 4 + kMaxOwnWords * 4 + kMaxItemsPerWg +
-                            kBuckets * (2 + 8);
-  if (lds + static_lds > (size_t)max_lds) return hipErrorInvalidValue;
+  // static LDS besides the event list (+ 64 for the one-entry arrays of the large-list
+  // kernels and alignment)
+  const size_t static_lds = kRunBlock * 4 + sizeof(BlockScan::storage_type) +
+                            (kPhases + 1) * 8 + 64 + kMaxLdsTypes * kRow * 4 +
+                            kMaxOwnWords * 4 + kMaxItemsPerWg + 64;
+  const int64_t per_thread = (tpg * geo->range_n + kRunBlock - 1) / kRunBlock;
+  // a list larger than kRunBlock entries after the accumulator where it fits (and the
+  // workgroup has at most kBigMaxi items per thread); else kRunBlock entries in static LDS
+  const size_t list_off = (lds + 15) / 16 * 16;
+  int32_t cap = 0;
+  for (int32_t c = kMaxList; c > kRunBlock && cap == 0 && per_thread <= kBigMaxi;
+       c -= kRunBlock)
+    if (static_lds + list_off + (size_t)list_bytes(c) <= (size_t)max_lds) cap = c;
+  size_t dyn = lds;
+  if (cap > 0) {
+    dyn = list_off + (size_t)list_bytes(cap);
+  } else {
+    cap = kRunBlock;
+    if (static_lds + (size_t)list_bytes(kRunBlock) + lds > (size_t)max_lds)
+      return hipErrorInvalidValue;
+  }
+  a.list_off = (int64_t)list_off;
+  a.list_cap = cap;
   if (ff->n_src > 0 && io->x) {
     const int64_t rows = io->B * io->T;
     hipLaunchKernelGGL(compact_input_kernel, dim3((unsigned)rows), dim3(256), 0,
@@ -361,9 +379,8 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
     hipError_t ce = hipGetLastError();
     if (ce != hipSuccess) return ce;
   }
-  const int64_t per_thread = (tpg * geo->range_n + kRunBlock - 1) / kRunBlock;
   const bool coop = tab->K_rec > 0 && rec->n_src > 0 && geo->R > 1;
-  return dispatch_S<RunLaunch>(tab->S, a, lds, per_thread, (hipStream_t)stream, coop);
+  return dispatch_S<RunLaunch>(tab->S, a, dyn, per_thread, (hipStream_t)stream, coop);
 }
 
 extern "C" int wt_cond_run(const wt_tables* tab, const wt_side* rec, const wt_side* ff,

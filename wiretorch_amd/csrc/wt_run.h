@@ -43,6 +43,8 @@ struct RunArgs {
   uint64_t* timing;     // [wgs][kPhases] wall-clock ticks per phase, or null
   int64_t words;        // bitmap words per workgroup range (range_n / 32)
   int64_t tpg_max;      // trials of the largest group
+  int64_t list_off;     // byte offset of the event list in dynamic LDS (after the accumulator)
+  int32_t list_cap;     // event list capacity: 1024, 2048, 3072 or 4096 entries
 };
 
 // Phases timed by wt_cond_run_timed (thread 0's view): its own update, the wait for the
@@ -56,7 +58,12 @@ constexpr int kTypeCols = 6;  // global table: theta, U_reset, E_L, C_m, beta, n
 constexpr int kRow = 16;
 constexpr int kMaxItemsPerWg = 8 * kRunBlock;        // trials x range per workgroup
 constexpr int kMaxOwnWords = kMaxItemsPerWg / 32;    // the workgroup's own fired bits
-constexpr int kBuckets = 256;  // 64-edge buckets of a scanned event list with a direct entry map
+constexpr int kMaxList = 4 * kRunBlock;  // event list entries at most (four per thread)
+
+// Dynamic LDS of the event list of `cap` entries and its entry map (cap / 4 buckets of 64
+// edges): e0 (8), heads (8 per bucket), count, row, value (4 each), first (2 per bucket),
+// side (1).
+constexpr int64_t list_bytes(int64_t cap) { return cap * 21 + (cap / 4) * 10; }
 
 using BlockScan = rocprim::block_scan<int32_t, kRunBlock,
                                       rocprim::block_scan_algorithm::using_warp_scan>;
@@ -187,8 +194,10 @@ struct EventList {
   uint8_t* side;
   int32_t* n;      // entries appended; past the capacity, events pushed at once by
                    // append_event or left for another round
-  int16_t* first;  // [kBuckets] after the scan: the entry holding edge 64 b
-  uint64_t* heads; // [kBuckets] after the scan: bit f % 64 of word f / 64 where an entry starts
+  int16_t* first;  // [nbk] after the scan: the entry holding edge 64 b
+  uint64_t* heads; // [nbk] after the scan: bit f % 64 of word f / 64 where an entry starts
+  int cap;         // capacity (entries)
+  int nbk;         // buckets of the entry map, cap / 4
 };
 
 __device__ inline void append_event(const EventList& L, double* acc, const int32_t* targets,
@@ -196,7 +205,7 @@ __device__ inline void append_event(const EventList& L, double* acc, const int32
                                     int64_t row, int64_t lo, float value, Fixed fx) {
   if (e1 <= e0) return;
   const int pos = atomicAdd(L.n, 1);
-  if (pos < kRunBlock) {
+  if (pos < L.cap) {
     L.e0[pos] = e0;
     L.count[pos] = (int32_t)(e1 - e0);
     L.row[pos] = (int32_t)(row - lo);
@@ -252,7 +261,7 @@ __device__ inline int wave_reserve(int32_t* counter, uint32_t total) {
 // Every listed synapse, spread evenly over the workgroup (four per thread per round,
 // loads issued before the atomics), added to the accumulator. After the scan L.count
 // holds the exclusive prefix of the entries' edge counts, L.e0 each entry's first edge
-// minus its prefix, and L.first / L.heads the entry map of the first kBuckets buckets.
+// minus its prefix, and L.first / L.heads the entry map of the first L.nbk buckets.
 __device__ inline void run_events(const EventList& L, int m, int32_t total, double* acc,
                                   int64_t lo, Fixed fx) {
   ArgPtr P = kargs();
@@ -276,10 +285,10 @@ __device__ inline void run_events(const EventList& L, int m, int32_t total, doub
       const int32_t f = base + u * stride, b = f >> 6;
       if (b >= nb) {
         a[u] = 0;  // no edge of the wave here
-      } else if (b < kBuckets) {
+      } else if (b < L.nbk) {
         a[u] = L.first[b] + __builtin_popcountll(L.heads[b] & upto & ~1ull);
       } else {
-        int lo2 = L.first[kBuckets - 1], z = m;
+        int lo2 = L.first[L.nbk - 1], z = m;
         while (z - lo2 > 1) {
           const int mid = (lo2 + z) >> 1;
           if (L.count[mid] <= f) lo2 = mid; else z = mid;
@@ -317,7 +326,10 @@ __device__ inline void run_events(const EventList& L, int m, int32_t total, doub
 // The persistent forward. Each thread owns up to MAXI (trial, neuron) items — item
 // threadIdx.x + i * blockDim.x of its workgroup — whose state stays in registers for
 // the whole launch.
-template <int S, int MAXI, bool EXTRA, bool REFR>
+// BIG: the event list lives in dynamic LDS after the accumulator with the capacity the
+// host found room for (more than kRunBlock entries); otherwise kRunBlock entries in static
+// LDS at fixed addresses.
+template <int S, int MAXI, bool EXTRA, bool REFR, bool BIG>
 __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   static_assert(MAXI <= 8, "the overflow note holds one bit per preloaded word");
   extern __shared__ __align__(16) double acc[];  // [K][tpg][range_n]
@@ -325,11 +337,6 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   __shared__ uint32_t s_bits[kMaxOwnWords];  // [tpg][words]: the next step's own spikes
   __shared__ uint32_t s_flag;
   __shared__ uint64_t s_time[kPhases + 1];
-  __shared__ int64_t s_e0[kRunBlock];
-  __shared__ int32_t s_count[kRunBlock];
-  __shared__ int32_t s_row[kRunBlock];
-  __shared__ float s_value[kRunBlock];
-  __shared__ uint8_t s_side[kRunBlock];
   __shared__ int32_t s_nev;
   __shared__ int32_t s_nfired;
   __shared__ uint32_t s_fired[kRunBlock];  // this step's fired sources: j | trial << 24
@@ -359,9 +366,33 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   const bool has_ff = A.ff.n_src > 0;
   const float dt = *A.tab.dt;
   const Fixed fx{ldexpf(1.0f, (int)A.geo.frac_bits), ldexp(1.0, -(int)A.geo.frac_bits)};
-  __shared__ int16_t s_first[kBuckets];
-  __shared__ uint64_t s_heads[kBuckets];
-  const EventList EL{s_e0, s_count, s_row, s_value, s_side, &s_nev, s_first, s_heads};
+  // the event list and its entry map
+  constexpr int kStatic = BIG ? 1 : kRunBlock;
+  __shared__ int64_t s_e0_fixed[kStatic];
+  __shared__ uint64_t s_heads_fixed[kStatic / 4 + 1];
+  __shared__ int32_t s_count_fixed[kStatic], s_row_fixed[kStatic];
+  __shared__ float s_value_fixed[kStatic];
+  __shared__ int16_t s_first_fixed[kStatic / 4 + 1];
+  __shared__ uint8_t s_side_fixed[kStatic];
+  const int cap = BIG ? A.list_cap : kRunBlock, nbk = cap / 4;
+  int64_t* s_e0 = s_e0_fixed;
+  uint64_t* s_heads = s_heads_fixed;
+  int32_t* s_count = s_count_fixed;
+  int32_t* s_row = s_row_fixed;
+  float* s_value = s_value_fixed;
+  int16_t* s_first = s_first_fixed;
+  uint8_t* s_side = s_side_fixed;
+  if constexpr (BIG) {  // after the accumulator (the host sizes both)
+    char* const lp = reinterpret_cast<char*>(acc) + A.list_off;
+    s_e0 = reinterpret_cast<int64_t*>(lp);
+    s_heads = reinterpret_cast<uint64_t*>(lp + (int64_t)cap * 8);
+    s_count = reinterpret_cast<int32_t*>(lp + (int64_t)cap * 8 + nbk * 8);
+    s_row = s_count + cap;
+    s_value = reinterpret_cast<float*>(s_row + cap);
+    s_first = reinterpret_cast<int16_t*>(s_value + cap);
+    s_side = reinterpret_cast<uint8_t*>(s_first + nbk);
+  }
+  const EventList EL{s_e0, s_count, s_row, s_value, s_side, &s_nev, s_first, s_heads, cap, nbk};
   Synapses<S> syn;
   load_synapses<S>(A.tab, syn);
   uint64_t made = 0;  // bit k * S + s: pathway k drives synapse type s
@@ -735,7 +766,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     }
     tick(s_time, 4);
     // (2) The listed sources and inputs (their lookups issued before the update), then
-    // the fired sources the list could not hold (rest), in rounds of at most kRunBlock
+    // the fired sources the list could not hold (rest), in rounds of at most cap
     // events: each round appends what fits, scans and pushes it. A round that could not
     // take every event leaves the list's count past its capacity — read by every thread
     // after the round's barrier — and the events not taken for the next round. (Sparse
@@ -768,14 +799,14 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
           const uint32_t below = wave_prefix<2>((uint32_t)rec_pending + in_pending, total);
           int pos = wave_reserve(EL.n, total) + (int)below;
           if (rec_pending) {
-            if (pos < kRunBlock) {
+            if (pos < cap) {
               put_event(EL, pos, 0, re0, re1, rk * acc_stride + (int64_t)(rj >> 24) * range_n,
                         lo, 1.0f);
               rec_pending = false;
             }
             ++pos;
           }
-          if (in_pending && pos < kRunBlock) {
+          if (in_pending && pos < cap) {
             put_event(EL, pos, 1, ie0, ie1,
                       (P->tab.K_rec * tpg + (int64_t)(threadIdx.x / kInCap)) * range_n +
                           ik * acc_stride,
@@ -788,7 +819,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
         // (a list already full takes nothing more this round: its count, which only
         // grows, then calls for another)
         while (__ballot(rest_any(rest_bits)) != 0 &&
-               __builtin_amdgcn_readfirstlane(*EL.n) < kRunBlock) {
+               __builtin_amdgcn_readfirstlane(*EL.n) < cap) {
           constexpr int kTake = 4;
           uint32_t src[kTake], trial[kTake];
           bool has[kTake];
@@ -841,7 +872,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
           for (int c = 0; c < kTake; ++c) {
             if (!has[c] || stop) continue;
             if (kk[c] >= 0 && f1[c] > f0[c]) {
-              if (pos >= kRunBlock) {
+              if (pos >= cap) {
                 stop = true;
                 continue;
               }
@@ -862,33 +893,43 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
               done = true;
             }
           }
-          if (base + (int)total >= kRunBlock) break;  // uniform: the list is full
+          if (base + (int)total >= cap) break;  // uniform: the list is full
         }
         // the entry map is cleared for this round's scan (its last reader, the previous
         // round's push, is behind a barrier; its next writer after the one below)
-        for (int w = threadIdx.x; w < kBuckets; w += blockDim.x) s_heads[w] = 0;
+        for (int w = threadIdx.x; w < nbk; w += blockDim.x) s_heads[w] = 0;
         __syncthreads();
         tick(s_time, 6);
         const int n_ev = s_nev;
-        const int m = n_ev < kRunBlock ? n_ev : kRunBlock;
+        const int m = n_ev < cap ? n_ev : cap;
         if (m > 0) {  // m is uniform: every thread takes part in the scan
           const int tid = threadIdx.x;
-          int32_t c = tid < m ? s_count[tid] : 0, total;
-          const int32_t cnt = c;
-          BlockScan().exclusive_scan(c, c, 0, total, s_scan);
-          if (tid < m) {  // entry tid holds edges [c, c + cnt) of the round, cnt > 0
-            s_count[tid] = c;
-            s_e0[tid] -= c;
-            for (int32_t b = (c + 63) >> 6; b < kBuckets && (b << 6) < c + cnt; ++b)
-              s_first[b] = (int16_t)tid;
-            if (c < kBuckets * 64)
+          // thread tid scans entries tid * per .. + per - 1 (per = cap / kRunBlock)
+          const int per = cap / kRunBlock, a0 = tid * per;
+          int32_t cnt[kMaxList / kRunBlock], sum = 0, c, total;
+#pragma unroll
+          for (int j = 0; j < kMaxList / kRunBlock; ++j) {
+            cnt[j] = (j < per && a0 + j < m) ? s_count[a0 + j] : 0;
+            sum += cnt[j];
+          }
+          BlockScan().exclusive_scan(sum, c, 0, total, s_scan);
+#pragma unroll
+          for (int j = 0; j < kMaxList / kRunBlock; ++j) {
+            if (j >= per || a0 + j >= m) continue;
+            const int a = a0 + j;  // entry a holds edges [c, c + cnt) of the round, cnt > 0
+            s_count[a] = c;
+            s_e0[a] -= c;
+            for (int32_t b = (c + 63) >> 6; b < nbk && (b << 6) < c + cnt[j]; ++b)
+              s_first[b] = (int16_t)a;
+            if (c < nbk * 64)
               atomicOr((unsigned long long*)&s_heads[c >> 6], 1ull << (c & 63));
+            c += cnt[j];
           }
           __syncthreads();
           run_events(EL, m, total, acc, lo, fx);
         }
-        if (n_ev < kRunBlock) break;  // uniform: every event of the step was taken
-        // (a full list may leave events: n_ev == kRunBlock takes one more, possibly empty,
+        if (n_ev < cap) break;  // uniform: every event of the step was taken
+        // (a full list may leave events: n_ev == cap takes one more, possibly empty,
         // round)
         __syncthreads();  // the list is consumed
         if (threadIdx.x == 0) s_nev = 0;
@@ -953,27 +994,40 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   if (A.timing && threadIdx.x < kPhases) A.timing[wg * kPhases + threadIdx.x] = s_time[threadIdx.x];
 }
 
-template <int S, int MAXI, bool EXTRA, bool REFR>
+template <int S, int MAXI, bool EXTRA, bool REFR, bool BIG>
 inline hipError_t launch_one(RunArgs& a, size_t lds, hipStream_t stream, bool coop) {
-  const void* fn = reinterpret_cast<const void*>(&cond_run_kernel<S, MAXI, EXTRA, REFR>);
+  const void* fn = reinterpret_cast<const void*>(&cond_run_kernel<S, MAXI, EXTRA, REFR, BIG>);
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   dim3 grid((unsigned)(a.geo.groups * a.geo.R)), blk((unsigned)kRunBlock);
   void* params[] = {&a};
   if (coop) return hipLaunchCooperativeKernel(fn, grid, blk, params, (unsigned)lds, stream);
-  hipLaunchKernelGGL((cond_run_kernel<S, MAXI, EXTRA, REFR>), grid, blk, lds, stream, a);
+  hipLaunchKernelGGL((cond_run_kernel<S, MAXI, EXTRA, REFR, BIG>), grid, blk, lds, stream, a);
   return hipGetLastError();
 }
 
-template <int S, int MAXI>
-inline hipError_t launch_run(RunArgs& a, size_t lds, hipStream_t stream, bool coop) {
+template <int S, int MAXI, bool BIG>
+inline hipError_t launch_flags(RunArgs& a, size_t lds, hipStream_t stream, bool coop) {
   const bool extra = a.io.prob || a.io.v_saved || a.io.A_saved || a.io.track_v || a.io.track_g;
   const bool refr = a.tab.n_ref != nullptr;
   if (extra)
-    return refr ? launch_one<S, MAXI, true, true>(a, lds, stream, coop)
-                : launch_one<S, MAXI, true, false>(a, lds, stream, coop);
-  return refr ? launch_one<S, MAXI, false, true>(a, lds, stream, coop)
-              : launch_one<S, MAXI, false, false>(a, lds, stream, coop);
+    return refr ? launch_one<S, MAXI, true, true, BIG>(a, lds, stream, coop)
+                : launch_one<S, MAXI, true, false, BIG>(a, lds, stream, coop);
+  return refr ? launch_one<S, MAXI, false, true, BIG>(a, lds, stream, coop)
+              : launch_one<S, MAXI, false, false, BIG>(a, lds, stream, coop);
+}
+
+// The large-list kernels exist for up to kBigMaxi items per thread (workgroups whose
+// accumulator leaves room for the list); the host asks for them only there.
+constexpr int kBigMaxi = 4;
+
+template <int S, int MAXI>
+inline hipError_t launch_run(RunArgs& a, size_t lds, hipStream_t stream, bool coop) {
+  if (a.list_cap > kRunBlock) {
+    if constexpr (MAXI <= kBigMaxi) return launch_flags<S, MAXI, true>(a, lds, stream, coop);
+    return hipErrorInvalidValue;
+  }
+  return launch_flags<S, MAXI, false>(a, lds, stream, coop);
 }
 
 template <int S>
