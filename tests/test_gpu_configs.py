@@ -4,9 +4,11 @@
 * Configuration 1 (forward, dt 0.1 ms): spike raster identical to the oracle's over the
   first 200 steps, voltages within 1e-5 relative — the bar of configuration 0.
 * Dense firing (a strongly driven configuration-3 network at 70 Hz, 16 trials, two per
-  workgroup): most steps list more fired sources per workgroup than its event list
-  holds (1,024), some more than twice that, so they are pushed in two or three rounds;
-  forward and training step to the bars of configurations 1 and 3.
+  workgroup): most steps list more than 1,024 fired sources per workgroup, some more than
+  2,048. With the event list as large as fits (4,096 entries here) each step is pushed in
+  one round; with the list limited to 1,024 entries (``engine.MAX_LIST``, the static list
+  of the kernels for larger workgroups) in two or three. Forward and training step to the
+  bars of configurations 1 and 3, both ways.
 * Configuration 3 (training step: per-synapse learnt weights, learnt per-type tau_mem and
   theta, fast-sigmoid surrogate of slope 10, squared error of 20 ms-binned rates against
   gamma(2, 5 Hz) targets, dt 1 ms): over 100 steps, the same raster, the loss within 1e-5
@@ -92,7 +94,15 @@ def _fired_per_workgroup_step(spikes):
     return spikes.reshape(-1, groups, T, N).sum(axis=(0, 3))
 
 
-def test_dense_firing_forward_matches_oracle():
+@pytest.fixture(params=[0, 1024], ids=["list-as-fits", "list-1024"])
+def max_list(request):
+    saved = engine.MAX_LIST
+    engine.MAX_LIST = request.param
+    yield request.param
+    engine.MAX_LIST = saved
+
+
+def test_dense_firing_forward_matches_oracle(max_list):
     wl = _dense_workload()
     x = torch.from_numpy(wl.x).float()
     s_ref, v_ref = _forward(wl.model, x, oracle_engine)
@@ -105,7 +115,7 @@ def test_dense_firing_forward_matches_oracle():
     np.testing.assert_allclose(v_gpu, v_ref, rtol=1e-5, atol=1e-5 * 65)
 
 
-def test_dense_firing_training_step_matches_oracle():
+def test_dense_firing_training_step_matches_oracle(max_list):
     wl = _dense_workload()
     x = torch.from_numpy(wl.x).float()
     target = torch.from_numpy(synthetic.gamma_targets(5, wl.N, 2))

@@ -32,7 +32,8 @@ class Side(ctypes.Structure):
 
 
 class Geometry(ctypes.Structure):
-    _fields_ = [("groups", I64), ("R", I64), ("range_n", I64), ("frac_bits", I64)]
+    _fields_ = [("groups", I64), ("R", I64), ("range_n", I64), ("frac_bits", I64),
+                ("max_list", I64)]
 
 
 class RunIO(ctypes.Structure):

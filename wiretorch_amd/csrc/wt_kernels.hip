@@ -302,7 +302,8 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
     return hipErrorInvalidValue;
   if (geo->groups < 1 || geo->groups > kMaxGroups || geo->R < 1 || geo->R > 256 ||
       geo->range_n < 32 || geo->range_n % 32 != 0 || geo->R * geo->range_n < tab->N ||
-      geo->frac_bits < 0 || geo->frac_bits > 60)
+      geo->frac_bits < 0 || geo->frac_bits > 60 || geo->max_list < 0 ||
+      geo->max_list > kMaxList || geo->max_list % kRunBlock != 0)
     return hipErrorInvalidValue;
   const int64_t tpg = run_tpg_max(geo, io->B);
   if (io->B < 1 || io->T < 0) return hipErrorInvalidValue;
@@ -361,7 +362,9 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
   int32_t cap = 0;
   for (int32_t c = kMaxList; c > kRunBlock && cap == 0 && per_thread <= kBigMaxi;
        c -= kRunBlock)
-    if (static_lds + list_off + (size_t)list_bytes(c) <= (size_t)max_lds) cap = c;
+    if ((geo->max_list == 0 || c <= geo->max_list) &&
+        static_lds + list_off + (size_t)list_bytes(c) <= (size_t)max_lds)
+      cap = c;
   size_t dyn = lds;
   if (cap > 0) {
     dyn = list_off + (size_t)list_bytes(cap);

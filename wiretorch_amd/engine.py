@@ -74,6 +74,9 @@ class _timed:
 PHASE_TIMING: list | None = None
 #: Phase slots per workgroup that ``wt_cond_run_timed`` writes.
 PHASES = 8
+#: Limit on the forward's per-workgroup event list (entries, a multiple of 1024; 0 = the
+#: largest that fits). Results do not depend on it; tests lower it to exercise the rounds.
+MAX_LIST = 0
 
 
 # =====================================================================
@@ -429,7 +432,7 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
 def _launch(L: _Plan, x, scale, v, g, counter, spikes, prob, saved, tracked,
             rec_weights=None, ff_weights=None) -> None:
     groups, R, range_n = L.geo
-    geo = _lib.Geometry(groups, R, range_n, L.frac_bits)
+    geo = _lib.Geometry(groups, R, range_n, L.frac_bits, MAX_LIST)
     lib = _lib.load()
     scratch = torch.empty(int(lib.wt_cond_run_scratch_bytes(geo, L.B, L.T)),
                           dtype=torch.uint8, device=L.device)
