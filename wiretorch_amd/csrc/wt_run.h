@@ -623,17 +623,38 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
             gr[i][s] = gr[i][s] * syn.decay_r[s];
             gd[i][s] = gd[i][s] * syn.decay_d[s];
           }
-          double* cell = acc + __umul24(q, (uint32_t)range_n) + ln;
-          for (int64_t k = 0; k < K; ++k, cell += acc_stride) {
-            const float a = (float)*cell;
-            if (valid) *cell = 0.0;
-            if (EXTRA && valid && A.io.A_saved) A.io.A_saved[((k * B + b) * T + (t - 1)) * N + n] = a;
-            const float sc = row[8 + k];
+          // the item's pathways four at a time: their accumulators and scales read
+          // together, then cleared, then added in pathway order
+          double* const cell = acc + __umul24(q, (uint32_t)range_n) + ln;
+          for (int32_t k0 = 0; k0 < K; k0 += 4) {
+            double ad[4];
+            float sc[4];
 #pragma unroll
-            for (int s = 0; s < S; ++s) {
-              if ((made >> (k * S + s)) & 1u) {
-                gr[i][s] = gr[i][s] + a * (syn.jump_r[s] * sc);
-                gd[i][s] = gd[i][s] + a * (syn.jump_d[s] * sc);
+            for (int j = 0; j < 4; ++j) {
+              ad[j] = 0.0;
+              sc[j] = 0.0f;
+              if (k0 + j < K) {
+                ad[j] = cell[(uint32_t)(k0 + j) * acc_stride];
+                sc[j] = row[8 + k0 + j];
+              }
+            }
+            if (valid) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                if (k0 + j < K) cell[(uint32_t)(k0 + j) * acc_stride] = 0.0;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              if (k0 + j >= K) continue;
+              const int64_t k = k0 + j;
+              const float a = (float)ad[j];
+              if (EXTRA && valid && A.io.A_saved) A.io.A_saved[((k * B + b) * T + (t - 1)) * N + n] = a;
+#pragma unroll
+              for (int s = 0; s < S; ++s) {
+                if ((made >> (k * S + s)) & 1u) {
+                  gr[i][s] = gr[i][s] + a * (syn.jump_r[s] * sc[j]);
+                  gd[i][s] = gd[i][s] + a * (syn.jump_d[s] * sc[j]);
+                }
               }
             }
           }
