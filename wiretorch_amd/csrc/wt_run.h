@@ -501,6 +501,15 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     barrier_arrive(my_barrier);
     ++phase;
   }
+  // Every step starts with its own spike bits clear and both lists empty: cleared here
+  // for step 0, and after the publication (their last reader) for each next step.
+  __syncthreads();
+  for (int64_t w = threadIdx.x; w < tpg * words; w += blockDim.x) s_bits[w] = 0;
+  if (threadIdx.x == 0) {
+    s_nev = 0;
+    s_nfired = 0;
+  }
+  __syncthreads();
 
   for (int32_t t = 0, buf = 0; t < T; ++t, buf = buf == 2 ? 0 : buf + 1) {
     const bool more = t + 1 < T;
@@ -528,12 +537,6 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       in_j = gload(P->in_idx + slot);
       in_v = gload(P->in_val + slot);
     }
-    for (int64_t w = threadIdx.x; w < tpg * words; w += blockDim.x) s_bits[w] = 0;
-    if (threadIdx.x == 0) {
-      s_nev = 0;
-      s_nfired = 0;
-    }
-    __syncthreads();
     tick(s_time, 0);
 
     // ---------------- events of step t, listed before the update ----------------
@@ -786,6 +789,9 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       __syncthreads();
     }
     tick(s_time, 4);
+    // the next step's own bits and fired list start empty (their readers are done)
+    for (int64_t w = threadIdx.x; w < tpg * words; w += blockDim.x) s_bits[w] = 0;
+    if (threadIdx.x == 0) s_nfired = 0;
     // (2) The listed sources and inputs (their lookups issued before the update), then
     // the fired sources the list could not hold (rest), in rounds of at most cap
     // events: each round appends what fits, scans and pushes it. A round that could not
@@ -958,6 +964,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       }
     }
     __syncthreads();  // the accumulator is complete for the next update
+    if (threadIdx.x == 0) s_nev = 0;  // every thread has read it; its next use is behind barriers
     tick(s_time, 7);
   }
 
