@@ -9,6 +9,9 @@
   one round; with the list limited to 1,024 entries (``engine.MAX_LIST``, the static list
   of the kernels for larger workgroups) in two or three. Forward and training step to the
   bars of configurations 1 and 3, both ways.
+* Two training steps of configuration 3's network with the learnt weights changed in
+  between: the second takes the new weights through the cached layout of the dense
+  pathways (no new compression), to the same bar.
 * Configuration 3 (training step: per-synapse learnt weights, learnt per-type tau_mem and
   theta, fast-sigmoid surrogate of slope 10, squared error of 20 ms-binned rates against
   gamma(2, 5 Hz) targets, dt 1 ms): over 100 steps, the same raster, the loss within 1e-5
@@ -129,4 +132,28 @@ def test_dense_firing_training_step_matches_oracle(max_list):
     for key, value in g_ref.items():
         scale = np.abs(value).max()
         assert scale > 0, key
+        np.testing.assert_allclose(g_gpu[key], value, rtol=0, atol=1e-4 * scale, err_msg=key)
+
+
+def test_learnt_weights_update_reuses_layout(monkeypatch):
+    wl = synthetic.config3(B=2, T=60)
+    x = torch.from_numpy(wl.x).float()
+    target = torch.from_numpy(synthetic.gamma_targets(3, wl.N, 3))
+    _training_step(wl, x, target, engine, DEV)
+    built = []
+    original = engine._from_pathways
+    monkeypatch.setattr(engine, "_from_pathways",
+                        lambda *a, **k: built.append(1) or original(*a, **k))
+    with torch.no_grad():  # new values, same nonzero pattern
+        for name, p in wl.model.named_parameters():
+            if name.endswith("log_weights"):
+                p.mul_(1.05)
+    s_gpu, l_gpu, g_gpu = _training_step(wl, x, target, engine, DEV)
+    assert not built, "the dense pathways were compressed again"
+    s_ref, l_ref, g_ref = _training_step(wl, x, target, oracle_engine, "cpu")
+    differs = (s_gpu != s_ref).any(axis=(0, 2))
+    assert not differs.any(), f"rasters differ from step {int(np.argmax(differs))}"
+    np.testing.assert_allclose(l_gpu, l_ref, rtol=1e-5)
+    for key, value in g_ref.items():
+        scale = np.abs(value).max()
         np.testing.assert_allclose(g_gpu[key], value, rtol=0, atol=1e-4 * scale, err_msg=key)

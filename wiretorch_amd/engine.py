@@ -94,9 +94,25 @@ class _Side:
     row_local: torch.Tensor | None = None
     dense_shapes: tuple = ()
     max_in_sum: float = 0.0
+    #: For a side built from dense pathways: per pathway, its edges (positions in edge
+    #: order) and their flat indices into the pathway's (rows, N) weight matrix.
+    dense_edges: tuple = ()
     _split: dict = field(default_factory=dict)
     _edge_src: torch.Tensor | None = None
     _by_target: dict = field(default_factory=dict)
+
+    def with_weights(self, weights: torch.Tensor, max_in_sum: float) -> "_Side":
+        """The same structure with other edge weights; what is derived from the
+        structure alone (range splits, edge sources, the by-target order) is shared."""
+        c = self.conn
+        conn = Connectome(c.n_sources, c.n_targets, c.indptr, c.targets, weights, c.pathway,
+                          c.n_pathways)
+        side = _Side(conn, self.pathway32, row_local=self.row_local,
+                     dense_shapes=self.dense_shapes, max_in_sum=max_in_sum,
+                     dense_edges=self.dense_edges, _split=self._split,
+                     _by_target=self._by_target)
+        side._edge_src = self.edge_src(torch.cuda.current_stream(c.device).cuda_stream)
+        return side
 
     @property
     def n_src(self) -> int:
@@ -210,12 +226,34 @@ def _from_pathways(pathways, n_src: int, N: int, device) -> _Side:
     conn = from_dense(W_all, pathway, len(pathways))
     side = _Side(conn, pathway.to(torch.int32), row_local=row_local,
                  dense_shapes=tuple(shapes))
-    side.max_in_sum = _max_in_sum(conn)
+    side.max_in_sum = _dense_in_sum(pathways)
+    if conn.n_edges:
+        edge_src = side.edge_src(torch.cuda.current_stream(device).cuda_stream)
+        k_of_edge = conn.pathway[edge_src]
+        edges = []
+        for k in range(len(pathways)):
+            e = torch.nonzero(k_of_edge == k).flatten()
+            edges.append((e, row_local[edge_src[e]] * N + conn.targets[e].long()))
+        side.dense_edges = tuple(edges)
     return side
+
+
+def _dense_in_sum(pathways) -> float:
+    """The largest per-target sum of |weight| over the dense pathways (float64 sums)."""
+    total = None
+    for _, W in pathways:
+        col = torch.sum(W.detach().float().abs(), dim=0, dtype=torch.float64)
+        total = col if total is None else total + col
+    return float(total.max()) if total is not None and total.numel() else 0.0
 
 
 _CACHE: OrderedDict = OrderedDict()
 _CACHE_SIZE = 32
+#: Sides of dense pathways by structure (source rows and shapes), with the nonzero
+#: pattern of each pathway they were built from: a side whose weights changed but whose
+#: pattern did not (learnt weights) takes the new values without being compressed again.
+_LAYOUTS: OrderedDict = OrderedDict()
+_LAYOUTS_SIZE = 4
 
 
 def _side_of(pathways, sparse, n_src: int, N: int, device) -> _Side:
@@ -235,10 +273,34 @@ def _side_of(pathways, sparse, n_src: int, N: int, device) -> _Side:
         _CACHE.move_to_end(key)
         return hit[0]
     side = (_from_connectome(sparse, device) if sparse is not None
-            else _from_pathways(pathways, n_src, N, device))
+            else _dense_side(pathways, n_src, N, device))
     _CACHE[key] = (side, keep)  # holding the tensors keeps their addresses unique
     while len(_CACHE) > _CACHE_SIZE:
         _CACHE.popitem(last=False)
+    return side
+
+
+def _dense_side(pathways, n_src: int, N: int, device) -> _Side:
+    """The side of dense pathways: from the layout of the same structure and nonzero
+    pattern if one is cached (the edge weights gathered from the matrices), else
+    compressed anew."""
+    key = ("layout", n_src, N) + tuple(
+        (rows.data_ptr(), rows._version, tuple(rows.shape), tuple(W.shape))
+        for rows, W in pathways)
+    hit = _LAYOUTS.get(key)
+    if hit is not None:
+        base, masks, _keep = hit
+        if all(torch.equal(W.detach() != 0, m) for (_, W), m in zip(pathways, masks)):
+            _LAYOUTS.move_to_end(key)
+            weights = torch.empty_like(base.conn.weights)
+            for (_, W), (e, flat) in zip(pathways, base.dense_edges):
+                weights[e] = W.detach().to(device, torch.float32).reshape(-1)[flat]
+            return base.with_weights(weights, _dense_in_sum(pathways))
+    side = _from_pathways(pathways, n_src, N, device)
+    masks = tuple((W.detach() != 0).to(device) for _, W in pathways)
+    _LAYOUTS[key] = (side, masks, tuple(rows for rows, _ in pathways))
+    while len(_LAYOUTS) > _LAYOUTS_SIZE:
+        _LAYOUTS.popitem(last=False)
     return side
 
 
@@ -616,15 +678,14 @@ def _weight_grads(L: _Plan, side: _Side, activity, grad_A, k0, weights, needs):
     if side.row_local is None:  # compressed side: the gradient of its weights
         return [grad_e if needs[0] else None]
     out = []
-    k_of_edge = c.pathway[edge_src]
-    row_of_edge = side.row_local[edge_src]
     for k, (shape, need) in enumerate(zip(side.dense_shapes, needs)):
         if not need:
             out.append(None)
             continue
-        sel = k_of_edge == k
         G = torch.zeros(shape, device=L.device)
-        G[row_of_edge[sel], c.targets[sel].long()] = grad_e[sel]
+        if side.dense_edges:
+            e, flat = side.dense_edges[k]
+            G.view(-1)[flat] = grad_e[e]
         out.append(G)
     return out
 
