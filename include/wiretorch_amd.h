@@ -273,6 +273,19 @@ int wt_rate_backward(const wt_rate_tables* tab, const wt_rate_operand* op,
 int wt_edge_sources(const int64_t* indptr, int64_t n_src, int64_t* edge_src,
                     wt_stream_t stream);
 
+/* wt_events_count / wt_events_fill — per source, the nonzero entries of an activity
+ * (BT, n) f32 (spikes, or inputs), in ascending row (trial*T + step) order: the event
+ * lists the weight gradients take. Replaces the torch nonzero / argsort / bincount that
+ * form them around the reference's weight_gradient (network_simulators/engine.py:327-350).
+ * count writes indptr (n+1) int64 (indptr[n] = number of events) and fills scratch
+ * (wt_events_scratch_bytes); fill, with the same scratch, writes bt (indptr[n]) int64 and
+ * value (indptr[n]) f32. Deterministic. BT may have at most 65535 * 256 rows. */
+int64_t wt_events_scratch_bytes(int64_t BT, int64_t n);
+int wt_events_count(const float* activity, int64_t BT, int64_t n, void* scratch,
+                    int64_t* indptr, wt_stream_t stream);
+int wt_events_fill(const float* activity, int64_t BT, int64_t n, const void* scratch,
+                   const int64_t* indptr, int64_t* bt, float* value, wt_stream_t stream);
+
 /* wt_weight_gradient — dL/dW on the connectome's support (its edges), event-driven:
  * grad_w[e] = sum over the events i of src(e) of ev_val[i] * grad_A[k, ev_bt[i], tgt(e)]
  * with k = pathway_offset + pathway(src(e)). Events of source j are ev_indptr[j] ..

@@ -212,6 +212,81 @@ __global__ void edge_source_kernel(const int64_t* indptr, int64_t n_src, int64_t
   for (int64_t e = indptr[j]; e < indptr[j + 1]; ++e) edge_src[e] = j;
 }
 
+// ---- Events by source: the nonzero entries of a (BT, n) activity, per column j in
+// ascending row order. Rows are taken in chunks of kEvChunk; thread (chunk c, column j)
+// counts, then writes, its chunk's entries of column j (a wave reads 64 consecutive
+// columns of one row at a time).
+constexpr int64_t kEvChunk = 256;
+constexpr int kEvBlock = 256;
+
+__global__ void events_count_kernel(const float* __restrict__ act, int64_t BT, int64_t n,
+                                    int32_t* __restrict__ chunk) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  const int64_t r0 = (int64_t)blockIdx.y * kEvChunk;
+  const int64_t r1 = r0 + kEvChunk < BT ? r0 + kEvChunk : BT;
+  int32_t count = 0;
+#pragma unroll 8
+  for (int64_t r = r0; r < r1; ++r) count += act[r * n + j] != 0.0f ? 1 : 0;
+  chunk[blockIdx.y * n + j] = count;
+}
+
+// Per column: each chunk's count becomes its offset within the column; the column's
+// total goes to totals[j].
+__global__ void events_column_kernel(int32_t* __restrict__ chunk, int64_t n_chunks, int64_t n,
+                                     int64_t* __restrict__ totals) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  int32_t sum = 0;
+  for (int64_t c = 0; c < n_chunks; ++c) {
+    const int32_t v = chunk[c * n + j];
+    chunk[c * n + j] = sum;
+    sum += v;
+  }
+  totals[j] = sum;
+}
+
+// indptr[0] = 0, indptr[j + 1] = totals[0] + ... + totals[j]; one workgroup, each thread
+// a contiguous segment. totals may alias indptr + 1.
+__global__ __launch_bounds__(kRunBlock) void events_indptr_kernel(const int64_t* totals,
+                                                                 int64_t n, int64_t* indptr) {
+  using Scan64 = rocprim::block_scan<int64_t, kRunBlock>;
+  __shared__ typename Scan64::storage_type storage;
+  const int64_t per = (n + kRunBlock - 1) / kRunBlock;
+  const int64_t j0 = threadIdx.x * per, j1 = j0 + per < n ? j0 + per : n;
+  int64_t local = 0;
+  for (int64_t j = j0; j < j1; ++j) local += totals[j];
+  int64_t before = 0, all = 0;
+  Scan64().exclusive_scan(local, before, (int64_t)0, all, storage);
+  __syncthreads();  // every total is read before any is overwritten (aliasing)
+  int64_t run = before;
+  for (int64_t j = j0; j < j1; ++j) {  // totals[j] is read before indptr[j + 1] (its
+    const int64_t v = totals[j];         // alias) is written, by this thread alone
+    indptr[j + 1] = run + v;
+    run += v;
+  }
+  if (threadIdx.x == 0) indptr[0] = 0;
+}
+
+__global__ void events_fill_kernel(const float* __restrict__ act, int64_t BT, int64_t n,
+                                   const int32_t* __restrict__ chunk,
+                                   const int64_t* __restrict__ indptr, int64_t* __restrict__ bt,
+                                   float* __restrict__ value) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  const int64_t r0 = (int64_t)blockIdx.y * kEvChunk;
+  const int64_t r1 = r0 + kEvChunk < BT ? r0 + kEvChunk : BT;
+  int64_t pos = indptr[j] + chunk[blockIdx.y * n + j];
+  for (int64_t r = r0; r < r1; ++r) {
+    const float a = act[r * n + j];
+    if (a != 0.0f) {
+      bt[pos] = r;
+      value[pos] = a;
+      ++pos;
+    }
+  }
+}
+
 }  // namespace wt
 
 // ===================================================================================
@@ -467,6 +542,51 @@ extern "C" int wt_edge_sources(const int64_t* indptr, int64_t n_src, int64_t* ed
   const int block = 256;
   hipLaunchKernelGGL(edge_source_kernel, dim3((unsigned)((n_src + block - 1) / block)),
                      dim3(block), 0, (hipStream_t)stream, indptr, n_src, edge_src);
+  return hipGetLastError();
+}
+
+extern "C" int64_t wt_events_scratch_bytes(int64_t BT, int64_t n) {
+  if (BT < 0 || n < 0) return 0;
+  return ((BT + kEvChunk - 1) / kEvChunk) * n * 4;
+}
+
+extern "C" int wt_events_count(const float* activity, int64_t BT, int64_t n, void* scratch,
+                               int64_t* indptr, wt_stream_t stream) {
+  if (!indptr || BT < 0 || n < 0) return hipErrorInvalidValue;
+  const int64_t n_chunks = (BT + kEvChunk - 1) / kEvChunk;
+  if (n_chunks > 65535) return hipErrorInvalidValue;
+  if (n > 0 && BT > 0 && (!activity || !scratch)) return hipErrorInvalidValue;
+  int32_t* chunk = static_cast<int32_t*>(scratch);
+  const dim3 cols((unsigned)((n + kEvBlock - 1) / kEvBlock));
+  if (n > 0 && BT > 0) {
+    hipLaunchKernelGGL(events_count_kernel, dim3(cols.x, (unsigned)n_chunks), dim3(kEvBlock), 0,
+                       (hipStream_t)stream, activity, BT, n, chunk);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (n > 0) {  // column totals into indptr[1 .. n], then scanned in place
+    hipLaunchKernelGGL(events_column_kernel, cols, dim3(kEvBlock), 0, (hipStream_t)stream,
+                       chunk, n_chunks, n, indptr + 1);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(events_indptr_kernel, dim3(1), dim3(kRunBlock), 0, (hipStream_t)stream,
+                     indptr + 1, n, indptr);
+  return hipGetLastError();
+}
+
+extern "C" int wt_events_fill(const float* activity, int64_t BT, int64_t n, const void* scratch,
+                              const int64_t* indptr, int64_t* bt, float* value,
+                              wt_stream_t stream) {
+  if (BT < 0 || n < 0) return hipErrorInvalidValue;
+  if (BT == 0 || n == 0) return hipSuccess;
+  if (!activity || !scratch || !indptr || !bt || !value) return hipErrorInvalidValue;
+  const int64_t n_chunks = (BT + kEvChunk - 1) / kEvChunk;
+  if (n_chunks > 65535) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(events_fill_kernel,
+                     dim3((unsigned)((n + kEvBlock - 1) / kEvBlock), (unsigned)n_chunks),
+                     dim3(kEvBlock), 0, (hipStream_t)stream, activity, BT, n,
+                     static_cast<const int32_t*>(scratch), indptr, bt, value);
   return hipGetLastError();
 }
 

@@ -640,26 +640,35 @@ def _sparse_weights(L: _Plan, weights, n_rec_w):
     return rec, ff
 
 
-def _events(activity: torch.Tensor):
+def _events(activity: torch.Tensor, stream):
     """Per source, its (trial*T + step) events ascending and their values:
-    ``(indptr, bt, value)`` from ``activity`` ``(B, T, n_src)``."""
+    ``(indptr, bt, value)`` from ``activity`` ``(B, T, n_src)`` (``wt_events_count`` /
+    ``wt_events_fill``; the host reads the number of events to size the lists)."""
     B, T, n = activity.shape
-    flat = activity.reshape(B * T, n)
-    bt, j = torch.nonzero(flat, as_tuple=True)
-    key = j * (B * T) + bt
-    order = torch.argsort(key)
-    j, bt = j[order], bt[order]
-    value = flat[bt, j].contiguous()
-    indptr = torch.zeros(n + 1, dtype=torch.int64, device=activity.device)
-    indptr[1:] = torch.cumsum(torch.bincount(j, minlength=n), 0)
-    return indptr, bt.contiguous(), value
+    BT = B * T
+    flat = activity.reshape(BT, n).float().contiguous()
+    dev = activity.device
+    lib = _lib.load()
+    scratch = torch.empty(max(int(lib.wt_events_scratch_bytes(BT, n)), 1), dtype=torch.uint8,
+                          device=dev)
+    indptr = torch.empty(n + 1, dtype=torch.int64, device=dev)
+    _lib.check(lib.wt_events_count(flat.data_ptr(), BT, n, scratch.data_ptr(),
+                                   indptr.data_ptr(), stream), "wt_events_count")
+    total = int(indptr[-1])
+    bt = torch.empty(total, dtype=torch.int64, device=dev)
+    value = torch.empty(total, dtype=torch.float32, device=dev)
+    if total:
+        _lib.check(lib.wt_events_fill(flat.data_ptr(), BT, n, scratch.data_ptr(),
+                                      indptr.data_ptr(), bt.data_ptr(), value.data_ptr(),
+                                      stream), "wt_events_fill")
+    return indptr, bt, value
 
 
 def _weight_grads(L: _Plan, side: _Side, activity, grad_A, k0, weights, needs):
     """Gradients of a side's weight tensors from the event-driven support gradient:
     ``wt_weight_gradient_by_target`` over dL/da transposed to (pathway, target) rows."""
     c = side.conn
-    indptr, bt, value = _events(activity)
+    indptr, bt, value = _events(activity, L.stream)
     grad_e = torch.zeros(c.n_edges, device=L.device)
     edge_src = side.edge_src(L.stream)
     n_path = int(c.n_pathways)
