@@ -43,6 +43,29 @@ __device__ inline float nonlin(int code, float x) {
     default: return tanhf(x);                                  // tanh
   }
 }
+// The same for M values of one neuron (one code): the switch is taken once, so that the
+// M evaluations are independent and interleave.
+template <int M>
+__device__ inline void nonlin_n(int code, float gain, const float (&x)[M], float (&r)[M]) {
+  switch (code) {
+    case 0:
+#pragma unroll
+      for (int v = 0; v < M; ++v) r[v] = gain * (x[v] > 0.0f ? x[v] : 0.0f);
+      break;
+    case 1:
+#pragma unroll
+      for (int v = 0; v < M; ++v) r[v] = gain * (x[v] > 20.0f ? x[v] : log1pf(expf(x[v])));
+      break;
+    case 2:
+#pragma unroll
+      for (int v = 0; v < M; ++v) r[v] = gain * (1.0f / (1.0f + expf(-x[v])));
+      break;
+    default:
+#pragma unroll
+      for (int v = 0; v < M; ++v) r[v] = gain * tanhf(x[v]);
+      break;
+  }
+}
 __device__ inline float nonlin_grad(int code, float x) {
   switch (code) {
     case 0: return x > 0.0f ? 1.0f : 0.0f;
@@ -365,28 +388,64 @@ __global__ __launch_bounds__(kThreads) void rate_step_kernel(RateArgs a) {
       for (int q = 0; q < S; ++q) target[v][q] = target[v][q] + act[v] * jump[q];
     }
   };
+  // The state update of the lane's 16 trials. Its inputs do not depend on the product, so
+  // every one of their loads is issued before it (their latency passes during the K
+  // loop); after it, the arithmetic in registers, then every store.
+  // With the voltages saved, the voltage entering this step is the saved one (written by
+  // the previous step, or the first rates' launch), and the state v is written only
+  // after the last step. A current whose decay is 0 is its target: its state is neither
+  // read nor, before the last step, written.
+  const bool in_range = n < N;
+  const int64_t nn = in_range ? n : 0;
+  auto row_b = [&](int v) { return b0 + wi * 32 + out_row(v, lane); };
+  auto ok = [&](int v) { return in_range && row_b(v) < B; };
+  auto el = [&](int v) { return (row_b(v) * T_ + t) * N + n; };  // (b, t, n) in (B, T, N)
+  float decay[S], sign[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    decay[s] = tb.decay[s];
+    sign[s] = tb.sign[s];
+  }
+  const float beta = tb.beta[nn], theta = tb.theta[nn], gain = tb.gain[nn];
+  const int code = tb.nonlinearity[nn];
+  const int32_t pos = op.rpos ? op.rpos[nn] : -1;
+  const bool has_ff = tb.K > tb.K_rec;
+  float act0[16], jump0[S];  // the first input pathway
+#pragma unroll
+  for (int q = 0; q < S; ++q) jump0[q] = has_ff ? tb.jump[(tb.K_rec * N + nn) * S + q] : 0.0f;
+  const float* __restrict__ A0 = io.A_ff;
+  const float* __restrict__ v_saved_in = io.v_saved;
+  const float* __restrict__ v_state_in = io.v;
+  const float* __restrict__ I_in = io.I;
+  float vv[16], I[16][S];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const bool o = ok(v);
+    const int64_t b = row_b(v);
+    act0[v] = o && has_ff ? A0[el(v)] : 0.0f;
+    vv[v] = !o ? 0.0f : v_saved_in ? v_saved_in[el(v)] : v_state_in[b * N + n];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+      I[v][s] = o && decay[s] != 0.0f ? I_in[(b * S + s) * N + n] : 0.0f;
+  }
   Acc c = {};
   tile_product<T>(lds, c, (int)op.n_seg, count, src, fold);
   if (n >= N) return;
-  // The state update of the lane's 16 trials, in three phases — every load, then the
-  // arithmetic in registers, then every store — so that no store sits between two loads
-  // (the pointers do not alias).
-  bool ok[16];
-  int64_t el[16];  // (b, t, n) in the (B, T, N) arrays
-#pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const int64_t b = b0 + wi * 32 + out_row(v, lane);
-    ok[v] = b < B;
-    el[v] = ((ok[v] ? b : 0) * T_ + t) * N + n;
-  }
   // the input pathways' activations, after the recurrent ones (pathway order)
   for (int64_t k = tb.K_rec; k < tb.K; ++k) {
-    const float* __restrict__ A = io.A_ff + (k - tb.K_rec) * B * T_ * N;
     float act[16], jump[S];
+    if (k == tb.K_rec) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) act[v] = ok[v] ? A[el[v]] : 0.0f;
+      for (int v = 0; v < 16; ++v) act[v] = act0[v];
 #pragma unroll
-    for (int q = 0; q < S; ++q) jump[q] = tb.jump[(k * N + n) * S + q];
+      for (int q = 0; q < S; ++q) jump[q] = jump0[q];
+    } else {
+      const float* __restrict__ A = io.A_ff + (k - tb.K_rec) * B * T_ * N;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) act[v] = ok(v) ? A[el(v)] : 0.0f;
+#pragma unroll
+      for (int q = 0; q < S; ++q) jump[q] = tb.jump[(k * N + n) * S + q];
+    }
 #pragma unroll
     for (int v = 0; v < 16; ++v)
 #pragma unroll
@@ -395,36 +454,11 @@ __global__ __launch_bounds__(kThreads) void rate_step_kernel(RateArgs a) {
       float* __restrict__ As = io.A_saved + k * B * T_ * N;
 #pragma unroll
       for (int v = 0; v < 16; ++v)
-        if (ok[v]) As[el[v]] = act[v];
+        if (ok(v)) As[el(v)] = act[v];
     }
   }
-  const float beta = tb.beta[n], theta = tb.theta[n], gain = tb.gain[n];
-  const int code = tb.nonlinearity[n];
-  const int32_t pos = op.rpos ? op.rpos[n] : -1;
   const bool last = t + 1 == T_;
-  // With the voltages saved, the voltage entering this step is the saved one (written by
-  // the previous step, or the first rates' launch), and the state v is written only
-  // after the last step. A current whose decay is 0 is its target: its state is neither
-  // read nor, before the last step, written.
-  float decay[S], sign[S];
-#pragma unroll
-  for (int s = 0; s < S; ++s) {
-    decay[s] = tb.decay[s];
-    sign[s] = tb.sign[s];
-  }
-  const float* __restrict__ v_saved_in = io.v_saved;
-  const float* __restrict__ v_state_in = io.v;
-  const float* __restrict__ I_in = io.I;
-  float vv[16], I[16][S];
-#pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const int64_t b = b0 + wi * 32 + out_row(v, lane);
-    vv[v] = !ok[v] ? 0.0f : v_saved_in ? v_saved_in[el[v]] : v_state_in[b * N + n];
-#pragma unroll
-    for (int s = 0; s < S; ++s)
-      I[v][s] = ok[v] && decay[s] != 0.0f ? I_in[(b * S + s) * N + n] : 0.0f;
-  }
-  float r[16];
+  float r[16], x[16];
 #pragma unroll
   for (int v = 0; v < 16; ++v) {
     float I_syn = 0.0f;
@@ -435,8 +469,9 @@ __global__ __launch_bounds__(kThreads) void rate_step_kernel(RateArgs a) {
       I_syn = I_syn + I[v][s] * sign[s];
     }
     vv[v] = beta * vv[v] + (1.0f - beta) * I_syn;
-    r[v] = gain * nonlin(code, vv[v] - theta);
+    x[v] = vv[v] - theta;
   }
+  nonlin_n<16>(code, gain, x, r);  // the lane's 16 trials share its neuron's nonlinearity
   float* __restrict__ out = io.out;
   float* __restrict__ v_saved_out = io.v_saved;
   float* __restrict__ v_state = io.v;
@@ -444,12 +479,12 @@ __global__ __launch_bounds__(kThreads) void rate_step_kernel(RateArgs a) {
   T* __restrict__ rin_next = static_cast<T*>(op.rin) + ((t + 1) & 1) * op.B_pad * op.K_rec_pad;
 #pragma unroll
   for (int v = 0; v < 16; ++v) {
-    if (!ok[v]) continue;
+    if (!ok(v)) continue;
     const int64_t b = b0 + wi * 32 + out_row(v, lane);
     if (!last) {
-      out[el[v] + N] = r[v];
+      out[el(v) + N] = r[v];
       if (pos >= 0) rin_next[b * op.K_rec_pad + pos] = to_storage<T>(r[v]);
-      if (v_saved_out) v_saved_out[el[v] + N] = vv[v];
+      if (v_saved_out) v_saved_out[el(v) + N] = vv[v];
     }
     if (!v_saved_out || last) v_state[b * N + n] = vv[v];
 #pragma unroll
@@ -460,12 +495,12 @@ __global__ __launch_bounds__(kThreads) void rate_step_kernel(RateArgs a) {
   if (io.target_saved || io.I_saved || io.track_v) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      if (!ok[v]) continue;
+      if (!ok(v)) continue;
       const int64_t b = b0 + wi * 32 + out_row(v, lane);
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        if (io.target_saved) io.target_saved[el[v] * S + s] = target[v][s];
-        if (io.I_saved && !last) io.I_saved[(el[v] + N) * S + s] = I[v][s];
+        if (io.target_saved) io.target_saved[el(v) * S + s] = target[v][s];
+        if (io.I_saved && !last) io.I_saved[(el(v) + N) * S + s] = I[v][s];
       }
       if (io.track_v && (io.track_b < 0 || io.track_b == b)) {
         const int64_t row = ((io.track_b < 0 ? b : 0) * T_ + t) * N + n;
