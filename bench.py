@@ -337,10 +337,13 @@ def bench_config4(args):
         "backward": 2.0 * B * N * N * T,
         "grad_w": 2.0 * B * T * N * (N + n_in),
     }
-    peak = {"forward": "bf16", "backward": "bf16", "grad_w": "f32"}
+    # (the recurrent weight gradient runs as three bf16 products of the operands' hi/lo
+    # split, wt_split_bf16: its algorithmic flops are those of the one float32 product)
+    peak = {"forward": "bf16", "backward": "bf16", "grad_w": "bf16"}
     kernel = {"forward": "rate_step_kernel (wt_rate_forward)",
               "backward": "rate_back_elem_kernel + rate_back_gemm_kernel (wt_rate_backward)",
-              "grad_w": "weight-gradient GEMM (torch.matmul, float32)"}
+              "grad_w": "weight-gradient products: wt_split_bf16 + three bf16 GEMMs with "
+                        "float32 accumulation (torch.mm / addmm, out_dtype float32)"}
     dominant = max(ms, key=ms.get)
     achieved = flops[dominant] / (ms[dominant] / 1e3) / 1e12
     peak_tf = MFMA_PEAK_TFLOPS[peak[dominant]]
@@ -367,7 +370,8 @@ def bench_config4(args):
         "config": {
             "workload": "config4: dense rate network, forward + backward",
             "neurons": N, "inputs": n_in, "batch": B, "time_steps": T, "dt_ms": synthetic.RATE_DT,
-            "products": "bf16 operands, f32 accumulation; f32 state; f32 weight gradients",
+            "products": "bf16 operands, f32 accumulation; f32 state; weight gradients as "
+                        "bf16 hi/lo split products (float32-accurate)",
             "parallelism": "single GPU",
         },
         "roofline": {

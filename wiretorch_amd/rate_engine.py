@@ -276,6 +276,28 @@ class _RateRun(torch.autograd.Function):
                 grad_beta, grad_decay, *grad_w)
 
 
+def _split(x: torch.Tensor):
+    """``(hi, lo)`` bfloat16 with ``x = hi + lo`` to 2^-17 relative (``wt_split_bf16``)."""
+    x = x.float().contiguous()
+    if x.data_ptr() % 16:  # the kernel moves 16-byte vectors
+        x = x.clone()
+    hi = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    lo = torch.empty_like(hi)
+    _lib.check(_lib.load().wt_split_bf16(x.data_ptr(), x.numel(), hi.data_ptr(), lo.data_ptr(),
+                                         torch.cuda.current_stream(x.device).cuda_stream),
+               "wt_split_bf16")
+    return hi, lo
+
+
+def _split_product(a_hi, a_lo, b_hi, b_lo) -> torch.Tensor:
+    """``a^T b`` of float32 matrices given as bf16 (hi, lo) pairs: hi.hi + hi.lo + lo.hi on
+    the matrix cores, float32 accumulation and output (the lo.lo term is below float32's
+    rounding of the sum)."""
+    C = torch.mm(a_hi.T, b_hi, out_dtype=torch.float32)
+    C = torch.addmm(C, a_hi.T, b_lo, out_dtype=torch.float32)
+    return torch.addmm(C, a_lo.T, b_hi, out_dtype=torch.float32)
+
+
 def _weight_and_input_grads(L: _Plan, out, x, grad_A, weights, w_needs, want_x):
     """``dL/dW_k = sum_{b,t} pre ⊗ dL/da_k`` (``pre``: the source rates, or the inputs) and
     ``dL/dx = dL/da_k W_k^T`` per input pathway (``rate/engine.py:367-376``), float32."""
@@ -283,8 +305,9 @@ def _weight_and_input_grads(L: _Plan, out, x, grad_A, weights, w_needs, want_x):
     grad_w = [None] * len(weights)
     for k, rows in enumerate(L.rows_rec):
         if w_needs[k]:
-            r_k = _columns(out, rows).reshape(B * T, -1)
-            grad_w[k] = r_k.T @ grad_A[k].reshape(B * T, N)
+            r_hi, r_lo = _split(_columns(out, rows).reshape(B * T, -1))
+            g_hi, g_lo = _split(grad_A[k].reshape(B * T, N))
+            grad_w[k] = _split_product(r_hi, r_lo, g_hi, g_lo)
     grad_x = torch.zeros_like(x, dtype=torch.float32) if want_x else None
     for j, (rows, W) in enumerate(zip(L.rows_ff, weights[L.K_rec:])):
         k = L.K_rec + j
