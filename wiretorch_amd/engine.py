@@ -272,18 +272,24 @@ def _side_of(pathways, sparse, n_src: int, N: int, device) -> _Side:
     if hit is not None:
         _CACHE.move_to_end(key)
         return hit[0]
-    side = (_from_connectome(sparse, device) if sparse is not None
-            else _dense_side(pathways, n_src, N, device))
+    if sparse is not None:
+        side = _from_connectome(sparse, device)
+    else:
+        side, derived = _dense_side(pathways, n_src, N, device)
+        if derived:
+            # weights recomputed each call (learnt projections) never come again: caching
+            # them by value would only hold their dense matrices
+            return side
     _CACHE[key] = (side, keep)  # holding the tensors keeps their addresses unique
     while len(_CACHE) > _CACHE_SIZE:
         _CACHE.popitem(last=False)
     return side
 
 
-def _dense_side(pathways, n_src: int, N: int, device) -> _Side:
+def _dense_side(pathways, n_src: int, N: int, device) -> tuple[_Side, bool]:
     """The side of dense pathways: from the layout of the same structure and nonzero
-    pattern if one is cached (the edge weights gathered from the matrices), else
-    compressed anew."""
+    pattern if one is cached (the edge weights gathered from the matrices; second item
+    True), else compressed anew."""
     key = ("layout", n_src, N) + tuple(
         (rows.data_ptr(), rows._version, tuple(rows.shape), tuple(W.shape))
         for rows, W in pathways)
@@ -295,13 +301,13 @@ def _dense_side(pathways, n_src: int, N: int, device) -> _Side:
             weights = torch.empty_like(base.conn.weights)
             for (_, W), (e, flat) in zip(pathways, base.dense_edges):
                 weights[e] = W.detach().to(device, torch.float32).reshape(-1)[flat]
-            return base.with_weights(weights, _dense_in_sum(pathways))
+            return base.with_weights(weights, _dense_in_sum(pathways)), True
     side = _from_pathways(pathways, n_src, N, device)
     masks = tuple((W.detach() != 0).to(device) for _, W in pathways)
     _LAYOUTS[key] = (side, masks, tuple(rows for rows, _ in pathways))
     while len(_LAYOUTS) > _LAYOUTS_SIZE:
         _LAYOUTS.popitem(last=False)
-    return side
+    return side, False
 
 
 # =====================================================================
