@@ -545,9 +545,13 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     // bitmap after the update.
     // Then one thread per listed source, and per listed input, issues its range lookups
     // (and pathway) into registers: their latency passes during the update.
+    // The list holds 2 x kRunBlock sources: the first kRunBlock in s_fired, the next in
+    // the event list's count array (unused until the appends after the update).
     // rest: bit u (u < 8) — every fired bit of preloaded word u is past the list's
     // capacity; bits 8-15 = u + 1 and bits 16-23 = k for the word whose k lowest fired
     // bits were listed and whose others were not (at most one per workgroup).
+    constexpr int kListed = 2 * kRunBlock;
+    uint32_t* const s_fired2 = reinterpret_cast<uint32_t*>(s_count);
     uint32_t rest = 0u;
 #pragma unroll
     for (int u = 0; u < MAXI; ++u) {
@@ -562,14 +566,18 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       const uint32_t q = w / (uint32_t)total_words, wl = w - q * (uint32_t)total_words;
       const uint32_t j0 =
           (wl / (uint32_t)words) * (uint32_t)range_n + (wl % (uint32_t)words) * 32;
-      if (pos >= kRunBlock) {
+      if (pos >= kListed) {
         rest |= 1u << u;
         continue;
       }
-      if (pos + (int)n > kRunBlock)
-        rest |= (uint32_t)(u + 1) << 8 | (uint32_t)(kRunBlock - pos) << 16;
-      for (; bits && pos < kRunBlock; ++pos) {
-        s_fired[pos] = (j0 + __builtin_ctz(bits)) | (q << 24);
+      if (pos + (int)n > kListed)
+        rest |= (uint32_t)(u + 1) << 8 | (uint32_t)(kListed - pos) << 16;
+      for (; bits && pos < kListed; ++pos) {
+        const uint32_t f = (j0 + __builtin_ctz(bits)) | (q << 24);
+        if (pos < kRunBlock)
+          s_fired[pos] = f;
+        else
+          s_fired2[pos - kRunBlock] = f;
         bits &= bits - 1;
       }
     }
@@ -719,6 +727,23 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       update(std::false_type{});
     else
       update(std::true_type{});
+    // A second listed source per thread (sources kRunBlock .. 2 kRunBlock - 1): its
+    // lookups are issued now, its entry read before the barrier below (the appends that
+    // follow it write the event list over the entries).
+    int64_t re0b = 0, re1b = 0;
+    int32_t rkb = -1;
+    uint32_t rjb = 0;
+    if (s_nfired > kRunBlock) {  // uniform (a burst of firing)
+      ArgPtr P = kargs();
+      const int n_list2 = (s_nfired < kListed ? s_nfired : kListed) - kRunBlock;
+      if ((int)threadIdx.x < n_list2) {
+        rjb = s_fired2[threadIdx.x];
+        const int64_t* sp = P->rec.split + (int64_t)(rjb & 0xffffffu) * (R + 1) + r;
+        re0b = gload(sp);
+        re1b = gload(sp + 1);
+        rkb = gload(P->rec.pathway + (rjb & 0xffffffu));
+      }
+    }
     tick(s_time, 2);
     __syncthreads();  // the accumulator is read and cleared; the next bits are complete
     tick(s_time, 3);
@@ -801,6 +826,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     {
       ArgPtr P = kargs();
       bool rec_pending = rk >= 0 && re1 > re0, in_pending = ik >= 0 && ie1 > ie0;
+      bool rec2_pending = rkb >= 0 && re1b > re0b;
       uint32_t rest_bits[MAXI];
 #pragma unroll
       for (int u = 0; u < MAXI; ++u) rest_bits[u] = 0u;
@@ -823,13 +849,22 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
         // the listed source and input of each thread: one reservation per wave
         {
           uint32_t total;
-          const uint32_t below = wave_prefix<2>((uint32_t)rec_pending + in_pending, total);
+          const uint32_t below =
+              wave_prefix<2>((uint32_t)rec_pending + rec2_pending + in_pending, total);
           int pos = wave_reserve(EL.n, total) + (int)below;
           if (rec_pending) {
             if (pos < cap) {
               put_event(EL, pos, 0, re0, re1, rk * acc_stride + (int64_t)(rj >> 24) * range_n,
                         lo, 1.0f);
               rec_pending = false;
+            }
+            ++pos;
+          }
+          if (rec2_pending) {
+            if (pos < cap) {
+              put_event(EL, pos, 0, re0b, re1b,
+                        rkb * acc_stride + (int64_t)(rjb >> 24) * range_n, lo, 1.0f);
+              rec2_pending = false;
             }
             ++pos;
           }
