@@ -91,6 +91,36 @@ __device__ inline BackNeuron back_neuron(const wt_tables& tab, int64_t n) {
   return c;
 }
 
+// One reverse step's inputs at (b, t, n): what the forward saved of step t and the
+// spike's gradient. The reverse loop loads them a step ahead, so that their latency
+// passes during the step before.
+template <int S>
+struct StepIn {
+  float v, spike, held, grad_spike, grad_prob;
+  float G[S];
+  float A[WT_MAX_K];  // the injected activations (when their partials are wanted)
+};
+
+template <int S>
+__device__ inline void load_step(StepIn<S>& in, const BackArgs& P, int64_t b, int64_t n,
+                                 int64_t t) {
+  const wt_tables& tab = P.tab;
+  const wt_backward_io& io = P.io;
+  const int64_t N = tab.N, K = tab.K, B = io.B, T = io.T;
+  const int64_t out = (b * T + t) * N + n;
+  in.v = io.v_saved[out];
+  in.spike = io.spikes[out];
+  in.held = io.held ? (float)io.held[out] : 0.0f;
+  in.grad_spike = io.grad_spikes[out];
+  in.grad_prob = io.grad_prob ? io.grad_prob[out] : 0.0f;
+#pragma unroll
+  for (int s = 0; s < S; ++s) in.G[s] = io.G_saved[out * S + s];
+  const bool want_A = io.grad_decay || io.grad_jump || io.grad_scale;
+#pragma unroll
+  for (int k = 0; k < WT_MAX_K; ++k)
+    in.A[k] = want_A && k < K ? io.A[((k * B + b) * T + t) * N + n] : 0.0f;
+}
+
 // Reverse step t, all but the spike of step t: the injections of step t (dL/da_k, the
 // jump and decay partials), the membrane update, and the conductances decaying into
 // step t+1. Leaves st.dv = dL/dv_t without the spike's term. When grad_now is set,
@@ -98,29 +128,31 @@ __device__ inline BackNeuron back_neuron(const wt_tables& tab, int64_t n) {
 template <int S>
 __device__ inline void back_membrane_step(BackState<S>& st, const BackArgs& P,
                                           const Synapses<S>& syn, const BackNeuron& c,
-                                          int64_t b, int64_t n, int64_t t) {
+                                          int64_t b, int64_t n, int64_t t,
+                                          const StepIn<S>& in, const float (&scale)[WT_MAX_K]) {
   const wt_tables& tab = P.tab;
   const wt_backward_io& io = P.io;
   const int64_t N = tab.N, K = tab.K, B = io.B, T = io.T;
   const bool refractory = io.held != nullptr;
   const bool want_A = io.grad_A != nullptr, want_scale = io.grad_scale != nullptr;
   const bool want_decay = io.grad_decay != nullptr, want_jump = io.grad_jump != nullptr;
-  const int64_t out = (b * T + t) * N + n;
-  const float v = io.v_saved[out];
-  const float s_sp = io.spikes[out];
-  const float held = refractory ? (float)io.held[out] : 0.0f;
+  const float v = in.v;
+  const float s_sp = in.spike;
+  const float held = in.held;
   const float r = refractory ? fmaxf(s_sp, held) : s_sp;
   float G[S];
 #pragma unroll
-  for (int s = 0; s < S; ++s) G[s] = io.G_saved[out * S + s];
+  for (int s = 0; s < S; ++s) G[s] = in.G[s];
 
   // Injections of step t: per unit jump, sum_k a_k scale_k made_k (jump, decay).
   if (want_decay || want_jump) {
     float base[S];
 #pragma unroll
     for (int s = 0; s < S; ++s) base[s] = 0.0f;
-    for (int64_t k = 0; k < K; ++k) {
-      const float as = io.A[((k * B + b) * T + t) * N + n] * tab.scale[k * N + n];
+#pragma unroll
+    for (int k = 0; k < WT_MAX_K; ++k) {
+      if (k >= K) break;
+      const float as = in.A[k] * scale[k];
 #pragma unroll
       for (int s = 0; s < S; ++s) base[s] += as * tab.made[k * S + s];
     }
@@ -147,10 +179,10 @@ __device__ inline void back_membrane_step(BackState<S>& st, const BackArgs& P,
     for (int s = 0; s < S; ++s)
       qk += (syn.jump_r[s] * st.lr[s] + syn.jump_d[s] * st.ld[s]) * tab.made[k * S + s];
     const int64_t ka = ((k * B + b) * T + t) * N + n;
-    const float ga = qk * tab.scale[k * N + n];
+    const float ga = qk * scale[k];
     if (want_A) io.grad_A[ka] = ga;
     if (P.grad_now && k < tab.K_rec) P.grad_now[(k * N + n) * B + b] = ga;
-    if (want_scale) st.acc_scale[k] += qk * io.A[ka];
+    if (want_scale) st.acc_scale[k] += qk * in.A[k];
   }
   // Membrane.
   const float gx = st.dv * (1.0f - r);
@@ -190,18 +222,16 @@ __device__ inline void back_membrane_step(BackState<S>& st, const BackArgs& P,
 // dL/ds_t through the recurrent synapses (0 when gradients do not flow there).
 template <int S>
 __device__ inline void back_spike_step(BackState<S>& st, const BackArgs& P,
-                                       const BackNeuron& c, int64_t b, int64_t n, int64_t t,
-                                       float carried) {
+                                       const BackNeuron& c, float carried,
+                                       const StepIn<S>& in) {
   const wt_backward_io& io = P.io;
-  const int64_t N = P.tab.N, T = io.T;
-  const int64_t out = (b * T + t) * N + n;
-  const float x = io.v_saved[out] - c.theta;
-  float g_x = surrogate(x, io.grad_spikes[out] + carried, c.k_surr);
+  const float x = in.v - c.theta;
+  float g_x = surrogate(x, in.grad_spike + carried, c.k_surr);
   if (io.grad_prob) {
     const float p = 1.0f / (1.0f + expf(-(c.k_surr * x)));
-    g_x += io.grad_prob[out] * c.k_surr * p * (1.0f - p);
+    g_x += in.grad_prob * c.k_surr * p * (1.0f - p);
   }
-  if (io.held) g_x *= 1.0f - (float)io.held[out];
+  if (io.held) g_x *= 1.0f - in.held;
   st.dv += g_x;
   st.acc_theta -= g_x;
 }
@@ -250,11 +280,18 @@ __global__ __launch_bounds__(256) void cond_backward_kernel(BackArgs P) {
   Synapses<S> syn;
   load_synapses<S>(P.tab, syn);
   const BackNeuron c = back_neuron(P.tab, n);
+  float scale[WT_MAX_K];
+#pragma unroll
+  for (int k = 0; k < WT_MAX_K; ++k) scale[k] = k < P.tab.K ? P.tab.scale[k * N + n] : 0.0f;
   BackState<S> st;
   state_zero(st);
+  StepIn<S> cur, next;
+  if (T > 0) load_step<S>(cur, P, b, n, T - 1);
   for (int64_t t = T - 1; t >= 0; --t) {
-    back_membrane_step<S>(st, P, syn, c, b, n, t);
-    back_spike_step<S>(st, P, c, b, n, t, 0.0f);
+    if (t > 0) load_step<S>(next, P, b, n, t - 1);  // a step ahead
+    back_membrane_step<S>(st, P, syn, c, b, n, t, cur, scale);
+    back_spike_step<S>(st, P, c, 0.0f, cur);
+    cur = next;
   }
   back_finish<S>(st, P, b, n);
 }
@@ -269,9 +306,14 @@ __global__ __launch_bounds__(256) void rg_membrane_kernel(BackArgs P, int64_t t)
   Synapses<S> syn;
   load_synapses<S>(P.tab, syn);
   const BackNeuron c = back_neuron(P.tab, n);
+  float scale[WT_MAX_K];
+#pragma unroll
+  for (int k = 0; k < WT_MAX_K; ++k) scale[k] = k < P.tab.K ? P.tab.scale[k * N + n] : 0.0f;
   BackState<S> st;
   if (t == P.io.T - 1) state_zero(st); else state_io<S>(st, P.state, B * N, idx, false);
-  back_membrane_step<S>(st, P, syn, c, b, n, t);
+  StepIn<S> in;
+  load_step<S>(in, P, b, n, t);
+  back_membrane_step<S>(st, P, syn, c, b, n, t, in, scale);
   state_io<S>(st, P.state, B * N, idx, true);
 }
 
@@ -297,7 +339,16 @@ __global__ __launch_bounds__(256) void rg_spike_kernel(BackArgs P, int64_t t) {
   BackState<S> st;
   st.dv = P.state[item];
   st.acc_theta = P.state[(int64_t)(back_fields<S>() - 5) * BN + item];
-  back_spike_step<S>(st, P, c, b, j, t, R);
+  StepIn<S> in;
+  {
+    const wt_backward_io& io = P.io;
+    const int64_t out = (b * io.T + t) * N + j;
+    in.v = io.v_saved[out];
+    in.grad_spike = io.grad_spikes[out];
+    in.grad_prob = io.grad_prob ? io.grad_prob[out] : 0.0f;
+    in.held = io.held ? (float)io.held[out] : 0.0f;
+  }
+  back_spike_step<S>(st, P, c, R, in);
   P.state[item] = st.dv;
   P.state[(int64_t)(back_fields<S>() - 5) * BN + item] = st.acc_theta;
 }
