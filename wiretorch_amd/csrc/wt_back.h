@@ -94,11 +94,13 @@ __device__ inline BackNeuron back_neuron(const wt_tables& tab, int64_t n) {
 // One reverse step's inputs at (b, t, n): what the forward saved of step t and the
 // spike's gradient. The reverse loop loads them a step ahead, so that their latency
 // passes during the step before.
+constexpr int kPreK = 4;  // pathways whose activations are loaded ahead (the rest in step)
+
 template <int S>
 struct StepIn {
   float v, spike, held, grad_spike, grad_prob;
   float G[S];
-  float A[WT_MAX_K];  // the injected activations (when their partials are wanted)
+  float A[kPreK];  // the injected activations (when their partials are wanted)
 };
 
 template <int S>
@@ -117,8 +119,16 @@ __device__ inline void load_step(StepIn<S>& in, const BackArgs& P, int64_t b, in
   for (int s = 0; s < S; ++s) in.G[s] = io.G_saved[out * S + s];
   const bool want_A = io.grad_decay || io.grad_jump || io.grad_scale;
 #pragma unroll
-  for (int k = 0; k < WT_MAX_K; ++k)
+  for (int k = 0; k < kPreK; ++k)
     in.A[k] = want_A && k < K ? io.A[((k * B + b) * T + t) * N + n] : 0.0f;
+}
+
+// Activation k of the step at (b, t, n): loaded ahead for the first kPreK pathways.
+template <int S>
+__device__ inline float step_A(const StepIn<S>& in, const BackArgs& P, int k, int64_t b,
+                               int64_t n, int64_t t) {
+  if (k < kPreK) return in.A[k];
+  return P.io.A[((k * P.io.B + b) * P.io.T + t) * P.tab.N + n];
 }
 
 // Reverse step t, all but the spike of step t: the injections of step t (dL/da_k, the
@@ -152,7 +162,7 @@ __device__ inline void back_membrane_step(BackState<S>& st, const BackArgs& P,
 #pragma unroll
     for (int k = 0; k < WT_MAX_K; ++k) {
       if (k >= K) break;
-      const float as = in.A[k] * scale[k];
+      const float as = step_A<S>(in, P, k, b, n, t) * scale[k];
 #pragma unroll
       for (int s = 0; s < S; ++s) base[s] += as * tab.made[k * S + s];
     }
@@ -182,7 +192,7 @@ __device__ inline void back_membrane_step(BackState<S>& st, const BackArgs& P,
     const float ga = qk * scale[k];
     if (want_A) io.grad_A[ka] = ga;
     if (P.grad_now && k < tab.K_rec) P.grad_now[(k * N + n) * B + b] = ga;
-    if (want_scale) st.acc_scale[k] += qk * in.A[k];
+    if (want_scale) st.acc_scale[k] += qk * step_A<S>(in, P, k, b, n, t);
   }
   // Membrane.
   const float gx = st.dv * (1.0f - r);
