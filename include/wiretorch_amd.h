@@ -75,9 +75,10 @@ typedef struct {
  * b = g, g+groups, ...; workgroup slot r of a group owns targets [r*range_n, ...);
  * range_n is a multiple of 32, and a workgroup owns at most 8192 (trial, neuron) items.
  * frac_bits: activations are accumulated exactly as int64 multiples of 2^-frac_bits.
- * max_list: limit on the per-workgroup event list (1024, 2048, 3072 or 4096 entries; 0 =
- * the largest that fits in LDS). A step's events beyond the list are pushed in further
- * rounds; results do not depend on it. */
+ * max_list: the per-workgroup event list, 1024 or 2048 entries (0 = the largest that
+ * fits in LDS; 2048 needs at most 4096 items per workgroup and room beside the
+ * accumulator). A step's events beyond the list are pushed in further rounds; results do
+ * not depend on it. */
 typedef struct {
   int64_t groups, R, range_n, frac_bits, max_list;
 } wt_geometry;

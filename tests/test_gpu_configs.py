@@ -5,9 +5,8 @@
   first 200 steps, voltages within 1e-5 relative — the bar of configuration 0.
 * Dense firing (a strongly driven configuration-3 network at 70 Hz, 16 trials, two per
   workgroup): most steps list more than 1,024 fired sources per workgroup, some more than
-  2,048. With the event list as large as fits (4,096 entries here) each step is pushed in
-  one round; with the list limited to 1,024 entries (``engine.MAX_LIST``, the static list
-  of the kernels for larger workgroups) in two or three. Forward and training step to the
+  2,048. With the 2,048-entry event list most steps are pushed in one round, with the
+  1,024-entry list (``engine.MAX_LIST``) in two or three. Forward and training step to the
   bars of configurations 1 and 3, both ways.
 * Two training steps of configuration 3's network with the learnt weights changed in
   between: the second takes the new weights through the cached layout of the dense
@@ -97,7 +96,7 @@ def _fired_per_workgroup_step(spikes):
     return spikes.reshape(-1, groups, T, N).sum(axis=(0, 3))
 
 
-@pytest.fixture(params=[0, 1024], ids=["list-as-fits", "list-1024"])
+@pytest.fixture(params=[2048, 1024], ids=["list-2048", "list-1024"])
 def max_list(request):
     saved = engine.MAX_LIST
     engine.MAX_LIST = request.param

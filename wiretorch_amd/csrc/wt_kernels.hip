@@ -430,31 +430,20 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
   if (qe == hipSuccess)
     qe = hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   if (qe != hipSuccess) return qe;
-  // static LDS besides the event list (+ 64 for the one-entry arrays of the large-list
-  // kernels and alignment)
+  // static LDS besides the event list (+ 64 for alignment)
   const size_t static_lds = kRunBlock * 4 + sizeof(BlockScan::storage_type) +
                             (kPhases + 1) * 8 + 64 + kMaxLdsTypes * kRow * 4 +
                             kMaxOwnWords * 4 + kMaxItemsPerWg + 64;
   const int64_t per_thread = (tpg * geo->range_n + kRunBlock - 1) / kRunBlock;
-  // a list larger than kRunBlock entries after the accumulator where it fits (and the
-  // workgroup has at most kBigMaxi items per thread); else kRunBlock entries in static LDS
-  const size_t list_off = (lds + 15) / 16 * 16;
-  int32_t cap = 0;
-  for (int32_t c = kMaxList; c > kRunBlock && cap == 0 && per_thread <= kBigMaxi;
-       c -= kRunBlock)
-    if ((geo->max_list == 0 || c <= geo->max_list) &&
-        static_lds + list_off + (size_t)list_bytes(c) <= (size_t)max_lds)
-      cap = c;
-  size_t dyn = lds;
-  if (cap > 0) {
-    dyn = list_off + (size_t)list_bytes(cap);
-  } else {
-    cap = kRunBlock;
-    if (static_lds + (size_t)list_bytes(kRunBlock) + lds > (size_t)max_lds)
-      return hipErrorInvalidValue;
-  }
-  a.list_off = (int64_t)list_off;
+  // the kMaxList-entry list where the accumulator leaves room for it (and the workgroup
+  // has at most kBigMaxi items per thread); else kRunBlock entries
+  int32_t cap = kRunBlock;
+  if (per_thread <= kBigMaxi && (geo->max_list == 0 || geo->max_list >= kMaxList) &&
+      static_lds + (size_t)list_bytes(kMaxList) + lds <= (size_t)max_lds)
+    cap = kMaxList;
+  if (static_lds + (size_t)list_bytes(cap) + lds > (size_t)max_lds) return hipErrorInvalidValue;
   a.list_cap = cap;
+  const size_t dyn = lds;
   if (ff->n_src > 0 && io->x) {
     const int64_t rows = io->B * io->T;
     hipLaunchKernelGGL(compact_input_kernel, dim3((unsigned)rows), dim3(256), 0,

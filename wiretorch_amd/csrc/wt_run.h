@@ -43,8 +43,7 @@ struct RunArgs {
   uint64_t* timing;     // [wgs][kPhases] wall-clock ticks per phase, or null
   int64_t words;        // bitmap words per workgroup range (range_n / 32)
   int64_t tpg_max;      // trials of the largest group
-  int64_t list_off;     // byte offset of the event list in dynamic LDS (after the accumulator)
-  int32_t list_cap;     // event list capacity: 1024, 2048, 3072 or 4096 entries
+  int32_t list_cap;     // event list capacity: 1024 or 2048 entries
 };
 
 // Phases timed by wt_cond_run_timed (thread 0's view): its own update, the wait for the
@@ -58,9 +57,9 @@ constexpr int kTypeCols = 6;  // global table: theta, U_reset, E_L, C_m, beta, n
 constexpr int kRow = 16;
 constexpr int kMaxItemsPerWg = 8 * kRunBlock;        // trials x range per workgroup
 constexpr int kMaxOwnWords = kMaxItemsPerWg / 32;    // the workgroup's own fired bits
-constexpr int kMaxList = 4 * kRunBlock;  // event list entries at most (four per thread)
+constexpr int kMaxList = 2 * kRunBlock;  // event list entries at most (two per thread)
 
-// Dynamic LDS of the event list of `cap` entries and its entry map (cap / 4 buckets of 64
+// LDS of the event list of `cap` entries and its entry map (cap / 4 buckets of 64
 // edges): e0 (8), heads (8 per bucket), count, row, value (4 each), first (2 per bucket),
 // side (1).
 constexpr int64_t list_bytes(int64_t cap) { return cap * 21 + (cap / 4) * 10; }
@@ -326,9 +325,8 @@ __device__ inline void run_events(const EventList& L, int m, int32_t total, doub
 // The persistent forward. Each thread owns up to MAXI (trial, neuron) items — item
 // threadIdx.x + i * blockDim.x of its workgroup — whose state stays in registers for
 // the whole launch.
-// BIG: the event list lives in dynamic LDS after the accumulator with the capacity the
-// host found room for (more than kRunBlock entries); otherwise kRunBlock entries in static
-// LDS at fixed addresses.
+// BIG: the event list holds kMaxList entries, otherwise kRunBlock (static LDS, fixed
+// addresses either way; the host takes BIG where the accumulator leaves room).
 template <int S, int MAXI, bool EXTRA, bool REFR, bool BIG>
 __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   static_assert(MAXI <= 8, "the overflow note holds one bit per preloaded word");
@@ -367,31 +365,14 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   const float dt = *A.tab.dt;
   const Fixed fx{ldexpf(1.0f, (int)A.geo.frac_bits), ldexp(1.0, -(int)A.geo.frac_bits)};
   // the event list and its entry map
-  constexpr int kStatic = BIG ? 1 : kRunBlock;
-  __shared__ int64_t s_e0_fixed[kStatic];
-  __shared__ uint64_t s_heads_fixed[kStatic / 4 + 1];
-  __shared__ int32_t s_count_fixed[kStatic], s_row_fixed[kStatic];
-  __shared__ float s_value_fixed[kStatic];
-  __shared__ int16_t s_first_fixed[kStatic / 4 + 1];
-  __shared__ uint8_t s_side_fixed[kStatic];
-  const int cap = BIG ? A.list_cap : kRunBlock, nbk = cap / 4;
-  int64_t* s_e0 = s_e0_fixed;
-  uint64_t* s_heads = s_heads_fixed;
-  int32_t* s_count = s_count_fixed;
-  int32_t* s_row = s_row_fixed;
-  float* s_value = s_value_fixed;
-  int16_t* s_first = s_first_fixed;
-  uint8_t* s_side = s_side_fixed;
-  if constexpr (BIG) {  // after the accumulator (the host sizes both)
-    char* const lp = reinterpret_cast<char*>(acc) + A.list_off;
-    s_e0 = reinterpret_cast<int64_t*>(lp);
-    s_heads = reinterpret_cast<uint64_t*>(lp + (int64_t)cap * 8);
-    s_count = reinterpret_cast<int32_t*>(lp + (int64_t)cap * 8 + nbk * 8);
-    s_row = s_count + cap;
-    s_value = reinterpret_cast<float*>(s_row + cap);
-    s_first = reinterpret_cast<int16_t*>(s_value + cap);
-    s_side = reinterpret_cast<uint8_t*>(s_first + nbk);
-  }
+  constexpr int kList = BIG ? kMaxList : kRunBlock;
+  __shared__ int64_t s_e0[kList];
+  __shared__ uint64_t s_heads[kList / 4];
+  __shared__ int32_t s_count[kList], s_row[kList];
+  __shared__ float s_value[kList];
+  __shared__ int16_t s_first[kList / 4];
+  __shared__ uint8_t s_side[kList];
+  constexpr int cap = kList, nbk = kList / 4;
   const EventList EL{s_e0, s_count, s_row, s_value, s_side, &s_nev, s_first, s_heads, cap, nbk};
   Synapses<S> syn;
   load_synapses<S>(A.tab, syn);
@@ -966,8 +947,9 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
         const int m = n_ev < cap ? n_ev : cap;
         if (m > 0) {  // m is uniform: every thread takes part in the scan
           const int tid = threadIdx.x;
-          // thread tid scans entries tid * per .. + per - 1 (per = cap / kRunBlock)
-          const int per = cap / kRunBlock, a0 = tid * per;
+          // thread tid scans entries tid * per .. + per - 1
+          constexpr int per = cap / kRunBlock;
+          const int a0 = tid * per;
           int32_t cnt[kMaxList / kRunBlock], sum = 0, c, total;
 #pragma unroll
           for (int j = 0; j < kMaxList / kRunBlock; ++j) {

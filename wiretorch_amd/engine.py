@@ -74,9 +74,24 @@ class _timed:
 PHASE_TIMING: list | None = None
 #: Phase slots per workgroup that ``wt_cond_run_timed`` writes.
 PHASES = 8
-#: Limit on the forward's per-workgroup event list (entries, a multiple of 1024; 0 = the
-#: largest that fits). Results do not depend on it; tests lower it to exercise the rounds.
+#: The forward's per-workgroup event list (entries: 1024, or 2048 where the accumulator
+#: leaves room); 0 = chosen per call (``_list_size``). Results do not depend on it; tests
+#: set it to exercise both kernels and the rounds.
 MAX_LIST = 0
+#: Nominal firing rate (Hz) for the list size: the 2048-entry list is taken where a
+#: workgroup's trials could list more than 512 fired sources per step at this rate.
+_LIST_RATE_HZ = 50.0
+
+
+def _list_size(B: int, N: int, groups: int, dt_ms: float) -> int:
+    """1024 or 2048: the larger list costs registers, so it is taken only where dense
+    firing would overflow the smaller one (every workgroup lists the fired sources of
+    all its group's trials)."""
+    if MAX_LIST:
+        return MAX_LIST
+    tpg = -(-B // groups)
+    expected = tpg * N * _LIST_RATE_HZ * dt_ms / 1000.0
+    return 2048 if expected > 512 else 1024
 
 
 # =====================================================================
@@ -421,6 +436,7 @@ class _Plan:
     ff: _Side
     geo: tuple
     frac_bits: int
+    max_list: int
     refractory: bool
     probabilities: bool
     track: bool
@@ -467,6 +483,8 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
         raise ValueError("feedforward connectome does not match the input and network")
     n_cu, max_lds = _device_info(device)
     groups, R, range_n = geometry(B, N, K_rec + K_ff, n_cu, max_lds)
+    dt_ms = _cached(("dt",) + _key(p.dt), (p.dt,), lambda: float(p.dt))
+    max_list = _list_size(B, N, groups, dt_ms)
     bound = rec.max_in_sum
     if ff.n_src and ff.conn.n_edges:
         xd = x.detach()
@@ -490,7 +508,7 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
     tables = _cached(("tables", str(device)) + _key(*sources), sources, make_tables)
     return _Plan(
         B=B, T=T, N=N, S=S, K_rec=K_rec, K_ff=K_ff, n_in=n_in, tables=tables, rec=rec,
-        ff=ff, geo=(groups, R, range_n), frac_bits=_frac_bits(bound),
+        ff=ff, geo=(groups, R, range_n), frac_bits=_frac_bits(bound), max_list=max_list,
         refractory=p.n_ref is not None, probabilities=probabilities, track=track,
         track_b=(-1 if track_batch_idx is None else int(track_batch_idx)) if track else 0,
         stream=torch.cuda.current_stream(device).cuda_stream, device=device,
@@ -500,7 +518,7 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
 def _launch(L: _Plan, x, scale, v, g, counter, spikes, prob, saved, tracked,
             rec_weights=None, ff_weights=None) -> None:
     groups, R, range_n = L.geo
-    geo = _lib.Geometry(groups, R, range_n, L.frac_bits, MAX_LIST)
+    geo = _lib.Geometry(groups, R, range_n, L.frac_bits, L.max_list)
     lib = _lib.load()
     scratch = torch.empty(int(lib.wt_cond_run_scratch_bytes(geo, L.B, L.T)),
                           dtype=torch.uint8, device=L.device)
