@@ -3,8 +3,8 @@
 
 * Configuration 1 (forward, dt 0.1 ms): spike raster identical to the oracle's over the
   first 200 steps, voltages within 1e-5 relative — the bar of configuration 0.
-* Dense firing (a strongly driven configuration-3 network at 70 Hz, 16 trials, two per
-  workgroup): most steps list more than 1,024 fired sources per workgroup, some more than
+* Dense firing (a strongly driven configuration-3 network at 70 Hz, 16 trials in 8
+  groups, two per workgroup): most steps list more than 1,024 fired sources per workgroup, some more than
   2,048. With the 2,048-entry event list most steps are pushed in one round, with the
   1,024-entry list (``engine.MAX_LIST``) in two or three. Forward and training step to the
   bars of configurations 1 and 3, both ways.
@@ -98,10 +98,12 @@ def _fired_per_workgroup_step(spikes):
 
 @pytest.fixture(params=[2048, 1024], ids=["list-2048", "list-1024"])
 def max_list(request):
-    saved = engine.MAX_LIST
-    engine.MAX_LIST = request.param
+    """The event list's size, with 8 groups (two trials per group, so that a workgroup
+    lists more than 1,024 fired sources in most steps)."""
+    saved = engine.MAX_LIST, engine.MAX_GROUPS
+    engine.MAX_LIST, engine.MAX_GROUPS = request.param, 8
     yield request.param
-    engine.MAX_LIST = saved
+    engine.MAX_LIST, engine.MAX_GROUPS = saved
 
 
 def test_dense_firing_forward_matches_oracle(max_list):

@@ -41,7 +41,9 @@ from wiretorch_amd.network import Drive, Physiology, Run
 PHYSIOLOGY = ("theta", "U_reset", "E_L", "C_m", "beta", "E_syn", "decay", "jump")
 MAX_FRAC_BITS = 40
 BLOCK = 1024
-MAX_GROUPS = 8
+#: Upper limit on trial groups (the kernel takes up to 64); ``geometry`` picks the count.
+MAX_GROUPS = 64
+XCDS = 8
 MAX_TYPES = 256
 #: When a list, every ``wt_cond_run`` launch appends a pair of events recorded on its
 #: stream just before and after it (``bench.py`` times the kernel with them).
@@ -344,29 +346,44 @@ def _device_info(device) -> tuple[int, int]:
 
 
 def geometry(B: int, N: int, K: int, n_cu: int, max_lds: int) -> tuple[int, int, int]:
-    """``(groups, R, range_n)``: trials round-robin over up to 8 groups (one per XCD);
-    each group's targets split over R workgroups (range_n a multiple of 32), about one
-    (trial, neuron) item per thread and at most 8 per thread (they live in registers),
-    within the LDS budget of the int64 accumulator ``K * trials * range_n`` and the
-    fired bitmap."""
-    groups = max(1, min(MAX_GROUPS, B))
-    tpg = -(-B // groups)
-    limit = max(1, n_cu // groups)
+    """``(groups, R, range_n)``: trials round-robin over groups, each group's targets
+    split over R workgroups (range_n a multiple of 32), about one (trial, neuron) item per
+    thread and at most 8 per thread (they live in registers), within the LDS budget of
+    the int64 accumulator ``K * trials * range_n`` and the fired bitmap.
+
+    As many groups as fit, one trial each where the batch allows: every workgroup lists
+    and looks up the fired sources of all its group's trials, and waits for its group's
+    R arrivals each step, so fewer trials per group mean less of both for the same
+    targets. Past 8, groups come in multiples of 8: workgroup i is in group i % groups
+    and on XCD i % 8, so a group's workgroups share one XCD (and its L2)."""
     budget = max_lds - 54 * 1024  # static: event lists, type tables, own bits
 
-    def fits(R):
-        range_n = -(-(-(-N // R)) // 32) * 32
-        lds = max(K, 1) * tpg * range_n * 8
-        return lds <= budget and tpg * range_n <= 8 * BLOCK, range_n
+    def plan(groups):
+        tpg = -(-B // groups)
+        limit = max(1, n_cu // groups)
 
-    R = max(1, min(limit, -(-N * tpg // BLOCK)))
-    ok, range_n = fits(R)
-    while not ok and R < limit:
-        R += 1
+        def fits(R):
+            range_n = -(-(-(-N // R)) // 32) * 32
+            lds = max(K, 1) * tpg * range_n * 8
+            return lds <= budget and tpg * range_n <= 8 * BLOCK, range_n
+
+        R = max(1, min(limit, -(-N * tpg // BLOCK)))
         ok, range_n = fits(R)
-    if not ok:
-        raise ValueError(f"network too large for one launch (N {N}, batch {B}, {K} pathways)")
-    return groups, -(-N // range_n), range_n
+        while not ok and R < limit:
+            R += 1
+            ok, range_n = fits(R)
+        return (groups, -(-N // range_n), range_n) if ok else None
+
+    groups = max(1, min(MAX_GROUPS, B))
+    while True:
+        if groups > XCDS:
+            groups -= groups % XCDS
+        found = plan(groups)
+        if found is not None:
+            return found
+        if groups == 1:
+            raise ValueError(f"network too large for one launch (N {N}, batch {B}, {K} pathways)")
+        groups = groups // 2  # more workgroups per group for a larger network
 
 
 def _frac_bits(bound: float) -> int:
