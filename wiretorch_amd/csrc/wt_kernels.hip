@@ -3,8 +3,8 @@
 //
 // Forward (wt_cond_run): one persistent launch runs all T steps.
 //   * Workgroups form `groups` groups of R (workgroup i is in group i % groups, slot
-//     i / groups; with 8 groups this is one group per XCD, since the dispatcher places
-//     workgroup i on XCD i % 8). Group g owns trials g, g + groups, ...; slot r owns the
+//     i / groups; with a multiple of 8 groups each group lies on one XCD, since the
+//     dispatcher places workgroup i on XCD i % 8). Group g owns trials g, g + groups, ...; slot r owns the
 //     targets [r * range_n, (r + 1) * range_n) of those trials, for the whole run.
 //   * Step t, per workgroup: (A) update the owned neurons — inject step t-1's
 //     activations, spike, membrane, refractory — and decide their spikes of step t+1,

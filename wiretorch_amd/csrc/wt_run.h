@@ -36,7 +36,7 @@ struct RunArgs {
   // scratch
   uint32_t* err;        // [0]: error flags
   uint32_t* barrier;    // one counter per group, 128 bytes apart
-  uint32_t* bitmap;     // [2][groups][tpg_max][R * words]: which neurons fired
+  uint32_t* bitmap;     // [3][groups][tpg_max][R * words]: which neurons fired
   const int32_t* in_count;  // [B*T]: nonzero inputs of each (trial, step), or > kInCap
   const int32_t* in_idx;    // [B*T][kInCap]
   const float* in_val;      // [B*T][kInCap]
