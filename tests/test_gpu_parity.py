@@ -136,11 +136,14 @@ def _saved_run(drive, p, x, B, N, S):
     return spikes, saved[3]
 
 
-def test_sparse_propagation_is_exactly_rounded():
-    wl = synthetic.fly_scale(N=6000, n_types=300, mean_degree=150, k_max=2000, B=3, T=60,
+# Batches of 3, 20 and 40 trials: 3 groups of one trial, 16 groups of one or two
+# trials, 40 groups of one (whole XCDs past 8 groups)
+@pytest.mark.parametrize("B", [3, 20, 40])
+def test_sparse_propagation_is_exactly_rounded(B):
+    wl = synthetic.fly_scale(N=6000, n_types=300, mean_degree=150, k_max=2000, B=B, T=60,
                              frac_sensory=0.1, rate_hz=200.0, device=DEV)
     x = torch.from_numpy(wl.x).float().to(DEV)
-    spikes, A = _saved_run(wl.drive, wl.physiology, x, 3, wl.N, wl.S)
+    spikes, A = _saved_run(wl.drive, wl.physiology, x, B, wl.N, wl.S)
     assert spikes.sum() > 0
     rec, ff = wl.drive.sparse_recurrent, wl.drive.sparse_feedforward
     for t in range(0, 60, 7):
@@ -157,15 +160,16 @@ def test_sparse_propagation_is_exactly_rounded():
         )
 
 
-def test_sparse_network_matches_oracle():
-    wl = synthetic.fly_scale(N=5000, n_types=200, mean_degree=120, k_max=1500, B=2, T=300,
+@pytest.mark.parametrize("B", [2, 20])  # 2 groups of one trial; 16 of one or two
+def test_sparse_network_matches_oracle(B):
+    wl = synthetic.fly_scale(N=5000, n_types=200, mean_degree=120, k_max=1500, B=B, T=300,
                              frac_sensory=0.1, rate_hz=100.0)
     x = torch.from_numpy(wl.x).float()
-    v, g, counter = synthetic.rest_state(2, wl.N, 2)
+    v, g, counter = synthetic.rest_state(B, wl.N, 2)
     ref = oracle_engine.simulate(v, g, x, wl.drive, wl.physiology, refractory=counter)
     drive_gpu, p_gpu = synthetic.sparse_drive(wl.drive.sparse_recurrent.to(DEV),
                                               wl.drive.sparse_feedforward.to(DEV), wl.N, 0.1, DEV)
-    v, g, counter = synthetic.rest_state(2, wl.N, 2, DEV)
+    v, g, counter = synthetic.rest_state(B, wl.N, 2, DEV)
     out = engine.simulate(v, g, x.to(DEV), drive_gpu, p_gpu, refractory=counter)
     s_ref, s_gpu = ref.spikes.numpy(), out.spikes.cpu().numpy()
     assert s_ref[:, :200].sum() > 0
