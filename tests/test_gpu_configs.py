@@ -158,3 +158,15 @@ def test_learnt_weights_update_reuses_layout(monkeypatch):
     for key, value in g_ref.items():
         scale = np.abs(value).max()
         np.testing.assert_allclose(g_gpu[key], value, rtol=0, atol=1e-4 * scale, err_msg=key)
+    # back on the GPU (new tensors: a new layout), then one synapse fewer: a new nonzero
+    # pattern under the same structure, compressed anew
+    _training_step(wl, x, target, engine, DEV)
+    built.clear()
+    with torch.no_grad():
+        mask = dict(wl.model.named_buffers())["rec_projections.E__E.mask"]
+        flat = mask.view(-1)
+        flat[int(torch.nonzero(flat)[0])] = 0.0
+    s_gpu, _, _ = _training_step(wl, x, target, engine, DEV)
+    assert built, "a changed nonzero pattern kept the old layout"
+    s_ref, _, _ = _training_step(wl, x, target, oracle_engine, "cpu")
+    assert np.array_equal(s_gpu, s_ref)

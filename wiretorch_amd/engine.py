@@ -112,23 +112,25 @@ class _Side:
     dense_shapes: tuple = ()
     max_in_sum: float = 0.0
     #: For a side built from dense pathways: per pathway, its edges (positions in edge
-    #: order) and their flat indices into the pathway's (rows, N) weight matrix.
+    #: order, a slice where they are consecutive) and their flat indices into the
+    #: pathway's (rows, N) weight matrix.
     dense_edges: tuple = ()
     _split: dict = field(default_factory=dict)
     _edge_src: torch.Tensor | None = None
     _by_target: dict = field(default_factory=dict)
 
-    def with_weights(self, weights: torch.Tensor, max_in_sum: float) -> "_Side":
+    def with_weights(self, weights: torch.Tensor) -> "_Side":
         """The same structure with other edge weights; what is derived from the
         structure alone (range splits, edge sources, the by-target order) is shared."""
         c = self.conn
         conn = Connectome(c.n_sources, c.n_targets, c.indptr, c.targets, weights, c.pathway,
                           c.n_pathways)
         side = _Side(conn, self.pathway32, row_local=self.row_local,
-                     dense_shapes=self.dense_shapes, max_in_sum=max_in_sum,
+                     dense_shapes=self.dense_shapes,
                      dense_edges=self.dense_edges, _split=self._split,
                      _by_target=self._by_target)
         side._edge_src = self.edge_src(torch.cuda.current_stream(c.device).cuda_stream)
+        side.max_in_sum = _max_in_sum(conn, self.target_order())
         return side
 
     @property
@@ -181,6 +183,16 @@ class _Side:
             self._by_target[key] = (in_indptr, in_edge)
         return self._by_target[key]
 
+    def target_order(self):
+        """``(indptr, edge)``: every edge grouped by target (for per-target sums)."""
+        if "targets" not in self._by_target:
+            c = self.conn
+            edge = torch.argsort(c.targets, stable=True)
+            indptr = torch.zeros(c.n_targets + 1, dtype=torch.int64, device=c.device)
+            indptr[1:] = torch.cumsum(torch.bincount(c.targets.long(), minlength=c.n_targets), 0)
+            self._by_target["targets"] = (indptr, edge)
+        return self._by_target["targets"]
+
     def abi(self, R: int, range_n: int, stream, weights: torch.Tensor | None = None) -> _lib.Side:
         c = self.conn
         w = c.weights if weights is None else weights
@@ -197,11 +209,21 @@ def _empty_side(device) -> _Side:
     return _Side(conn, torch.zeros(1, dtype=torch.int32, device=device))
 
 
-def _max_in_sum(conn: Connectome) -> float:
+def _max_in_sum(conn: Connectome, order=None) -> float:
+    """The largest per-target sum of |weight|, in float64: by atomic adds, or, given the
+    edges in target order (``_Side.target_order``), as differences of a running sum at
+    the targets' boundaries (no atomics: a few hundred edges share each target)."""
     if conn.n_edges == 0:
         return 0.0
-    per_target = torch.zeros(conn.n_targets, dtype=torch.float64, device=conn.device)
-    per_target.index_add_(0, conn.targets.long(), conn.weights.detach().abs().double())
+    w = conn.weights.detach()
+    if order is None:
+        per_target = torch.zeros(conn.n_targets, dtype=torch.float64, device=conn.device)
+        per_target.index_add_(0, conn.targets.long(), w.abs().double())
+    else:
+        indptr, edge = order
+        running = torch.zeros(conn.n_edges + 1, dtype=torch.float64, device=conn.device)
+        torch.cumsum(w[edge].abs().double(), 0, out=running[1:])
+        per_target = running[indptr[1:]] - running[indptr[:-1]]
     return float(per_target.max())
 
 
@@ -243,32 +265,27 @@ def _from_pathways(pathways, n_src: int, N: int, device) -> _Side:
     conn = from_dense(W_all, pathway, len(pathways))
     side = _Side(conn, pathway.to(torch.int32), row_local=row_local,
                  dense_shapes=tuple(shapes))
-    side.max_in_sum = _dense_in_sum(pathways)
+    side.max_in_sum = _max_in_sum(conn, side.target_order())
+    none = torch.zeros(0, dtype=torch.int64, device=device)
+    edges = [(none, none)] * len(pathways)
     if conn.n_edges:
         edge_src = side.edge_src(torch.cuda.current_stream(device).cuda_stream)
         k_of_edge = conn.pathway[edge_src]
-        edges = []
         for k in range(len(pathways)):
             e = torch.nonzero(k_of_edge == k).flatten()
-            edges.append((e, row_local[edge_src[e]] * N + conn.targets[e].long()))
-        side.dense_edges = tuple(edges)
+            flat = row_local[edge_src[e]] * N + conn.targets[e].long()
+            if e.numel() and int(e[-1]) - int(e[0]) + 1 == e.numel():
+                e = slice(int(e[0]), int(e[-1]) + 1)  # a pathway of consecutive sources
+            edges[k] = (e, flat)
+    side.dense_edges = tuple(edges)
     return side
-
-
-def _dense_in_sum(pathways) -> float:
-    """The largest per-target sum of |weight| over the dense pathways (float64 sums)."""
-    total = None
-    for _, W in pathways:
-        col = torch.sum(W.detach().float().abs(), dim=0, dtype=torch.float64)
-        total = col if total is None else total + col
-    return float(total.max()) if total is not None and total.numel() else 0.0
 
 
 _CACHE: OrderedDict = OrderedDict()
 _CACHE_SIZE = 32
-#: Sides of dense pathways by structure (source rows and shapes), with the nonzero
-#: pattern of each pathway they were built from: a side whose weights changed but whose
-#: pattern did not (learnt weights) takes the new values without being compressed again.
+#: Sides of dense pathways by structure (source rows and shapes): a side whose weights
+#: changed but whose nonzero pattern did not (learnt weights) takes the new values
+#: without being compressed again.
 _LAYOUTS: OrderedDict = OrderedDict()
 _LAYOUTS_SIZE = 4
 
@@ -312,16 +329,22 @@ def _dense_side(pathways, n_src: int, N: int, device) -> tuple[_Side, bool]:
         for rows, W in pathways)
     hit = _LAYOUTS.get(key)
     if hit is not None:
-        base, masks, _keep = hit
-        if all(torch.equal(W.detach() != 0, m) for (_, W), m in zip(pathways, masks)):
+        base, _keep = hit
+        weights = torch.empty_like(base.conn.weights)
+        off = []
+        for (_, W), (e, flat) in zip(pathways, base.dense_edges):
+            W = W.detach().to(device, torch.float32).reshape(-1)
+            values = W[flat]
+            weights[e] = values
+            # the pattern is the layout's when W has as many nonzeros as the layout has
+            # edges and is nonzero at each of them (one read of W, no stored mask)
+            off.append(torch.count_nonzero(W) - flat.numel())
+            off.append(torch.count_nonzero(values == 0))
+        if not off or not bool(torch.stack(off).any()):
             _LAYOUTS.move_to_end(key)
-            weights = torch.empty_like(base.conn.weights)
-            for (_, W), (e, flat) in zip(pathways, base.dense_edges):
-                weights[e] = W.detach().to(device, torch.float32).reshape(-1)[flat]
-            return base.with_weights(weights, _dense_in_sum(pathways)), True
+            return base.with_weights(weights), True
     side = _from_pathways(pathways, n_src, N, device)
-    masks = tuple((W.detach() != 0).to(device) for _, W in pathways)
-    _LAYOUTS[key] = (side, masks, tuple(rows for rows, _ in pathways))
+    _LAYOUTS[key] = (side, tuple(rows for rows, _ in pathways))
     while len(_LAYOUTS) > _LAYOUTS_SIZE:
         _LAYOUTS.popitem(last=False)
     return side, False
