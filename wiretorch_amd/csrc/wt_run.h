@@ -732,10 +732,13 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     // ---------------- publish step t+1's spikes ----------------
     const bool publish = recurrent && more;
     if (publish) {
+      // each word's place recomputed here in 32 bits (hoisted out of the step loop, its
+      // first value was spilled to scratch and reloaded before the stores every step)
       uint32_t* out_bits = group_bits + (buf == 2 ? 0 : buf + 1) * buffer_words;
-      for (int64_t w = threadIdx.x; w < tpg * words; w += blockDim.x) {
-        const int64_t q = w / words;
-        store_agent(out_bits + q * total_words + r * words + (w - q * words), s_bits[w]);
+      for (uint32_t w = opaque(threadIdx.x); w < (uint32_t)(tpg * words); w += blockDim.x) {
+        const uint32_t q = w / (uint32_t)words;
+        store_agent(out_bits + (int64_t)q * total_words + r * words + (w - q * words),
+                    s_bits[w]);
       }
     }
 
@@ -813,9 +816,10 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       for (int u = 0; u < MAXI; ++u) rest_bits[u] = 0u;
       if (rest) {  // every word read at once (an index past the group's words is clamped)
 #pragma unroll
-        for (int u = 0; u < MAXI; ++u) {
-          const int64_t w = threadIdx.x + (int64_t)u * blockDim.x;
-          rest_bits[u] = load_agent(in_bits + (w < group_words ? w : group_words - 1));
+        for (int u = 0; u < MAXI; ++u) {  // (32-bit indexes, recomputed: not kept live)
+          const uint32_t w = opaque(threadIdx.x) + (uint32_t)u * blockDim.x;
+          const uint32_t last = (uint32_t)group_words - 1u;
+          rest_bits[u] = load_agent(in_bits + (w < last ? w : last));
         }
 #pragma unroll
         for (int u = 0; u < MAXI; ++u) {
