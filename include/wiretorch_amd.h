@@ -131,7 +131,10 @@ int wt_cond_run(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
  * fired sources, 2 range lookups + its own neuron update, 3 the wait for the rest of the
  * workgroup's update, 4 publication + unlisted events + barrier arrival, 5 barrier wait,
  * 6 appends to the event list, 7 scan + synapse push (+ further rounds). For profiling;
- * no counterpart in the reference. timing: (groups * R * 8) u64. */
+ * no counterpart in the reference. timing: (groups * R * 8) u64. Lean runs only: with
+ * saved tensors, probabilities or tracking it returns hipErrorInvalidValue; it always
+ * takes the 1024-entry event list (results do not depend on it). The timer is compiled
+ * into kernels of their own, so that wt_cond_run's carry no check of it. */
 int wt_cond_run_timed(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
                       const wt_geometry* geo, const wt_run_io* io, void* scratch,
                       uint64_t* timing, wt_stream_t stream);

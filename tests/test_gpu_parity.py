@@ -262,3 +262,21 @@ def test_recurrent_gradients_on_gpu(case):
     sc.use_engine(built.model, oracle_engine)
     _, g_plain = sc.gradients(built, device="cpu")
     assert any(not np.allclose(g_plain[k], g_cpu[k], rtol=1e-3, atol=1e-6) for k in g_cpu)
+
+
+def test_phase_timer_leaves_the_run_unchanged():
+    """``wt_cond_run_timed`` (its own kernels, the timer compiled in) gives the raster of
+    ``wt_cond_run`` and ticks in every workgroup."""
+    wl = synthetic.fly_scale(N=5000, n_types=200, mean_degree=120, k_max=1500, B=2, T=100,
+                             frac_sensory=0.1, rate_hz=100.0, device=DEV)
+    x = torch.from_numpy(wl.x).float().to(DEV)
+    v, g, counter = synthetic.rest_state(2, wl.N, 2, DEV)
+    plain = engine.simulate(v, g, x, wl.drive, wl.physiology, refractory=counter)
+    engine.PHASE_TIMING = []
+    try:
+        timed = engine.simulate(v, g, x, wl.drive, wl.physiology, refractory=counter)
+        ticks = engine.PHASE_TIMING[0]
+    finally:
+        engine.PHASE_TIMING = None
+    assert plain.spikes.sum() > 0 and torch.equal(plain.spikes, timed.spikes)
+    assert ticks.shape[1] == engine.PHASES and bool((ticks.sum(dim=1) > 0).all())

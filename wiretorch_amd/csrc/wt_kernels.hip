@@ -437,8 +437,8 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
   const int64_t per_thread = (tpg * geo->range_n + kRunBlock - 1) / kRunBlock;
   // the kMaxList-entry list where the accumulator leaves room for it (and the workgroup
   // has at most kBigMaxi items per thread); else kRunBlock entries
-  int32_t cap = kRunBlock;
-  if (per_thread <= kBigMaxi && (geo->max_list == 0 || geo->max_list >= kMaxList) &&
+  int32_t cap = kRunBlock;  // (a timed launch keeps it: its kernels have this list only)
+  if (!timing && per_thread <= kBigMaxi && (geo->max_list == 0 || geo->max_list >= kMaxList) &&
       static_lds + (size_t)list_bytes(kMaxList) + lds <= (size_t)max_lds)
     cap = kMaxList;
   if (static_lds + (size_t)list_bytes(cap) + lds > (size_t)max_lds) return hipErrorInvalidValue;

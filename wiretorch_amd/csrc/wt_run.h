@@ -174,8 +174,9 @@ __device__ inline void push_edges(double* row, const int32_t* targets, const flo
 
 // Phase timer (wt_cond_run_timed): s_time[0 .. kPhases) accumulate wall-clock ticks,
 // s_time[kPhases] holds the last reading.
+template <bool TIMED>
 __device__ inline void tick(uint64_t* s_time, int phase) {
-  if (threadIdx.x == 0 && kargs()->timing) {
+  if (TIMED && threadIdx.x == 0) {
     const uint64_t now = wall_clock64();
     s_time[phase] += now - s_time[kPhases];
     s_time[kPhases] = now;
@@ -327,7 +328,7 @@ __device__ inline void run_events(const EventList& L, int m, int32_t total, doub
 // the whole launch.
 // BIG: the event list holds kMaxList entries, otherwise kRunBlock (static LDS, fixed
 // addresses either way; the host takes BIG where the accumulator leaves room).
-template <int S, int MAXI, bool EXTRA, bool REFR, bool BIG>
+template <int S, int MAXI, bool EXTRA, bool REFR, bool BIG, bool TIMED>
 __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   static_assert(MAXI <= 8, "the overflow note holds one bit per preloaded word");
   extern __shared__ __align__(16) double acc[];  // [K][tpg][range_n]
@@ -499,7 +500,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     if (recurrent) {
       if (!barrier_wait(my_barrier, phase * (uint32_t)R, A.err, &s_flag)) return;
     }
-    tick(s_time, 5);
+    tick<TIMED>(s_time, 5);
     uint32_t pre[MAXI];
 #pragma unroll
     for (int u = 0; u < MAXI; ++u) {
@@ -518,7 +519,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       in_j = gload(P->in_idx + slot);
       in_v = gload(P->in_val + slot);
     }
-    tick(s_time, 0);
+    tick<TIMED>(s_time, 0);
 
     // ---------------- events of step t, listed before the update ----------------
     // The fired bits of the preloaded words are compacted into s_fired (source | trial
@@ -563,7 +564,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       }
     }
     __syncthreads();
-    tick(s_time, 1);
+    tick<TIMED>(s_time, 1);
     int64_t re0 = 0, re1 = 0, ie0 = 0, ie1 = 0;
     int32_t rk = -1, ik = -1;
     uint32_t rj = 0;
@@ -725,9 +726,9 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
         rkb = gload(P->rec.pathway + (rjb & 0xffffffu));
       }
     }
-    tick(s_time, 2);
+    tick<TIMED>(s_time, 2);
     __syncthreads();  // the accumulator is read and cleared; the next bits are complete
-    tick(s_time, 3);
+    tick<TIMED>(s_time, 3);
 
     // ---------------- publish step t+1's spikes ----------------
     const bool publish = recurrent && more;
@@ -797,7 +798,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     } else {
       __syncthreads();
     }
-    tick(s_time, 4);
+    tick<TIMED>(s_time, 4);
     // the next step's own bits and fired list start empty (their readers are done)
     for (int64_t w = threadIdx.x; w < tpg * words; w += blockDim.x) s_bits[w] = 0;
     if (threadIdx.x == 0) s_nfired = 0;
@@ -946,7 +947,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
         // round's push, is behind a barrier; its next writer after the one below)
         for (int w = threadIdx.x; w < nbk; w += blockDim.x) s_heads[w] = 0;
         __syncthreads();
-        tick(s_time, 6);
+        tick<TIMED>(s_time, 6);
         const int n_ev = s_nev;
         const int m = n_ev < cap ? n_ev : cap;
         if (m > 0) {  // m is uniform: every thread takes part in the scan
@@ -986,7 +987,7 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
     }
     __syncthreads();  // the accumulator is complete for the next update
     if (threadIdx.x == 0) s_nev = 0;  // every thread has read it; its next use is behind barriers
-    tick(s_time, 7);
+    tick<TIMED>(s_time, 7);
   }
 
   // The activations of the last step enter the conductances that leave the chunk.
@@ -1040,18 +1041,20 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
       A.io.g[(b * 2 * S + S + s) * N + n] = gd[i][s];
     }
   }
-  if (A.timing && threadIdx.x < kPhases) A.timing[wg * kPhases + threadIdx.x] = s_time[threadIdx.x];
+  if (TIMED && threadIdx.x < kPhases) A.timing[wg * kPhases + threadIdx.x] = s_time[threadIdx.x];
 }
 
-template <int S, int MAXI, bool EXTRA, bool REFR, bool BIG>
+template <int S, int MAXI, bool EXTRA, bool REFR, bool BIG, bool TIMED = false>
 inline hipError_t launch_one(RunArgs& a, size_t lds, hipStream_t stream, bool coop) {
-  const void* fn = reinterpret_cast<const void*>(&cond_run_kernel<S, MAXI, EXTRA, REFR, BIG>);
+  const void* fn =
+      reinterpret_cast<const void*>(&cond_run_kernel<S, MAXI, EXTRA, REFR, BIG, TIMED>);
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   dim3 grid((unsigned)(a.geo.groups * a.geo.R)), blk((unsigned)kRunBlock);
   void* params[] = {&a};
   if (coop) return hipLaunchCooperativeKernel(fn, grid, blk, params, (unsigned)lds, stream);
-  hipLaunchKernelGGL((cond_run_kernel<S, MAXI, EXTRA, REFR, BIG>), grid, blk, lds, stream, a);
+  hipLaunchKernelGGL((cond_run_kernel<S, MAXI, EXTRA, REFR, BIG, TIMED>), grid, blk, lds, stream,
+                     a);
   return hipGetLastError();
 }
 
@@ -1059,6 +1062,11 @@ template <int S, int MAXI, bool BIG>
 inline hipError_t launch_flags(RunArgs& a, size_t lds, hipStream_t stream, bool coop) {
   const bool extra = a.io.prob || a.io.v_saved || a.io.A_saved || a.io.track_v || a.io.track_g;
   const bool refr = a.tab.n_ref != nullptr;
+  if (a.timing) {  // timed kernels: lean outputs and the 1024-entry list only
+    if (extra || BIG) return hipErrorInvalidValue;
+    return refr ? launch_one<S, MAXI, false, true, false, true>(a, lds, stream, coop)
+                : launch_one<S, MAXI, false, false, false, true>(a, lds, stream, coop);
+  }
   if (extra)
     return refr ? launch_one<S, MAXI, true, true, BIG>(a, lds, stream, coop)
                 : launch_one<S, MAXI, true, false, BIG>(a, lds, stream, coop);

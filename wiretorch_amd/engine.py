@@ -72,7 +72,8 @@ class _timed:
             stop.record()
             PART_EVENTS.setdefault(self.name, []).append((self.start, stop))
 #: When a list, launches run ``wt_cond_run_timed`` and append the per-workgroup phase
-#: ticks ``(groups * R, 8)`` (profiling only; the phases are listed with the entry point).
+#: ticks ``(groups * R, 8)`` (profiling only, forwards without saved tensors,
+#: probabilities or tracking; the phases are listed with the entry point).
 PHASE_TIMING: list | None = None
 #: Phase slots per workgroup that ``wt_cond_run_timed`` writes.
 PHASES = 8
@@ -579,6 +580,9 @@ def _launch(L: _Plan, x, scale, v, g, counter, spikes, prob, saved, tracked,
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
     if PHASE_TIMING is not None:
+        if prob is not None or saved is not None or tracked is not None:
+            raise NotImplementedError("phase timing times forwards without saved tensors, "
+                                      "probabilities or tracking")
         ticks = torch.zeros((groups * R, PHASES), dtype=torch.int64, device=L.device)
         _lib.check(lib.wt_cond_run_timed(tab, rec, ff, geo, io, scratch.data_ptr(),
                                          ticks.data_ptr(), L.stream), "wt_cond_run_timed")
