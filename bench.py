@@ -391,6 +391,68 @@ def bench_config4(args):
     print(json.dumps(line), flush=True)
 
 
+def bench_filter(args):
+    """The spike-train losses' double-exponential filter (forward + backward) on spike
+    trains of config 3's training shape: 64 trials x 500 steps x 10,000 neurons."""
+    from wiretorch_amd.filtering import VanRossumLoss, double_exponential
+
+    dev = torch.device("cuda:0")
+    B, T, N = 64, (args.T if args.T != 2000 else 500), 10_000
+    gen = torch.Generator(device=dev).manual_seed(0)
+    x = (torch.rand((B, T, N), device=dev, generator=gen) < 0.002).float().requires_grad_(True)
+    g = torch.randn((B, T, N), device=dev, generator=gen)
+    loss = VanRossumLoss(5.0, 20.0, 0.1, T, device=dev)
+    kernels = loss.kernel_rise, loss.kernel_decay
+    fwd, bwd = [], []
+    for i in range(args.warmup + args.steps):
+        if i == args.warmup:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        e[0].record()
+        _, smooth = double_exponential(x, *kernels, None, None)
+        e[1].record()
+        e[2].record()
+        (grad,) = torch.autograd.grad(smooth, x, g)
+        e[3].record()
+        if i >= args.warmup:
+            fwd.append((e[0], e[1]))
+            bwd.append((e[2], e[3]))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    parts = _part_ms({"forward": fwd, "backward": bwd})
+    ms_per_step = wall * 1e3 / args.steps
+    elems = B * T * N
+    bytes_fwd, bytes_bwd = 12 * elems, 8 * elems  # x in, rise + smooth out; g in, dL/dx out
+    achieved = bytes_fwd / (parts["forward"] / 1e3) / 1e9
+    print(f"# filter: forward {parts['forward']:.3f} ms ({achieved:.0f} GB/s), backward "
+          f"{parts['backward']:.3f} ms ({bytes_bwd / parts['backward'] / 1e6:.0f} GB/s)",
+          file=sys.stderr, flush=True)
+    cpu = None
+    if args.cpu_steps > 0:
+        import oracle.filtering as of
+
+        steps = min(args.cpu_steps, T)
+        xs = x.detach()[:, :steps].cpu().numpy()
+        gs = g[:, :steps].cpu().numpy()
+        a_r, a_d = float(kernels[0][1]), float(kernels[1][1])
+        c0 = time.perf_counter()
+        of.forward(xs, a_r, a_d)
+        of.backward(gs, a_r, a_d)
+        elapsed = time.perf_counter() - c0
+        cpu = {"value": B * N * steps / elapsed, "unit": "neuron-steps/s", "cores": 1,
+               "kind": "port", "sample": f"oracle forward + backward of the first {steps} of "
+                                         f"{T} steps, all {B} trials ({elapsed:.1f} s)"}
+    _line(elems / (ms_per_step / 1e3), ms_per_step, args, "f32",
+          {"workload": "double-exponential spike-train filter, forward + backward",
+           "neurons": N, "batch": B, "time_steps": T, "tau_rise_ms": 5.0,
+           "tau_decay_ms": 20.0, "dt_ms": 0.1, "parallelism": "single GPU"},
+          {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "wt_filter_forward",
+           "kernel_ms": parts["forward"], "algorithmic_bytes_per_launch": bytes_fwd},
+          cpu, per_part_ms=parts)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -399,6 +461,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=int(os.environ.get("BENCH_CPU_STEPS", 400)))
     ap.add_argument("--T", type=int, default=2000)
     ap.add_argument("--config", type=int, choices=(1, 2, 3, 4), default=2)
+    ap.add_argument("--filter", action="store_true",
+                    help="measure the spike-train loss filter instead of a configuration")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run one device-to-device copy of this many bytes (the "
                          "reference kernel for calibrating rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -416,6 +480,10 @@ def main():
               "(the hot path runs on a single GPU)", file=sys.stderr)
         sys.exit(2)
     default_cpu = "--cpu-steps" not in sys.argv and "BENCH_CPU_STEPS" not in os.environ
+    if args.filter:
+        if default_cpu:
+            args.cpu_steps = 500
+        return bench_filter(args)
     if args.config == 4:
         if default_cpu:
             args.cpu_steps = 100

@@ -310,6 +310,23 @@ int wt_weight_gradient(const wt_side* side, const int64_t* edge_src, int64_t n_e
                        const float* grad_A, int64_t B, int64_t T, int64_t N,
                        int64_t pathway_offset, float* grad_w, wt_stream_t stream);
 
+/* wt_filter_forward — the causal double-exponential filter of spike trains, replacing
+ * _DoubleExponential.forward / _filter_forward (training_utils/filtering.py:75-86,103-123).
+ * x, rise, smooth (B, T, N) f32 contiguous; carried_rise, carried_smooth (B, N) f32 or NULL
+ * (zero). rise[t] = a_rise rise[t-1] + x[t], smooth[t] = a_decay smooth[t-1] + rise[t], the
+ * carried state entering undecayed at t = 0; each multiply and add rounded separately.
+ * B, T, N below 2^32. */
+int wt_filter_forward(const float* x, const float* carried_rise, const float* carried_smooth,
+                      float* rise, float* smooth, float a_rise, float a_decay, int64_t B,
+                      int64_t T, int64_t N, wt_stream_t stream);
+
+/* wt_filter_backward — its reverse recursion, replacing _DoubleExponential.backward /
+ * _filter_backward (training_utils/filtering.py:88-97,125-135): gs = g[t] + a_decay gs,
+ * gr = gs + a_rise gr, grad_x[t] = gr, for t = T-1 .. 0. grad_smooth, grad_x (B, T, N) f32
+ * contiguous. No gradient flows into the carried states or through rise. */
+int wt_filter_backward(const float* grad_smooth, float* grad_x, float a_rise, float a_decay,
+                       int64_t B, int64_t T, int64_t N, wt_stream_t stream);
+
 /* wt_weight_gradient_by_target — the same sums (in a fixed order of their own: a
  * wave's 64 lanes over consecutive events, then a tree), grouped by (pathway, target)
  * row: grad_A (n_pathways, BT, N) is the side's dL/da, first transposed into rows

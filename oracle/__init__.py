@@ -16,4 +16,8 @@ Modules:
 * ``oracle.sparse`` — the compressed-connectome propagation used at fly scale, where
   the reference's dense per-pathway rows cannot be built. Pinned against the dense
   product on small networks (``tests/test_oracle_sparse.py``).
+* ``oracle.filtering`` — the spike-train losses' double-exponential filter and its
+  reverse (``src/wiretorch/training_utils/filtering.py:103-135``). Pinned against the
+  reference tests' literal-sum definition, an impulse's closed form and the adjoint
+  identity (``tests/test_filter_oracle.py``).
 """

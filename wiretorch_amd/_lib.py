@@ -117,6 +117,10 @@ SIGNATURES = {
                                           I64, I64, I64, P, P]),
     "wt_weight_gradient_by_target": (ctypes.c_int, [P, I64, P, P, I64, I64, P, P, P, P, I64,
                                                     P, P, P]),
+    "wt_filter_forward": (ctypes.c_int, [P, P, P, P, P, ctypes.c_float, ctypes.c_float, I64,
+                                         I64, I64, P]),
+    "wt_filter_backward": (ctypes.c_int, [P, P, ctypes.c_float, ctypes.c_float, I64, I64, I64,
+                                          P]),
     "wt_device_info": (ctypes.c_int, [ctypes.POINTER(I64), ctypes.POINTER(I64)]),
 }  # fmt: skip
 
