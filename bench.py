@@ -60,10 +60,10 @@ def delivered_events(spikes, x, drive):
     return float(per_src @ out_rec + per_in @ out_ff)
 
 
-def measured_traffic():
-    """HBM bytes per launch of wt_cond_run on this workload, from the committed rocprofv3
+def measured_traffic(summary="wt_cond_run_config2_traffic.md"):
+    """HBM bytes per launch of a kernel on its workload, from the committed rocprofv3
     FETCH_SIZE + WRITE_SIZE summary (calibrated against a copy of known size), or None."""
-    path = ROOT / "profiles" / "wt_cond_run_config2_traffic.md"
+    path = ROOT / "profiles" / summary
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
@@ -448,7 +448,9 @@ def bench_filter(args):
            "neurons": N, "batch": B, "time_steps": T, "tau_rise_ms": 5.0,
            "tau_decay_ms": 20.0, "dt_ms": 0.1, "parallelism": "single GPU"},
           {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-           "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "wt_filter_forward",
+           "frac": achieved / HBM_PEAK_GBS,
+           "traffic": measured_traffic("wt_filter_config3_shape_traffic.md") if T == 500 else None,
+           "kernel": "wt_filter_forward",
            "kernel_ms": parts["forward"], "algorithmic_bytes_per_launch": bytes_fwd},
           cpu, per_part_ms=parts)
 
