@@ -315,7 +315,7 @@ int wt_weight_gradient(const wt_side* side, const int64_t* edge_src, int64_t n_e
  * x, rise, smooth (B, T, N) f32 contiguous; carried_rise, carried_smooth (B, N) f32 or NULL
  * (zero). rise[t] = a_rise rise[t-1] + x[t], smooth[t] = a_decay smooth[t-1] + rise[t], the
  * carried state entering undecayed at t = 0; each multiply and add rounded separately.
- * B, T, N below 2^32. */
+ * B, N below 2^32, T below 2^32 - 8. */
 int wt_filter_forward(const float* x, const float* carried_rise, const float* carried_smooth,
                       float* rise, float* smooth, float a_rise, float a_decay, int64_t B,
                       int64_t T, int64_t N, wt_stream_t stream);

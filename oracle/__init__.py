@@ -15,7 +15,8 @@ Modules:
   lockstep, free run, gradients), see ``tests/test_oracle_fixtures.py``.
 * ``oracle.sparse`` — the compressed-connectome propagation used at fly scale, where
   the reference's dense per-pathway rows cannot be built. Pinned against the dense
-  product on small networks (``tests/test_oracle_sparse.py``).
+  product on small networks (``tests/test_oracle_pinning.py``,
+  ``test_sparse_activations_equal_the_dense_product``).
 * ``oracle.filtering`` — the spike-train losses' double-exponential filter and its
   reverse (``src/wiretorch/training_utils/filtering.py:103-135``). Pinned against the
   reference tests' literal-sum definition, an impulse's closed form and the adjoint

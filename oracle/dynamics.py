@@ -16,6 +16,18 @@ bit for bit (same torch CPU kernels, same association order):
 
 A drive given in compressed form (``sparse_recurrent`` / ``sparse_feedforward``)
 propagates through ``oracle.sparse.activations`` instead of the dense products.
+
+``SUMS`` picks how a dense pathway's product ``s[:, rows] @ W`` is summed:
+
+* ``"float32"`` (default) — torch CPU's float32 matrix product, the reference's own
+  call; its rounding depends on the BLAS's blocking, and the reference's recorded
+  fixtures were made with it;
+* ``"exact"`` — the same products summed in float64 and rounded to float32 once: for
+  0/1 spikes times float32 weights the exactly rounded sum (float64 holds every partial
+  sum of a few thousand float32 weights within 2^29 of each other exactly), the value
+  ``oracle.sparse`` computes and the GPU kernels compute. Parity tests at sizes where
+  float32 BLAS rounding alone flips spikes use it (gradients then flow through the float64
+  product, rounded to float32).
 """
 
 from __future__ import annotations
@@ -87,10 +99,22 @@ def membrane(v, s, g, p):
     return v_next, I, I_leak
 
 
+SUMS = "float32"
+
+
+def product(a, W):
+    """``a @ W`` for a dense pathway, summed as ``SUMS`` says."""
+    if SUMS == "exact":
+        return (a.double() @ W.double()).float()
+    if SUMS != "float32":
+        raise ValueError(f"SUMS must be 'float32' or 'exact', got {SUMS!r}")
+    return a @ W
+
+
 def recurrent_activations(drive, s):
     if drive.sparse_recurrent is not None:
         return list(_sparse.activations(drive.sparse_recurrent, s))
-    return [s[:, rows] @ W for rows, W in drive.recurrent]
+    return [product(s[:, rows], W) for rows, W in drive.recurrent]
 
 
 def feedforward_activations(drive, x):
@@ -99,7 +123,12 @@ def feedforward_activations(drive, x):
         B, T, n_in = x.shape
         A = _sparse.activations(drive.sparse_feedforward, x.reshape(B * T, n_in))
         return A.reshape(A.shape[0], B, T, -1)
-    return drive.feedforward_activations(x)
+    if SUMS == "float32":
+        return drive.feedforward_activations(x)
+    B, T = x.shape[:2]
+    if not drive.feedforward:
+        return x.new_zeros((0, B, T, 0))
+    return torch.stack([product(x[:, :, rows], W) for rows, W in drive.feedforward])
 
 
 def stack_steps(tensors):

@@ -196,6 +196,35 @@ def test_sparse_activations_equal_the_dense_product(seed):
         np.testing.assert_array_equal(got[k].numpy(), expected.astype(np.float32))
 
 
+@pytest.mark.parametrize("seed", [0, 1])
+def test_exact_dense_product_is_the_exactly_rounded_sum(seed, monkeypatch):
+    """``oracle.dynamics.product`` with ``SUMS = "exact"``: each entry equals the
+    exactly rounded sum of its terms — ``math.fsum`` (exact, then rounded once) on a
+    brute-force loop — and the event-by-event ``oracle.sparse`` propagation bit for bit,
+    on lognormal weights like the configurations'; the float32 product stays within its
+    own error bound of it."""
+    import math
+
+    import oracle.dynamics as od
+
+    monkeypatch.setattr(od, "SUMS", "exact")
+    rng = np.random.default_rng(seed)
+    n_src, n_tgt, B = 300, 40, 4
+    W = (rng.lognormal(-1.0, 1.0, (n_src, n_tgt)) * (rng.random((n_src, n_tgt)) < 0.2))
+    W = W.astype(np.float32)
+    s = (rng.random((B, n_src)) < 0.3).astype(np.float32)
+    got = od.product(torch.from_numpy(s), torch.from_numpy(W)).numpy()
+    for b in range(B):
+        for n in range(n_tgt):
+            terms = [float(W[j, n]) for j in range(n_src) if s[b, j]]
+            assert got[b, n] == np.float32(math.fsum(terms)), (b, n)
+    conn = connectome.from_dense(torch.from_numpy(W), torch.zeros(n_src, dtype=torch.int64), 1)
+    np.testing.assert_array_equal(oracle_sparse.activations(conn, torch.from_numpy(s))[0].numpy(), got)
+    f32 = torch.from_numpy(s) @ torch.from_numpy(W)
+    bound = n_src * np.finfo(np.float32).eps * (s @ np.abs(W))
+    assert np.all(np.abs(f32.numpy().astype(np.float64) - got) <= bound + np.abs(got) * 2**-24)
+
+
 # ---------------------------------------------------------------------------------
 # The rate oracle's reduced-precision product (oracle/rate.py)
 # ---------------------------------------------------------------------------------

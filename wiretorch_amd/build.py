@@ -36,8 +36,17 @@ def _filter(stderr: str) -> str:
     return "\n".join(l for l in stderr.splitlines() if noise not in l)
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile every source to an object (in parallel), then link the shared library."""
+def _stale(src: Path, obj: Path) -> bool:
+    """Whether ``obj`` is older than its source or any header it may include."""
+    if not obj.exists():
+        return True
+    headers = list(CSRC.glob("*.h")) + list((PACKAGE.parent / "include").glob("*.h"))
+    return obj.stat().st_mtime < max(p.stat().st_mtime for p in [src, *headers])
+
+
+def build(verbose: bool = False, jobs: int | None = None, changed_only: bool = False) -> Path:
+    """Compile every source to an object (in parallel), then link the shared library.
+    ``changed_only``: recompile only objects older than their sources or the headers."""
     OBJ_DIR.mkdir(exist_ok=True)
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 1, 16)
     procs = []
@@ -45,6 +54,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     for src in SOURCES:
         obj = OBJ_DIR / (src.stem + ".o")
         objects.append(obj)
+        if changed_only and not _stale(src, obj):
+            continue
         cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
@@ -72,4 +83,4 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, changed_only="--changed" in sys.argv))

@@ -145,9 +145,10 @@ static bool wide(int64_t N, std::initializer_list<const void*> ptrs) {
 }
 
 static bool sizes_ok(int64_t B, int64_t T, int64_t N) {
-  // 32-bit B, T, N; the flat element index stays in 64 bits
-  return B >= 0 && T >= 0 && N >= 0 && B <= UINT32_MAX && T <= UINT32_MAX && N <= UINT32_MAX &&
-         B * N <= (int64_t)UINT32_MAX * BLOCK;
+  // 32-bit B, T, N; the flat element index stays in 64 bits. The forward's chunked loop
+  // tests t + CH <= T in 32 bits, so T stays CH below the 32-bit limit (no wrap-around).
+  return B >= 0 && T >= 0 && N >= 0 && B <= UINT32_MAX && T <= (int64_t)UINT32_MAX - CH &&
+         N <= UINT32_MAX && B * N <= (int64_t)UINT32_MAX * BLOCK;
 }
 
 }  // namespace filter
@@ -158,7 +159,7 @@ extern "C" int wt_filter_forward(const float* x, const float* carried_rise,
                                  float a_rise, float a_decay, int64_t B, int64_t T, int64_t N,
                                  wt_stream_t stream) {
   if (!wt::filter::sizes_ok(B, T, N)) return hipErrorInvalidValue;
-  if (B * T * N == 0) return hipSuccess;
+  if (B == 0 || T == 0 || N == 0) return hipSuccess;
   if (!x || !rise || !smooth) return hipErrorInvalidValue;
   const bool v4 = wt::filter::wide(N, {x, rise, smooth, carried_rise, carried_smooth});
   const int64_t cols = B * N / (v4 ? 4 : 1);
@@ -178,7 +179,7 @@ extern "C" int wt_filter_backward(const float* grad_smooth, float* grad_x, float
                                   float a_decay, int64_t B, int64_t T, int64_t N,
                                   wt_stream_t stream) {
   if (!wt::filter::sizes_ok(B, T, N)) return hipErrorInvalidValue;
-  if (B * T * N == 0) return hipSuccess;
+  if (B == 0 || T == 0 || N == 0) return hipSuccess;
   if (!grad_smooth || !grad_x) return hipErrorInvalidValue;
   const bool v4 = wt::filter::wide(N, {grad_smooth, grad_x});
   const int64_t cols = B * N / (v4 ? 4 : 1);

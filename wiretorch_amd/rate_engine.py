@@ -291,8 +291,10 @@ def _split(x: torch.Tensor):
 
 def _split_product(a_hi, a_lo, b_hi, b_lo) -> torch.Tensor:
     """``a^T b`` of float32 matrices given as bf16 (hi, lo) pairs: hi.hi + hi.lo + lo.hi on
-    the matrix cores, float32 accumulation and output (the lo.lo term is below float32's
-    rounding of the sum)."""
+    the matrix cores, float32 accumulation and output. Each operand is hi + lo to 2^-18
+    relative and the dropped lo.lo is below 2^-18 of the product, so each product is off
+    by at most 3 * 2^-18 of |a_i b_i| (float32's product: 2^-24) before the float32
+    accumulation, which both products share."""
     C = torch.mm(a_hi.T, b_hi, out_dtype=torch.float32)
     C = torch.addmm(C, a_hi.T, b_lo, out_dtype=torch.float32)
     return torch.addmm(C, a_lo.T, b_hi, out_dtype=torch.float32)
@@ -304,10 +306,14 @@ def _weight_and_input_grads(L: _Plan, out, x, grad_A, weights, w_needs, want_x):
     B, T, N = L.B, L.T, L.N
     grad_w = [None] * len(weights)
     for k, rows in enumerate(L.rows_rec):
-        if w_needs[k]:
-            r_hi, r_lo = _split(_columns(out, rows).reshape(B * T, -1))
-            g_hi, g_lo = _split(grad_A[k].reshape(B * T, N))
-            grad_w[k] = _split_product(r_hi, r_lo, g_hi, g_lo)
+        if not w_needs[k]:
+            continue
+        pre = _columns(out, rows).reshape(B * T, -1)
+        g = grad_A[k].reshape(B * T, N)
+        if L.op.dtype == torch.float32:  # the reference's precision: its float32 product
+            grad_w[k] = pre.T @ g
+        else:  # reduced-precision storage: the split product on the bf16 matrix cores
+            grad_w[k] = _split_product(*_split(pre), *_split(g))
     grad_x = torch.zeros_like(x, dtype=torch.float32) if want_x else None
     for j, (rows, W) in enumerate(zip(L.rows_ff, weights[L.K_rec:])):
         k = L.K_rec + j
