@@ -125,6 +125,22 @@ int wt_cond_run(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
                 const wt_geometry* geo, const wt_run_io* io, void* scratch,
                 wt_stream_t stream);
 
+/* wt_cond_run_noalloc — wt_cond_run for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. The workspace is a file-scope device array of
+ * WT_NOALLOC_SCRATCH_BYTES bytes that every GPU the library runs on holds until the
+ * process ends; the call allocates nothing (it zeroes what must start at zero with a
+ * kernel of its own). Calls whose workspace (wt_cond_run_scratch_bytes) exceeds it return
+ * hipErrorOutOfMemory (2) without launching: split T into chunks. Every call on one GPU
+ * shares that GPU's array, so calls that overlap on one GPU (on different streams) race;
+ * calls in one stream are safe. flags (device, 4 bytes, may be NULL) receives the run's
+ * error flags, as the first word of wt_cond_run's scratch: 0, or nonzero when a group
+ * barrier timed out. Arguments otherwise as wt_cond_run. */
+#define WT_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int wt_cond_run_noalloc(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
+                        const wt_geometry* geo, const wt_run_io* io, uint32_t* flags,
+                        wt_stream_t stream);
+
 /* wt_cond_run_timed — wt_cond_run with per-workgroup wall-clock ticks (100 MHz) of each
  * phase of the step loop, as seen by the workgroup's first thread, added to
  * timing[wg * 8 + phase], phases: 0 bitmap and input loads + clears, 1 listing of the

@@ -13,6 +13,8 @@ LIBRARY = Path(__file__).resolve().parent / "libwiretorch_amd.so"
 
 P = ctypes.c_void_p
 I64 = ctypes.c_int64
+#: Size of wt_cond_run_noalloc's device workspace (WT_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 
 class Tables(ctypes.Structure):
@@ -95,6 +97,9 @@ SIGNATURES = {
     "wt_cond_run": (ctypes.c_int, [ctypes.POINTER(Tables), ctypes.POINTER(Side),
                                    ctypes.POINTER(Side), ctypes.POINTER(Geometry),
                                    ctypes.POINTER(RunIO), P, P]),
+    "wt_cond_run_noalloc": (ctypes.c_int, [ctypes.POINTER(Tables), ctypes.POINTER(Side),
+                                           ctypes.POINTER(Side), ctypes.POINTER(Geometry),
+                                           ctypes.POINTER(RunIO), P, P]),
     "wt_cond_run_timed": (ctypes.c_int, [ctypes.POINTER(Tables), ctypes.POINTER(Side),
                                          ctypes.POINTER(Side), ctypes.POINTER(Geometry),
                                          ctypes.POINTER(RunIO), P, P, P]),

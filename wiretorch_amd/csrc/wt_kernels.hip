@@ -28,6 +28,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/wiretorch_amd.h"
 #include "wt_math.h"
 
@@ -459,6 +461,76 @@ extern "C" int wt_cond_run(const wt_tables* tab, const wt_side* rec, const wt_si
                            const wt_geometry* geo, const wt_run_io* io, void* scratch,
                            wt_stream_t stream) {
   return run_impl(tab, rec, ff, geo, io, scratch, nullptr, stream);
+}
+
+// ---------------------------------------------------------------------------------
+// wt_cond_run_noalloc: wt_cond_run with its workspace in a file-scope device array, for
+// callers that cannot allocate. The array's host-side name is not a device address:
+// each device's copy is located once with hipGetSymbolAddress and only that pointer is
+// handed to kernels.
+// ---------------------------------------------------------------------------------
+namespace noalloc {
+
+__device__ __align__(256) unsigned char scratch[WT_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex lock;
+void* device_scratch[kMaxDevices] = {};
+
+// Zero `words` 32-bit words (a kernel, not hipMemsetAsync, so that the call may be
+// captured into a graph).
+__global__ void zero_words(uint32_t* p, int64_t words) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+__global__ void copy_word(const uint32_t* from, uint32_t* to) {
+  if (threadIdx.x == 0) *to = *from;
+}
+
+// This device's copy of the array (looked up on the device's first call).
+hipError_t locate(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> guard(lock);
+  if (!device_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    device_scratch[dev] = p;
+  }
+  *out = device_scratch[dev];
+  return hipSuccess;
+}
+
+}  // namespace noalloc
+
+extern "C" int wt_cond_run_noalloc(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
+                                   const wt_geometry* geo, const wt_run_io* io,
+                                   uint32_t* flags, wt_stream_t stream) {
+  if (!tab || !rec || !ff || !geo || !io) return hipErrorInvalidValue;
+  if (geo->groups < 1 || geo->groups > kMaxGroups || geo->R < 1 || geo->range_n < 32 ||
+      io->B < 1 || io->T < 0)
+    return hipErrorInvalidValue;
+  const int64_t bytes = wt_cond_run_scratch_bytes(geo, io->B, io->T);
+  if (bytes > WT_NOALLOC_SCRATCH_BYTES) return hipErrorOutOfMemory;
+  void* work = nullptr;
+  hipError_t e = noalloc::locate(&work);
+  if (e != hipSuccess) return e;
+  const int64_t words = scratch_zeroed(geo) / 4;
+  hipLaunchKernelGGL(noalloc::zero_words, dim3((unsigned)((words + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, static_cast<uint32_t*>(work), words);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  e = (hipError_t)run_impl(tab, rec, ff, geo, io, work, nullptr, stream);
+  if (e != hipSuccess || !flags) return e;
+  hipLaunchKernelGGL(noalloc::copy_word, dim3(1), dim3(64), 0, (hipStream_t)stream,
+                     static_cast<const uint32_t*>(work), flags);
+  return hipGetLastError();
 }
 
 extern "C" int wt_cond_run_timed(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
