@@ -12,7 +12,10 @@ bit for bit (same torch CPU kernels, same association order):
 * ``refractory_mask`` / ``held_at_reset`` / ``count_down`` —
   ``network_simulators/network.py:294-318``;
 * ``recurrent_activations`` — ``network_simulators/network.py:260-271``;
-* ``Drive.feedforward_activations`` — ``network_simulators/network.py:142-157``.
+* ``Drive.feedforward_activations`` — ``network_simulators/network.py:142-157``;
+* ``fold`` — the injection's sum regrouped by the synapse types pathways make
+  (``conductance/dynamics.py:95-100,206-208``), the form the engine evaluates for drives
+  of many pathways.
 
 A drive given in compressed form (``sparse_recurrent`` / ``sparse_feedforward``)
 propagates through ``oracle.sparse.activations`` instead of the dense products.
@@ -129,6 +132,48 @@ def feedforward_activations(drive, x):
     if not drive.feedforward:
         return x.new_zeros((0, B, T, 0))
     return torch.stack([product(x[:, :, rows], W) for rows, W in drive.feedforward])
+
+
+def fold(drive):
+    """The drive with its dense pathways merged per (side, synapse types made): the
+    pathways of a group keep their source rows, each row's weights multiplied by its
+    pathway's kernel scale (a float32 product), and the group's scale is 1.
+
+    This restates the identity ``sum_k a_k (jump scale_k made_k) = sum_g (sum_{k in g}
+    sum_j s_j W_k[j] scale_k) (jump made_g)`` of the reference's injection
+    (``conductance/dynamics.py:95-100,206-208``), which holds for pathways that make the
+    same synapse types; the engine evaluates a drive of more pathways than its kernels
+    hold this way. Groups keep the order of first appearance, recurrent first. A
+    compressed side is left as it is."""
+    from wiretorch_amd.network import Drive
+
+    made = drive.made.bool()
+    K_rec, K = drive.K_rec, drive.K_rec + drive.K_ff
+    out_made, sides = [], []
+    for lo, hi, pathways, sparse in ((0, K_rec, drive.recurrent, drive.sparse_recurrent),
+                                     (K_rec, K, drive.feedforward, drive.sparse_feedforward)):
+        if sparse is not None:
+            out_made += [made[k] for k in range(lo, hi)]
+            sides.append([])
+            continue
+        rows_of = {}
+        for k in range(lo, hi):
+            key = tuple(made[k].tolist())
+            rows_of.setdefault(key, []).append(k)
+        merged = []
+        for key, members in rows_of.items():
+            out_made.append(made[members[0]])
+            rows = torch.cat([pathways[k - lo][0] for k in members])
+            W = torch.cat([pathways[k - lo][1] * drive.scale[k] for k in members], dim=0)
+            merged.append((rows, W))
+        sides.append(merged)
+    N = drive.scale.shape[1]
+    return Drive(made=torch.stack(out_made), scale=torch.ones((len(out_made), N)),
+                 recurrent=sides[0], feedforward=sides[1],
+                 differentiable_inputs=drive.differentiable_inputs,
+                 recurrent_gradients=drive.recurrent_gradients,
+                 sparse_recurrent=drive.sparse_recurrent,
+                 sparse_feedforward=drive.sparse_feedforward)
 
 
 def stack_steps(tensors):

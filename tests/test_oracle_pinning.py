@@ -275,3 +275,93 @@ def test_rounded_product_rounds_operands_and_dl_da_only():
         torch.testing.assert_close(W1.grad, a.T @ g, rtol=1e-6, atol=1e-6)
     # float32 storage is the plain product
     torch.testing.assert_close(oracle_rate.product(a, W, torch.float32, True), a @ W)
+
+
+# ---------------------------------------------------------------------------------
+# Pathways folded per receptor kind (oracle.dynamics.fold)
+# ---------------------------------------------------------------------------------
+
+
+def _random_drive(seed, K_rec=9, K_ff=4, S=3, N=40, n_src=50, n_in=30):
+    from wiretorch_amd.network import Drive
+
+    rng = np.random.default_rng(seed)
+    kinds = rng.random((3, S)) < 0.6
+    kinds[:, 0] |= ~kinds.any(axis=1)
+    made = torch.from_numpy(kinds[rng.integers(0, 3, K_rec + K_ff)])
+    scale = torch.from_numpy(rng.lognormal(0, 0.5, (K_rec + K_ff, N)).astype(np.float32))
+
+    def pathways(n, K):
+        rows = np.array_split(rng.permutation(n), K)
+        return [(torch.from_numpy(r).long(),
+                 torch.from_numpy((rng.lognormal(-1, 1, (len(r), N)) * (rng.random((len(r), N)) < 0.3))
+                                  .astype(np.float32))) for r in rows]
+
+    return Drive(made=made, scale=scale, recurrent=pathways(n_src, K_rec),
+                 feedforward=pathways(n_in, K_ff))
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_fold_regroups_the_injection_exactly(seed):
+    """In float64 arithmetic (a float64 drive) the folded drive injects what the
+    per-pathway drive does (the reference's sum over pathways of a_k (jump scale_k
+    made_k), with a_k the pathway's rows times its weights): one step's conductance
+    increment from random spikes and inputs, 13 pathways of 3 kinds, agrees to 1e-12
+    relative."""
+    import oracle.dynamics as od
+
+    drive = _random_drive(seed)
+    drive.scale = drive.scale.double()  # the regrouping alone (fold's products in float64)
+    drive.recurrent = [(r, W.double()) for r, W in drive.recurrent]
+    drive.feedforward = [(r, W.double()) for r, W in drive.feedforward]
+    folded = od.fold(drive)
+    rng = np.random.default_rng(seed + 10)
+    s = torch.from_numpy((rng.random((2, 50)) < 0.4).astype(np.float64))
+    x = torch.from_numpy((rng.random((2, 30)) < 0.4).astype(np.float64))
+    jump = torch.from_numpy(rng.normal(0, 1, (2, 3)))
+
+    def increment(d):
+        total = torch.zeros((2, 40, 2, 3), dtype=torch.float64)
+        acts = ([s[:, rows] @ W.double() for rows, W in d.recurrent]
+                + [x[:, rows] @ W.double() for rows, W in d.feedforward])
+        assert len(acts) == d.made.shape[0]
+        for k, a in enumerate(acts):
+            kernel = jump[None] * d.scale[k].double()[:, None, None] * d.made[k].double()
+            total += a[:, :, None, None] * kernel
+        return total
+
+    want, got = increment(drive), increment(folded)
+    assert folded.made.shape[0] <= 6 and len(folded.recurrent) <= 3
+    assert torch.allclose(got, want, rtol=1e-12, atol=1e-12 * float(want.abs().max()))
+
+
+def test_fold_of_many_types_follows_the_per_pathway_run(monkeypatch):
+    """The many-cell-type network (21 pathways): 200 steps of the folded drive against
+    the per-pathway one, both with exactly rounded sums: voltages within 1e-5 relative,
+    spikes identical; and the engine's own folding gives the oracle's folded weights
+    bit for bit."""
+    import oracle.dynamics as od
+    import scenarios as sc
+    from wiretorch_amd import engine, synthetic
+
+    monkeypatch.setattr(od, "SUMS", "exact")
+    wl = synthetic.many_types(T=200)
+    model = wl.model
+    sc.use_engine(model, od)
+    drive, p = model._drive(), model._physiology()
+    assert drive.K_rec + drive.K_ff == 21
+    x = torch.from_numpy(wl.x).float()
+    model.reset_state()
+    with torch.no_grad():
+        a = od.simulate(model.v, model._synaptic, x, drive, p, track=True)
+        b = od.simulate(model.v, model._synaptic, x, od.fold(drive), p, track=True)
+    assert a.output.sum() > 0
+    assert torch.equal(a.output, b.output)
+    np.testing.assert_allclose(b.tracked["v"].numpy(), a.tracked["v"].numpy(), rtol=1e-5,
+                               atol=65e-5)
+    mine = engine.fold_pathways(drive)
+    theirs = od.fold(drive)
+    assert torch.equal(mine.made, theirs.made)
+    for (r1, W1), (r2, W2) in zip(mine.recurrent + mine.feedforward,
+                                  theirs.recurrent + theirs.feedforward):
+        assert torch.equal(r1, r2) and torch.equal(W1, W2)

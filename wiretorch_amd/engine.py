@@ -116,6 +116,8 @@ class _Side:
     #: order, a slice where they are consecutive) and their flat indices into the
     #: pathway's (rows, N) weight matrix.
     dense_edges: tuple = ()
+    #: the version of ``conn.weights`` the side was built with
+    weights_version: int = -1
     _split: dict = field(default_factory=dict)
     _edge_src: torch.Tensor | None = None
     _by_target: dict = field(default_factory=dict)
@@ -240,7 +242,10 @@ def _from_connectome(conn: Connectome, device) -> _Side:
         raise ValueError("Connectome pathway ids must be < n_pathways (or -1)")
     if int(conn.indptr[-1]) != conn.n_edges or conn.indptr.numel() != conn.n_sources + 1:
         raise ValueError("Connectome indptr does not match its edges")
-    return _Side(conn, conn.pathway.to(torch.int32).contiguous(), max_in_sum=_max_in_sum(conn))
+    side = _Side(conn, conn.pathway.to(torch.int32).contiguous())
+    side.max_in_sum = _max_in_sum(conn, side.target_order())
+    side.weights_version = conn.weights._version
+    return side
 
 
 def _row_starts(conn: Connectome) -> torch.Tensor:
@@ -292,10 +297,28 @@ _LAYOUTS_SIZE = 4
 
 
 def _side_of(pathways, sparse, n_src: int, N: int, device) -> _Side:
-    """The compressed side of a drive, cached while its tensors are unchanged."""
+    """The compressed side of a drive, cached while its tensors are unchanged. A
+    compressed connectome's structure (indptr, targets, pathways) is validated and cached
+    once; new edge weights on the same structure (learnt or folded each call) are taken
+    without either (``_Side.with_weights``)."""
     if sparse is not None:
-        key = ("sparse", id(sparse), sparse.weights._version, sparse.weights.data_ptr())
-        keep = (sparse,)
+        c = sparse
+        key = ("sparse",) + _key(c.indptr, c.targets, c.pathway) + (c.n_pathways,)
+        hit = _CACHE.get(key)
+        if hit is None:
+            base = _from_connectome(sparse, device)
+            _CACHE[key] = (base, (c.indptr, c.targets, c.pathway))
+            while len(_CACHE) > _CACHE_SIZE:
+                _CACHE.popitem(last=False)
+        else:
+            _CACHE.move_to_end(key)
+            base = hit[0]
+        w = c.weights.to(device)
+        if base.conn.weights is w or (base.conn.weights.data_ptr() == w.data_ptr()
+                                      and base.weights_version == w._version):
+            return base
+        side = base.with_weights(w)
+        return side
     elif pathways:
         key = ("dense", n_src, N) + tuple(
             (rows.data_ptr(), W.data_ptr(), W._version, tuple(W.shape)) for rows, W in pathways
@@ -349,6 +372,102 @@ def _dense_side(pathways, n_src: int, N: int, device) -> tuple[_Side, bool]:
     while len(_LAYOUTS) > _LAYOUTS_SIZE:
         _LAYOUTS.popitem(last=False)
     return side, False
+
+
+# =====================================================================
+# Many pathways: one per receptor kind
+# =====================================================================
+
+#: Pathways the kernels accumulate separately (``WT_MAX_K``); a drive with more is folded.
+MAX_PATHWAYS = 8
+_GROUP_ROWS: OrderedDict = OrderedDict()
+
+
+def _group_order(made: torch.Tensor, ks: range) -> list[list[int]]:
+    """Pathways ``ks`` grouped by their row of ``made`` (first appearance first)."""
+    groups: dict[bytes, list[int]] = {}
+    rows = made.detach().to("cpu", torch.bool).numpy()
+    for k in ks:
+        groups.setdefault(rows[k].tobytes(), []).append(k)
+    return list(groups.values())
+
+
+def fold_pathways(drive: Drive) -> Drive:
+    """The drive with its pathways folded into one per (side, synapse types made).
+
+    Pathway ``k`` adds ``a_k ⊗ (jump · scale_k · made_k)`` (``conductance/dynamics.py:
+    95-100,206-208``), ``a_k[n] = Σ_j s_j W_k[j, n]``. Pathways that make the same synapse
+    types share ``made``, so their sum is ``(Σ_k Σ_j s_j · W_k[j, n] scale_k[n]) ⊗ (jump ·
+    made)``: one pathway per group whose weights are ``W_k[j, n] · scale_k[n]`` (a float32
+    product) and whose scale is 1. The sum is the same; its rounding is not the
+    reference's sequence of per-pathway additions (each group's is exactly rounded, as
+    every activation here). Recurrent groups come first, in order of first appearance.
+    Differentiable: the folded weights are torch expressions of ``W_k`` and ``scale``."""
+    K_rec, K = drive.K_rec, drive.K_rec + drive.K_ff
+    sides = (
+        (_group_order(drive.made, range(K_rec)), drive.recurrent, drive.sparse_recurrent, 0),
+        (_group_order(drive.made, range(K_rec, K)), drive.feedforward, drive.sparse_feedforward,
+         K_rec),
+    )
+    made, out = [], []
+    for groups, dense, sparse, k0 in sides:
+        made += [drive.made[g[0]] for g in groups]
+        if sparse is not None:
+            out.append(_fold_sparse(sparse, drive.scale[k0:k0 + sparse.n_pathways], groups, k0))
+        else:
+            out.append(_fold_dense(dense, drive.scale, groups, k0))
+    N = drive.scale.shape[1]
+    G = len(made)
+    rec, ff = out
+    return Drive(
+        made=torch.stack(made) if made else drive.made[:0],
+        scale=drive.scale.new_ones((G, N)).detach(),
+        recurrent=rec if isinstance(rec, list) else [],
+        feedforward=ff if isinstance(ff, list) else [],
+        differentiable_inputs=drive.differentiable_inputs,
+        recurrent_gradients=drive.recurrent_gradients,
+        gates=drive.gates,
+        sparse_recurrent=None if isinstance(rec, list) else rec,
+        sparse_feedforward=None if isinstance(ff, list) else ff,
+    )
+
+
+def _fold_dense(pathways, scale, groups, k0):
+    """One dense pathway per group: its members' rows back to back, each row's weights
+    times its pathway's scale. The concatenated row indices are cached by the members'
+    (so the engine's layout cache sees the same rows tensor each call)."""
+    out = []
+    for g in groups:
+        members = [pathways[k - k0] for k in g]
+        key = tuple((rows.data_ptr(), rows._version, rows.numel()) for rows, _ in members)
+        rows_g = _GROUP_ROWS.get(key)
+        if rows_g is None:
+            rows_g = _GROUP_ROWS[key] = (torch.cat([rows.long() for rows, _ in members]),
+                                         tuple(rows for rows, _ in members))
+            while len(_GROUP_ROWS) > _CACHE_SIZE:
+                _GROUP_ROWS.popitem(last=False)
+        W_g = torch.cat([W * scale[k][None, :].to(W.dtype) for k, (_, W) in zip(g, members)])
+        out.append((rows_g[0], W_g))
+    return out
+
+
+def _fold_sparse(conn: Connectome, scale, groups, k0):
+    """The compressed side with each edge's weight times its pathway's scale at its
+    target, sources tagged by group."""
+    group_of = torch.full((max(conn.n_pathways, 1),), -1, dtype=torch.int64)
+    for gi, g in enumerate(groups):
+        group_of[[k - k0 for k in g]] = gi
+    group_of = group_of.to(conn.device)
+    pathway = torch.where(conn.pathway >= 0, group_of[conn.pathway.clamp(min=0)], -1)
+    if conn.n_edges:
+        counts = conn.indptr[1:] - conn.indptr[:-1]
+        src = torch.repeat_interleave(torch.arange(conn.n_sources, device=conn.device), counts)
+        k = conn.pathway[src].clamp(min=0)
+        weights = conn.weights * scale[k, conn.targets.long()].to(conn.weights.dtype)
+    else:
+        weights = conn.weights
+    return Connectome(conn.n_sources, conn.n_targets, conn.indptr, conn.targets, weights,
+                      pathway, len(groups))
 
 
 # =====================================================================
@@ -512,8 +631,10 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
     if S > 8:
         raise NotImplementedError(f"at most 8 synapse types, got {S}")
     K_rec, K_ff = drive.K_rec, drive.K_ff
-    if K_rec + K_ff > 8:
-        raise NotImplementedError(f"at most 8 pathways, got {K_rec + K_ff}")
+    if K_rec + K_ff > MAX_PATHWAYS:
+        raise NotImplementedError(
+            f"{K_rec + K_ff} pathways make more than {MAX_PATHWAYS} distinct (side, synapse "
+            "types) combinations")
     if drive.made.shape != (K_rec + K_ff, S) or drive.scale.shape != (K_rec + K_ff, N):
         raise ValueError("drive.made / drive.scale do not match the pathways")
     rec = _side_of(drive.recurrent, drive.sparse_recurrent, N, N, device)
@@ -805,6 +926,8 @@ def simulate(
     if p.storage_dtype != torch.float32:
         raise NotImplementedError("float16 storage")
     device = x.device
+    if drive.K_rec + drive.K_ff > MAX_PATHWAYS:
+        drive = fold_pathways(drive)
     L = _plan(v, x, drive, p, probabilities, track, track_batch_idx)
     # The kernel updates the state in place: always work on copies, so the caller's
     # tensors keep their values (a permuted view may already be contiguous storage).

@@ -40,7 +40,8 @@ import numpy as np
 import torch
 from torch import nn
 
-from wiretorch_amd.projections import Projection, projection_mask
+from wiretorch_amd.connectome import Connectome
+from wiretorch_amd.projections import Projection, SparseProjection, projection_mask
 from wiretorch_amd.synapses import SynapseRegistry
 from wiretorch_amd.type_parameters import (
     TypeParameters,
@@ -217,12 +218,22 @@ def validate(dt, cell_params, cell_type_indices, sides) -> None:
         assert types.ndim == 1 and np.all((types >= 0) & (types < len(side.cell_params)))
         sources = {p["name"]: p["cell_id"] for p in side.cell_params}
         n_source = np.bincount(types, minlength=len(side.cell_params))
+        if is_sparse(side):
+            got = (side.projections.n_source, side.projections.n_target)
+            want = (len(types), len(cell_type_indices))
+            assert got == want, f"{side.attribute}: sparse projection {got} != {want}"
+            continue
         for (src, tgt), projection in side.projections.items():
             assert src in sources, f"{side.attribute}: source {src!r} not in its cell_params"
             assert tgt in targets, f"{side.attribute}: target {tgt!r} not in cell_params"
             want = (int(n_source[sources[src]]), int(n_target[targets[tgt]]))
             got = (projection.n_source, projection.n_target)
             assert got == want, f"{side.attribute} projection ({src!r}, {tgt!r}) {got} != {want}"
+
+
+def is_sparse(side: InputSide) -> bool:
+    """Whether a side is one ``SparseProjection`` (rather than per-type-pair blocks)."""
+    return isinstance(side.projections, SparseProjection)
 
 
 def _unsupported(cell_params, synapse_lists, stp) -> None:
@@ -294,6 +305,9 @@ class ProjectionNetwork(nn.Module):
         )
         self.register_buffer("cell_type_indices", _long(cell_type_indices))
         for side in sides:
+            if is_sparse(side):  # one module; no dense mask (the connectome is the mask)
+                setattr(self, side.attribute, side.projections)
+                continue
             modules = {f"{s}__{t}": p for (s, t), p in side.projections.items()}
             setattr(self, side.attribute, nn.ModuleDict(modules))
             self.register_buffer(side.mask_buffer, torch.from_numpy(self._mask(side)))
@@ -341,6 +355,9 @@ class ProjectionNetwork(nn.Module):
     def _build_pathways(self) -> list[Pathway]:
         pathways, made = [], []
         for side_no, side in enumerate(self._sides):
+            if is_sparse(side):
+                self._sparse_pathways(side_no, side, pathways, made)
+                continue
             names = {c["cell_id"]: c["name"] for c in side.cell_params}
             modes: dict[str, str] = {}
             for (src, _), projection in side.projections.items():
@@ -368,6 +385,27 @@ class ProjectionNetwork(nn.Module):
         # Recurrent pathways first: the order the dynamics inject them in.
         return sorted(pathways, key=lambda p: not self._sides[p.side].recurrent)
 
+    def _sparse_pathways(self, side_no: int, side: InputSide, pathways, made) -> None:
+        """A ``SparseProjection`` side's pathways: one per distinct set of synapse types
+        its source cell types make (in order of first appearance over ascending cell
+        type), instead of one per source cell type — the same sum (see
+        ``engine.fold_pathways``), and a handful of pathways however many cell types.
+        ``_group_of_<side>`` gives each source its pathway within the side (-1: its type
+        makes no synapse)."""
+        groups: dict[bytes, int] = {}
+        of_type = np.full(len(side.cell_params), -1, dtype=np.int64)
+        for cell_type, synapses in self.registry.made_by(side_no, side.synapse_params).items():
+            key = synapses.numpy().tobytes()
+            if key not in groups:
+                groups[key] = len(groups)
+                pathways.append(Pathway(len(pathways), side_no, -1, "sparse"))
+                made.append(synapses)
+            of_type[cell_type] = groups[key]
+        self.register_buffer(f"_group_of_{side_no}", _long(of_type[side.cell_type_indices]),
+                             persistent=False)
+        self._sparse_counts = getattr(self, "_sparse_counts", {})
+        self._sparse_counts[side_no] = len(groups)
+
     def _assemble(self, pathway: Pathway, connectome: bool = False) -> torch.Tensor:
         """The pathway's ``(n_rows, N)`` weights from its projections."""
         side = self._sides[pathway.side]
@@ -387,7 +425,7 @@ class ProjectionNetwork(nn.Module):
 
     def _cache_weights(self) -> None:
         for pathway in self.pathways:
-            if pathway.mode != "weights":
+            if pathway.mode not in ("weights", "sparse"):
                 W = self._assemble(pathway, connectome=pathway.mode == "scaling_factors")
                 self.register_buffer(f"_weights_{pathway.index}", W.detach(), persistent=False)
 
@@ -427,7 +465,18 @@ class ProjectionNetwork(nn.Module):
         scaling, assembled = {}, {}
         ones = torch.ones(self.n_neurons, **self._float)
         scales, recurrent, feedforward = [], [], []
+        sparse = {}
         for pathway in self.pathways:
+            if pathway.mode == "sparse":
+                scales.append(ones)
+                if pathway.side not in sparse:
+                    side = self._sides[pathway.side]
+                    proj = getattr(self, side.attribute)
+                    sparse[pathway.side] = Connectome(
+                        proj.n_source, self.n_neurons, proj.indptr, proj.targets, proj(),
+                        getattr(self, f"_group_of_{pathway.side}"),
+                        self._sparse_counts[pathway.side])
+                continue
             if pathway.mode != "weights":
                 W = getattr(self, f"_weights_{pathway.index}")
             else:
@@ -449,6 +498,9 @@ class ProjectionNetwork(nn.Module):
             feedforward=feedforward,
             differentiable_inputs=self.differentiable_inputs,
             recurrent_gradients=self.recurrent_gradients,
+            sparse_recurrent=next((c for i, c in sparse.items() if self._sides[i].recurrent), None),
+            sparse_feedforward=next((c for i, c in sparse.items() if not self._sides[i].recurrent),
+                                    None),
         )
 
     @torch.compiler.disable
@@ -531,6 +583,8 @@ class ProjectionNetwork(nn.Module):
 
     def _weight_matrix(self, side_index: int) -> torch.Tensor:
         side = self._sides[side_index]
+        if is_sparse(side):
+            return getattr(self, side.attribute).dense()
         W = torch.zeros((len(side.cell_type_indices), self.n_neurons), **self._float)
         for (src, tgt), _ in side.projections.items():
             rows, cols = self._block(side, src, tgt)
@@ -713,6 +767,12 @@ class ConductanceLIFNetwork(ConductanceNetwork):
     ``Projection``; synapse types with the same (cell type, synapse) signature on both
     sides share one conductance. Gradients flow through the recurrent spikes only if
     ``recurrent_gradients``.
+
+    Extensions for connectomes of many cell types (fly scale), which the reference's
+    dense per-pair blocks and per-cell-type synapse types cannot hold: either side may be
+    one ``SparseProjection`` instead of a dict, and a ``synapse_params`` entry may name
+    several source cell types in ``cell_id`` (``synapses.SynapseRegistry``), so thousands
+    of cell types share a few synapse types; ``unify_synapses`` is passed through.
     """
 
     def __init__(
@@ -737,6 +797,7 @@ class ConductanceLIFNetwork(ConductanceNetwork):
         recurrent_gradients: bool = False,
         rec_stp: dict | None = None,
         ff_stp: dict | None = None,
+        unify_synapses: bool = True,
     ):
         _unsupported(cell_params, (synapse_params, synapse_params_FF), (rec_stp, ff_stp))
         self.synapse_params = synapse_params
@@ -755,7 +816,7 @@ class ConductanceLIFNetwork(ConductanceNetwork):
                 InputSide(ff_projections, cell_params_FF, synapse_params_FF,
                           cell_type_indices_FF, False, "ff_projections", "weights_mask_FF"),
             ],
-            unify_synapses=True,
+            unify_synapses=unify_synapses,
             surrgrad_scale=surrgrad_scale,
             batch_size=batch_size,
             spike_mode=spike_mode,

@@ -215,3 +215,115 @@ def projection_mask(projection: Projection) -> np.ndarray:
     if isinstance(projection, SignedProjection):
         return np.ones((projection.n_source, projection.n_target), dtype=bool)
     raise TypeError(f"unknown Projection subclass {type(projection).__name__}")
+
+
+# ====================================================================
+# A whole side in compressed form (connectomes too large for dense blocks)
+# ====================================================================
+
+
+class SparseProjection(nn.Module):
+    """Every synapse of one input side, compressed by source, with one scaling factor per
+    (source cell type, target cell type) pair.
+
+    The reference describes a side as one dense ``(n_source, n_target)`` block per type
+    pair, each a ``ScalingFactorProjection`` (``projections.py:100-131``: weights
+    ``exp(log_sf) * connectome``, the factor applied to the synapse kernel). At fly scale
+    (140k neurons, 8000 cell types, ~50M synapses) neither the blocks (one module per
+    pair, dense rows of 140k) nor the network's dense masks can exist. This holds the same
+    information by synapse:
+
+    * ``indptr`` ``(n_source + 1,)`` int64, ``targets`` ``(E,)`` int32 ascending per
+      source, ``counts`` ``(E,)`` float32 — the connectome (synapse counts);
+    * ``pair`` ``(E,)`` int64 — each synapse's (source type, target type) pair,
+      ``source_type * n_target_types + target_type``;
+    * the factors ``(n_source_types, n_target_types)``: the parameter ``log_sf`` when
+      learnt, else the buffer ``sf``.
+
+    ``forward()`` gives each synapse's weight ``count * sf[pair]`` (float32), the factor
+    folded into the weights rather than the kernel: the activation it feeds is the same
+    sum. Duplicate (source, target) entries in the input are summed.
+    """
+
+    caching_mode = "sparse"
+
+    def __init__(self, n_source: int, n_target: int, source, target, counts, source_types,
+                 target_types, sf=1.0, learn_sf: bool = False, n_source_types=None,
+                 n_target_types=None):
+        super().__init__()
+        as_long = lambda a: torch.as_tensor(np.asarray(a) if not torch.is_tensor(a) else a).long()  # noqa: E731
+        src, tgt = as_long(source), as_long(target)
+        c = torch.as_tensor(counts if torch.is_tensor(counts) else np.asarray(counts)).float()
+        device = src.device
+        src_types, tgt_types = as_long(source_types).to(device), as_long(target_types).to(device)
+        self.n_source, self.n_target = int(n_source), int(n_target)
+        if src_types.numel() != self.n_source or tgt_types.numel() != self.n_target:
+            raise ValueError("source_types / target_types must give one type per neuron")
+        if src.numel() and (int(src.min()) < 0 or int(src.max()) >= self.n_source
+                            or int(tgt.min()) < 0 or int(tgt.max()) >= self.n_target):
+            raise ValueError("synapse endpoints out of range")
+        n_st = int(n_source_types if n_source_types is not None else int(src_types.max()) + 1)
+        n_tt = int(n_target_types if n_target_types is not None else int(tgt_types.max()) + 1)
+        key = src * self.n_target + tgt
+        key, order = torch.sort(key)
+        c = c.to(device)[order]
+        uniq, inverse = torch.unique_consecutive(key, return_inverse=True)
+        if uniq.numel() != key.numel():  # repeated pairs: their counts summed (in float64)
+            merged = torch.zeros(uniq.numel(), dtype=torch.float64, device=device)
+            merged.index_add_(0, inverse, c.double())
+            c = merged.float()
+        s_u, t_u = uniq // self.n_target, uniq % self.n_target
+        indptr = torch.zeros(self.n_source + 1, dtype=torch.int64, device=device)
+        indptr[1:] = torch.cumsum(torch.bincount(s_u, minlength=self.n_source), 0)
+        self.register_buffer("indptr", indptr)
+        self.register_buffer("targets", t_u.to(torch.int32).contiguous())
+        self.register_buffer("counts", c.contiguous())
+        self.register_buffer("pair", (src_types[s_u] * n_tt + tgt_types[t_u]).contiguous())
+        self.n_source_types, self.n_target_types = n_st, n_tt
+        table = torch.as_tensor(sf if torch.is_tensor(sf) else np.asarray(sf, dtype=np.float32))
+        table = table.float().to(device).expand(n_st, n_tt).contiguous()
+        if learn_sf:
+            if not bool((table > 0).all()):
+                raise ValueError("learnt scaling factors must start positive")
+            # log(sf + 1e-8) in float64, rounded once: ScalingFactorProjection's start
+            self.log_sf = nn.Parameter(torch.log(table.double() + 1e-8).float())
+        else:
+            self.register_buffer("sf", table)
+        self._memo = None
+
+    @property
+    def n_edges(self) -> int:
+        return int(self.targets.numel())
+
+    def factors(self) -> torch.Tensor:
+        """``(n_source_types, n_target_types)`` scaling factors."""
+        return torch.exp(self.log_sf) if hasattr(self, "log_sf") else self.sf
+
+    def forward(self) -> torch.Tensor:  # type: ignore[override]
+        """``(E,)`` float32 synapse weights, ``count * sf[pair]``. Without autograd
+        (fixed factors, or under ``no_grad``) the result is reused while the factors and
+        counts are unchanged."""
+        table = self.log_sf if hasattr(self, "log_sf") else self.sf
+        tracking = torch.is_grad_enabled() and table.requires_grad
+        key = (table.data_ptr(), table._version, self.counts.data_ptr(), self.counts._version,
+               self.pair.data_ptr())
+        if not tracking and self._memo is not None and self._memo[0] == key:
+            return self._memo[1]
+        w = self.counts * self.factors().reshape(-1)[self.pair]
+        if not tracking:
+            self._memo = (key, w.detach())
+        return w
+
+    def _apply(self, fn, recurse=True):
+        self._memo = None  # device or dtype moves invalidate the reused weights
+        return super()._apply(fn, recurse)
+
+    def dense(self) -> torch.Tensor:
+        """``(n_source, n_target)`` weights, for small networks (tests, inspection)."""
+        if self.n_source * self.n_target > 1 << 28:
+            raise ValueError("too large for a dense matrix")
+        W = torch.zeros((self.n_source, self.n_target), device=self.counts.device)
+        src = torch.repeat_interleave(torch.arange(self.n_source, device=self.counts.device),
+                                      self.indptr[1:] - self.indptr[:-1])
+        W[src, self.targets.long()] = self.forward()
+        return W

@@ -8,6 +8,12 @@ index, so e.g. AMPA made by excitatory neurons on both sides is one conductance.
 
 Follows ``src/wiretorch/network_simulators/synapses.py:18-86`` (index order: sides in
 order, each side's types in the order given; unification by signature).
+
+Extension for networks of many cell types: an entry's ``cell_id`` may list several
+source cell types, all of which make that synapse type (the reference needs one entry
+per cell type, hence one synapse type per cell type at fly scale). An entry whose
+``cell_id`` is a list has the signature ``(None, synapse name)``: unified, two sides'
+listed entries of one name share one index.
 """
 
 from __future__ import annotations
@@ -43,7 +49,8 @@ class SynapseRegistry:
             )
             mapping: dict[int, int] = {}
             for syn in order:
-                signature = (cell_name[syn["cell_id"]], syn["name"])
+                maker = None if _listed(syn) else cell_name[syn["cell_id"]]
+                signature = (maker, syn["name"])
                 key = signature if unify else (side_no, syn["synapse_id"])
                 if key not in index_of:
                     index_of[key] = len(entries)
@@ -69,8 +76,19 @@ class SynapseRegistry:
         """Per source cell type of ``side`` (ascending id), which indices it makes."""
         out: dict[int, torch.Tensor] = {}
         for syn in synapse_params:
-            mask = out.get(syn["cell_id"])
-            if mask is None:
-                mask = out[syn["cell_id"]] = torch.zeros(len(self), dtype=torch.bool)
-            mask[self.to_index[side][syn["synapse_id"]]] = True
+            for cell in _makers(syn):
+                mask = out.get(cell)
+                if mask is None:
+                    mask = out[cell] = torch.zeros(len(self), dtype=torch.bool)
+                mask[self.to_index[side][syn["synapse_id"]]] = True
         return {k: out[k] for k in sorted(out)}
+
+
+def _listed(syn: dict) -> bool:
+    """Whether an entry names its source cell types as a list (the extension)."""
+    return isinstance(syn["cell_id"], (list, tuple, range))
+
+
+def _makers(syn: dict) -> list[int]:
+    """The source cell types an entry names: one ``cell_id``, or a list of them."""
+    return [int(c) for c in syn["cell_id"]] if _listed(syn) else [int(syn["cell_id"])]

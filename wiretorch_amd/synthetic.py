@@ -225,27 +225,11 @@ def fly_scale(N=140_000, n_types=8000, exponent=2.1, mean_degree=357, k_max=8000
     sensory, each driven by its own Poisson channel (weight ``w_in``). The default
     weights were chosen by a sweep on the GPU for a stable, irregular state at the
     configuration's 10 Hz mean rate (9.3 Hz measured, 2% of neurons silent)."""
-    rng = np.random.default_rng(seed)
-    cell_type = rng.integers(0, n_types, N)
-    type_is_e = rng.random(n_types) < frac_e_types
+    cell_type, type_is_e, deg, tgt, counts, sf, sensory, x = _fly_draws(
+        N, n_types, exponent, mean_degree, k_max, count_mean, frac_e_types, frac_sensory,
+        rate_hz, B, T, dt, seed, input_seed, sf_sigma)
     is_e = type_is_e[cell_type]
-    grid = np.arange(1, k_max + 1, dtype=np.float64)
-    lo_k, hi_k = 1.0, float(mean_degree)
-    for _ in range(60):  # k_min for the requested mean, by bisection on the law's mean
-        mid = 0.5 * (lo_k + hi_k)
-        ks = grid[grid >= mid]
-        pk = ks ** -exponent
-        if (ks * pk).sum() / pk.sum() < mean_degree:
-            lo_k = mid
-        else:
-            hi_k = mid
-    deg = power_law_degrees(rng, N, exponent, int(round(lo_k)), k_max)
     n_draws = int(deg.sum())
-    tgt = rng.integers(0, N, n_draws, dtype=np.int64)
-    counts = rng.geometric(1.0 / count_mean, n_draws).astype(np.float32)
-    sf = rng.lognormal(0.0, sf_sigma, (n_types, n_types)).astype(np.float32)
-    sensory = np.sort(rng.choice(N, int(round(frac_sensory * N)), replace=False))
-    x = poisson(np.random.default_rng([seed, input_seed]), B, T, np.full(sensory.size, rate_hz), dt)
 
     dev = torch.device(device)
     src_t = torch.repeat_interleave(torch.arange(N, device=dev), torch.from_numpy(deg).to(dev))
@@ -276,6 +260,153 @@ def fly_scale(N=140_000, n_types=8000, exponent=2.1, mean_degree=357, k_max=8000
                      n_draws=np.array([n_draws]), sf_row0=sf[0])
     drive, p = sparse_drive(rec, ff, N, dt, device)
     return Workload("config2", x, structure, drive=drive, physiology=p, N=N, S=2)
+
+
+def _fly_draws(N, n_types, exponent, mean_degree, k_max, count_mean, frac_e_types,
+               frac_sensory, rate_hz, B, T, dt, seed, input_seed, sf_sigma=0.5):
+    """The random draws of configuration 2, in ``fly_scale``'s order (one stream)."""
+    rng = np.random.default_rng(seed)
+    cell_type = rng.integers(0, n_types, N)
+    type_is_e = rng.random(n_types) < frac_e_types
+    grid = np.arange(1, k_max + 1, dtype=np.float64)
+    lo_k, hi_k = 1.0, float(mean_degree)
+    for _ in range(60):  # k_min for the requested mean, by bisection on the law's mean
+        mid = 0.5 * (lo_k + hi_k)
+        ks = grid[grid >= mid]
+        pk = ks ** -exponent
+        if (ks * pk).sum() / pk.sum() < mean_degree:
+            lo_k = mid
+        else:
+            hi_k = mid
+    deg = power_law_degrees(rng, N, exponent, int(round(lo_k)), k_max)
+    n_draws = int(deg.sum())
+    tgt = rng.integers(0, N, n_draws, dtype=np.int64)
+    counts = rng.geometric(1.0 / count_mean, n_draws).astype(np.float32)
+    sf = rng.lognormal(0.0, sf_sigma, (n_types, n_types)).astype(np.float32)
+    sensory = np.sort(rng.choice(N, int(round(frac_sensory * N)), replace=False))
+    x = poisson(np.random.default_rng([seed, input_seed]), B, T, np.full(sensory.size, rate_hz), dt)
+    return cell_type, type_is_e, deg, tgt, counts, sf, sensory, x
+
+
+def fly_scale_network(N=140_000, n_types=8000, exponent=2.1, mean_degree=357, k_max=8000,
+                      count_mean=4.0, frac_e_types=0.7, frac_sensory=0.05, rate_hz=10.0, B=8,
+                      T=2000, dt=0.1, seed=2, w_e=1.0, w_i=5.0, w_in=30.0, sf_sigma=0.5,
+                      learn_sf=False, device="cpu", input_seed=0) -> Workload:
+    """Configuration 2 through the network API: a ``ConductanceLIFNetwork`` of ``n_types``
+    cell types whose recurrent side is one ``SparseProjection`` — each synapse's count
+    times the learnable scaling factor of its (source type, target type) pair — and whose
+    input side connects each sensory channel to its neuron. The draws are
+    ``fly_scale``'s; the receptor kinds' strengths ``w_e`` / ``w_i`` are the synapse
+    types' ``g_bar`` (one ``synapse_params`` entry per kind, made by all cell types of that
+    kind) instead of factors in the weights, so the dynamics equal ``fly_scale``'s up to
+    rounding."""
+    from wiretorch_amd.projections import SparseProjection
+
+    cell_type, type_is_e, deg, tgt, counts, sf, sensory, x = _fly_draws(
+        N, n_types, exponent, mean_degree, k_max, count_mean, frac_e_types, frac_sensory,
+        rate_hz, B, T, dt, seed, input_seed, sf_sigma)
+    dev = torch.device(device)
+    src = torch.repeat_interleave(torch.arange(N, device=dev), torch.from_numpy(deg).to(dev))
+    rec = SparseProjection(N, N, src, torch.from_numpy(tgt).to(dev),
+                           torch.from_numpy(counts).to(dev), torch.from_numpy(cell_type),
+                           torch.from_numpy(cell_type), sf=torch.from_numpy(sf),
+                           learn_sf=learn_sf, n_source_types=n_types, n_target_types=n_types)
+    del src
+    n_in = sensory.size
+    ff = SparseProjection(n_in, N, np.arange(n_in), sensory, np.full(n_in, w_in, np.float32),
+                          np.zeros(n_in, dtype=np.int64), cell_type, sf=1.0,
+                          n_source_types=1, n_target_types=n_types)
+    cells = [dict(name=f"type{i}", cell_id=i, tau_mem=TAU_MEM, theta=THETA, U_reset=U_RESET,
+                  E_L=E_L, g_L=G_L, tau_ref=TAU_REF) for i in range(n_types)]
+    kinds = [np.flatnonzero(type_is_e).tolist(), np.flatnonzero(~type_is_e).tolist()]
+    synapses = [
+        dict(name="exc", synapse_id=0, cell_id=kinds[0], tau_rise=0.0, tau_decay=5.0,
+             E_syn=0.0, g_bar=w_e),
+        dict(name="inh", synapse_id=1, cell_id=kinds[1], tau_rise=0.0, tau_decay=10.0,
+             E_syn=-80.0, g_bar=w_i),
+    ]
+    input_synapses = [dict(name="exc", synapse_id=0, cell_id=[0], tau_rise=0.0, tau_decay=5.0,
+                           E_syn=0.0, g_bar=w_e)]
+    model = ConductanceLIFNetwork(
+        dt=float(dt), rec_projections=rec, ff_projections=ff, cell_type_indices=cell_type,
+        cell_type_indices_FF=np.zeros(n_in, dtype=np.int64), cell_params=cells,
+        cell_params_FF=[dict(name="sensory", cell_id=0)], synapse_params=synapses,
+        synapse_params_FF=input_synapses, surrgrad_scale=10.0, batch_size=B,
+    ).to(dev)  # fmt: skip
+    structure = dict(cell_type=cell_type, type_is_e=type_is_e, deg=deg, sensory=sensory,
+                     n_draws=np.array([int(deg.sum())]), sf_row0=sf[0])
+    return Workload("config2", x, structure, model=model, N=N, S=len(model.registry))
+
+
+def many_types(N=600, n_types=20, frac_e_types=0.7, p=0.1, n_in=60, p_in=0.2, rate_hz=20.0,
+               B=2, T=200, dt=0.5, seed=11, input_seed=0, w_e=0.4, w_i=2.0, w_in=8.0,
+               sparse=False, learn_sf=True) -> Workload:
+    """A network of ``n_types`` cell types, more pathways than the kernels accumulate
+    separately: ER connectivity ``p`` with geometric synapse counts (mean 2), one
+    learnable scaling factor per (source type, target type) pair (lognormal(0, 0.3)
+    start), excitatory or inhibitory by type, ``n_in`` Poisson inputs. Two receptor
+    kinds, each one ``synapse_params`` entry listing its cell types (S = 2).
+
+    ``sparse=False``: the reference's form, one ``ScalingFactorProjection`` per pair
+    (``n_types`` recurrent pathways, folded by the engine); ``sparse=True``: the same
+    network as one ``SparseProjection`` (folded by the network). Both forms give each
+    synapse the weight ``count * sf`` (float32)."""
+    from wiretorch_amd.projections import ScalingFactorProjection, SparseProjection
+
+    rng = np.random.default_rng(seed)
+    types = rng.integers(0, n_types, N)
+    is_e = rng.random(n_types) < frac_e_types
+    counts = (rng.geometric(0.5, (N, N)) * (rng.random((N, N)) < p)).astype(np.float32)
+    np.fill_diagonal(counts, 0.0)
+    sf = rng.lognormal(0.0, 0.3, (n_types, n_types)).astype(np.float32)
+    w_inp = (rng.random((n_in, N)) < p_in).astype(np.float32)
+    x = poisson(np.random.default_rng([seed, input_seed]), B, T, np.full(n_in, rate_hz), dt)
+    names = [f"t{i}" for i in range(n_types)]
+    cells = [dict(name=names[i], cell_id=i, tau_mem=TAU_MEM, theta=THETA, U_reset=U_RESET,
+                  E_L=E_L, g_L=G_L, tau_ref=TAU_REF) for i in range(n_types)]
+    synapses = [
+        dict(name="exc", synapse_id=0, cell_id=np.flatnonzero(is_e).tolist(), tau_rise=0.0,
+             tau_decay=5.0, E_syn=0.0, g_bar=w_e),
+        dict(name="inh", synapse_id=1, cell_id=np.flatnonzero(~is_e).tolist(), tau_rise=0.0,
+             tau_decay=10.0, E_syn=-80.0, g_bar=w_i),
+    ]
+    input_synapses = [dict(name="exc", synapse_id=0, cell_id=[0], tau_rise=0.0, tau_decay=5.0,
+                           E_syn=0.0, g_bar=w_e)]
+    if sparse:
+        src, tgt = np.nonzero(counts)
+        rec = SparseProjection(N, N, src, tgt, counts[src, tgt], types, types, sf=sf,
+                               learn_sf=learn_sf, n_source_types=n_types,
+                               n_target_types=n_types)
+        s_in, t_in = np.nonzero(w_inp)
+        ff = SparseProjection(n_in, N, s_in, t_in, w_in * w_inp[s_in, t_in],
+                              np.zeros(n_in, dtype=np.int64), types, sf=1.0,
+                              n_source_types=1, n_target_types=n_types)
+    else:
+        rec, ff = {}, {}
+        for a in range(n_types):
+            for c in range(n_types):
+                block = counts[np.ix_(types == a, types == c)]
+                if block.size and block.any():
+                    rec[(names[a], names[c])] = ScalingFactorProjection(
+                        block, init_sf=float(sf[a, c])) if learn_sf else FrozenProjection(
+                        block * sf[a, c])
+        for c in range(n_types):
+            block = w_in * w_inp[:, types == c]
+            if block.size and block.any():
+                ff[("input", names[c])] = FrozenProjection(block)
+    model = ConductanceLIFNetwork(
+        dt=float(dt), rec_projections=rec, ff_projections=ff, cell_type_indices=types,
+        cell_type_indices_FF=np.zeros(n_in, dtype=np.int64), cell_params=cells,
+        cell_params_FF=[dict(name="input", cell_id=0)], synapse_params=synapses,
+        synapse_params_FF=input_synapses, surrgrad_scale=10.0, batch_size=B,
+    )  # fmt: skip
+    structure = dict(types=types, is_e=is_e, counts=counts, sf=sf, w_inp=w_inp)
+    return Workload("many_types", x, structure, model=model, N=N, S=len(model.registry))
+
+
+def config2(T=2000, B=8, device="cpu", **kwargs) -> Workload:
+    """Configuration 2 (fly scale) through the network API (``fly_scale_network``)."""
+    return fly_scale_network(T=T, B=B, device=device, **kwargs)
 
 
 def sparse_drive(rec: Connectome, ff: Connectome, N: int, dt: float, device="cpu",
