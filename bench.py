@@ -50,16 +50,6 @@ def algorithmic_bytes(B, T, N, S, events):
     return T * (B * N * (8 + 16 * S + 8 + 4) + 24 * N) + 8 * events
 
 
-def delivered_events(spikes, x, drive):
-    """Recurrent spikes x out-degree + input spikes x input out-degree, all trials/steps."""
-    rec, ff = drive.sparse_recurrent, drive.sparse_feedforward
-    out_rec = rec.out_degree().to(spikes.device, torch.float64)
-    out_ff = ff.out_degree().to(x.device, torch.float64)
-    per_src = spikes.double().sum(dim=(0, 1))
-    per_in = (x != 0).double().sum(dim=(0, 1))
-    return float(per_src @ out_rec + per_in @ out_ff)
-
-
 def measured_traffic(summary="wt_cond_run_config2_traffic.md"):
     """HBM bytes per launch of a kernel on its workload, from the committed rocprofv3
     FETCH_SIZE + WRITE_SIZE summary (calibrated against a copy of known size), or None."""
@@ -70,33 +60,6 @@ def measured_traffic(summary="wt_cond_run_config2_traffic.md"):
         if line.startswith("traffic_bytes_per_launch:"):
             return float(line.split(":", 1)[1])
     return None
-
-
-def cpu_baseline(wl, steps):
-    """The oracle (the reference's PyTorch step restated, compressed propagation) on the
-    first ``steps`` steps of the same workload, on this host's cores."""
-    import oracle.dynamics as oracle_engine
-    from wiretorch_amd.synthetic import sparse_drive
-
-    rec = wl.drive.sparse_recurrent.to("cpu")
-    ff = wl.drive.sparse_feedforward.to("cpu")
-    drive, p = sparse_drive(rec, ff, wl.N, 0.1, "cpu")
-    B = wl.x.shape[0]
-    x = torch.from_numpy(wl.x[:, :steps]).float()
-    v, g, c = synthetic.rest_state(B, wl.N, wl.S)
-    with torch.no_grad():
-        oracle_engine.simulate(v, g, x[:, :2], drive, p, refractory=c)  # warm-up
-        t0 = time.perf_counter()
-        oracle_engine.simulate(v, g, x, drive, p, refractory=c)
-        dt = time.perf_counter() - t0
-    return {
-        "value": B * wl.N * steps / dt,
-        "unit": "neuron-steps/s",
-        "cores": torch.get_num_threads(),
-        "kind": "port",
-        "sample": f"oracle on the first {steps} of {wl.x.shape[1]} steps, all {B} trials "
-                  f"({dt:.1f} s)",
-    }
 
 
 def er_events(wl, spikes, x):
@@ -114,7 +77,8 @@ def _part_ms(events):
 
 def _er_cpu_baseline(model, x_np, steps, train):
     """The oracle on the first ``steps`` steps of the same workload (all trials), on a
-    CPU copy of the benchmarked network."""
+    CPU copy of the benchmarked network, with this host's threads; and with one thread
+    (the reference's test setting, ``tests/conftest.py:12``) on an eighth of those steps."""
     import copy
 
     import oracle.dynamics as oracle_engine
@@ -126,29 +90,36 @@ def _er_cpu_baseline(model, x_np, steps, train):
         model._engine = engine_module
     model = cpu_model
     model._engine = oracle_engine
-    x = torch.from_numpy(x_np[:, :steps]).float()
-    B, N = x.shape[0], model.n_neurons
-    model.reset_state()
-    t0 = time.perf_counter()
-    if train:
-        model.zero_grad(set_to_none=True)
-        spikes = model(x)
-        dt = float(model.dt)
-        target = torch.from_numpy(synthetic.gamma_targets(3, N, max(1, int(steps * dt // 20))))
-        synthetic.binned_rate_loss(spikes, target, dt).backward()
-    else:
-        with torch.no_grad():
-            model(x)
-    elapsed = time.perf_counter() - t0
+    B, N = x_np.shape[0], model.n_neurons
     what = "forward + backward" if train else "forward"
-    return {
-        "value": B * N * steps / elapsed,
-        "unit": "neuron-steps/s",
-        "cores": torch.get_num_threads(),
-        "kind": "port",
-        "sample": f"oracle {what} of the first {steps} of {x_np.shape[1]} steps, all {B} "
-                  f"trials ({elapsed:.1f} s)",
-    }
+
+    def timed(n):
+        x = torch.from_numpy(x_np[:, :n]).float()
+        model.reset_state()
+        t0 = time.perf_counter()
+        if train:
+            model.zero_grad(set_to_none=True)
+            spikes = model(x)
+            dt = float(model.dt)
+            target = torch.from_numpy(synthetic.gamma_targets(3, N, max(1, int(n * dt // 20))))
+            synthetic.binned_rate_loss(spikes, target, dt).backward()
+        else:
+            with torch.no_grad():
+                model(x)
+        elapsed = time.perf_counter() - t0
+        return {"value": B * N * n / elapsed, "unit": "neuron-steps/s",
+                "cores": torch.get_num_threads(), "kind": "port",
+                "sample": f"oracle {what} of the first {n} of {x_np.shape[1]} steps, all {B} "
+                          f"trials ({elapsed:.1f} s)"}
+
+    out = timed(steps)
+    threads = torch.get_num_threads()
+    torch.set_num_threads(1)
+    try:
+        out["one_thread"] = timed(max(1, steps // 8))
+    finally:
+        torch.set_num_threads(threads)
+    return out
 
 
 def _line(value, ms_per_step, args, dtype, config, roofline, cpu, **extra):
@@ -163,9 +134,15 @@ def _line(value, ms_per_step, args, dtype, config, roofline, cpu, **extra):
 
 
 def bench_config1(args):
+    """Configuration 1 (or 0, ``--config 0``: 1,000 neurons, one trial, 1,000 steps — a
+    latency-bound case, reported in absolute numbers), forward through the network API."""
     dev = torch.device("cuda:0")
-    T = args.T if args.T != 2000 else 5000
-    wl = synthetic.config1(T=T)
+    if args.config == 0:
+        T = args.T if args.T != 2000 else 1000
+        wl = synthetic.config0(T=T)
+    else:
+        T = args.T if args.T != 2000 else 5000
+        wl = synthetic.config1(T=T)
     model = wl.model.to(dev)
     x = torch.from_numpy(wl.x).float().to(dev)
     B, N = x.shape[0], wl.N
@@ -188,11 +165,12 @@ def bench_config1(args):
     bytes_per_launch = algorithmic_bytes(B, T, N, S, events)
     achieved = bytes_per_launch / (parts["forward"] / 1e3) / 1e9
     rate_hz = float(spikes.mean()) / 0.1e-3
-    print(f"# config1: kernel {parts['forward']:.3f} ms, wall {ms_per_step:.3f} ms/step, "
+    print(f"# config{args.config}: kernel {parts['forward']:.3f} ms, wall {ms_per_step:.3f} ms/step, "
           f"rate {rate_hz:.2f} Hz", file=sys.stderr, flush=True)
     cpu = _er_cpu_baseline(model, wl.x, args.cpu_steps, False) if args.cpu_steps > 0 else None
     _line(B * N * T / (ms_per_step / 1e3), ms_per_step, args, "f32",
-          {"workload": "config1: mid-size conductance-LIF forward", "neurons": N,
+          {"workload": ("config1: mid-size conductance-LIF forward" if args.config == 1 else
+                        "config0: small conductance-LIF forward (latency-bound)"), "neurons": N,
            "synapses": int((wl.structure["w"] != 0).sum()), "batch": B, "time_steps": T,
            "dt_ms": 0.1, "parallelism": "single GPU"},
           {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -462,7 +440,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--cpu-steps", type=int, default=int(os.environ.get("BENCH_CPU_STEPS", 400)))
     ap.add_argument("--T", type=int, default=2000)
-    ap.add_argument("--config", type=int, choices=(1, 2, 3, 4), default=2)
+    ap.add_argument("--config", type=int, choices=(0, 1, 2, 3, 4), default=2)
     ap.add_argument("--filter", action="store_true",
                     help="measure the spike-train loss filter instead of a configuration")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -490,9 +468,9 @@ def main():
         if default_cpu:
             args.cpu_steps = 100
         return bench_config4(args)
-    if args.config == 1:
+    if args.config in (0, 1):
         if default_cpu:
-            args.cpu_steps = 50
+            args.cpu_steps = 50 if args.config == 1 else 1000
         return bench_config1(args)
     if args.config == 3:
         if default_cpu:
@@ -500,40 +478,45 @@ def main():
         return bench_config3(args)
     dev = torch.device("cuda:0")
     t_build = time.perf_counter()
-    wl = synthetic.fly_scale(T=args.T, device=dev)
+    wl = synthetic.config2(T=args.T, device=dev)
+    model = wl.model
     x = torch.from_numpy(wl.x).float().to(dev)
-    drive, p = wl.drive, wl.physiology
     B, T, N, S = x.shape[0], x.shape[1], wl.N, wl.S
-    v0, g0, c0 = synthetic.rest_state(B, N, S, dev)
-    print(f"# built config2 in {time.perf_counter() - t_build:.1f} s: N {N}, "
-          f"{drive.sparse_recurrent.n_edges} synapses, B {B}, T {T}", file=sys.stderr, flush=True)
+    rec, ff = model.rec_projections, model.ff_projections
+    print(f"# built config2 through ConductanceLIFNetwork in {time.perf_counter() - t_build:.1f} s: "
+          f"N {N}, {model.n_cell_types} cell types, {rec.n_edges} synapses, B {B}, T {T}",
+          file=sys.stderr, flush=True)
 
     def step():
-        return engine.simulate(v0, g0, x, drive, p, refractory=c0)
+        model.reset_state()
+        return model(x)
 
     with torch.no_grad():
         for _ in range(args.warmup):
-            run = step()
+            spikes = step()
         torch.cuda.synchronize()
         engine.LAUNCH_EVENTS = []
         t0 = time.perf_counter()
         for _ in range(args.steps):
-            run = step()
+            spikes = step()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         launches = engine.LAUNCH_EVENTS
         engine.LAUNCH_EVENTS = None
     kernel_ms = float(np.mean([a.elapsed_time(b) for a, b in launches]))
-    events = delivered_events(run.spikes, x, drive)
+    out_rec = (rec.indptr[1:] - rec.indptr[:-1]).double()
+    out_ff = (ff.indptr[1:] - ff.indptr[:-1]).double()
+    events = float(spikes.double().sum(dim=(0, 1)) @ out_rec
+                   + (x != 0).double().sum(dim=(0, 1)) @ out_ff)
     ms_per_step = wall * 1e3 / args.steps
     neuron_steps = B * N * T
     value = neuron_steps / (ms_per_step / 1e3)
     bytes_per_launch = algorithmic_bytes(B, T, N, S, events)
     achieved = bytes_per_launch / (kernel_ms / 1e3) / 1e9
-    rate_hz = float(run.spikes.mean()) / (0.1e-3)
+    rate_hz = float(spikes.mean()) / (0.1e-3)
     print(f"# kernel {kernel_ms:.3f} ms/launch, wall {ms_per_step:.3f} ms/step, "
           f"rate {rate_hz:.2f} Hz, events/step {events / T:.0f}", file=sys.stderr, flush=True)
-    cpu = cpu_baseline(wl, args.cpu_steps) if args.cpu_steps > 0 else None
+    cpu = _er_cpu_baseline(model, wl.x, args.cpu_steps, False) if args.cpu_steps > 0 else None
     line = {
         "metric": METRIC,
         "value": value,
@@ -551,8 +534,9 @@ def main():
         "mean_rate_hz": rate_hz,
         "config": {
             "workload": "config2: fly-scale conductance-LIF forward",
-            "neurons": N, "synapses": int(drive.sparse_recurrent.n_edges),
-            "cell_types": 8000, "batch": B, "time_steps": T, "dt_ms": 0.1,
+            "neurons": N, "synapses": int(rec.n_edges),
+            "cell_types": int(model.n_cell_types), "batch": B, "time_steps": T, "dt_ms": 0.1,
+            "built": "ConductanceLIFNetwork, SparseProjection sides",
             "parallelism": "single GPU",
         },
         "roofline": {

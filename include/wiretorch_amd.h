@@ -75,12 +75,17 @@ typedef struct {
  * b = g, g+groups, ...; workgroup slot r of a group owns targets [r*range_n, ...);
  * range_n is a multiple of 32, and a workgroup owns at most 8192 (trial, neuron) items.
  * frac_bits: activations are accumulated exactly as int64 multiples of 2^-frac_bits.
+ * bound: NULL, or a device pointer to the largest magnitude any activation can reach
+ * (per-target sums of |weight| times the largest |input|); then the kernel derives
+ * frac_bits itself, min(40, 51 - ceil(log2 bound)) (40 for a bound of 0), so the host
+ * need not read the bound back, and the frac_bits field is ignored.
  * max_list: the per-workgroup event list, 1024 or 2048 entries (0 = the largest that
  * fits in LDS; 2048 needs at most 4096 items per workgroup and room beside the
  * accumulator). A step's events beyond the list are pushed in further rounds; results do
  * not depend on it. */
 typedef struct {
   int64_t groups, R, range_n, frac_bits, max_list;
+  const double* bound;
 } wt_geometry;
 
 /* wt_split_ranges — (re)build side->split for R target ranges of range_n targets

@@ -34,7 +34,7 @@ def _run(model, x, entry):
     counter = model.refractory.detach().clone()
     spikes = torch.full((B, T, N), -1.0, device=DEV)
     groups, R, range_n = L.geo
-    geo = _lib.Geometry(groups, R, range_n, L.frac_bits, L.max_list)
+    geo = L.abi_geometry()
     io = _lib.RunIO(x.data_ptr(), B, T, L.n_in, v.data_ptr(), g.data_ptr(),
                     counter.data_ptr() if L.refractory else None, spikes.data_ptr(),
                     None, None, None, None, None, None, None, None, 0)
@@ -73,7 +73,7 @@ def test_noalloc_refuses_a_workspace_beyond_its_array():
     model, x = _inputs(wl, 2, 40)
     L = engine._plan(model.v, x, model._drive(), model._physiology(), False, False, None)
     groups, R, range_n = L.geo
-    geo = _lib.Geometry(groups, R, range_n, L.frac_bits, L.max_list)
+    geo = L.abi_geometry()
     lib = _lib.load()
     T_big = 1_000_000  # input lists alone: 2 * 1e6 * 516 bytes, past the array
     assert lib.wt_cond_run_scratch_bytes(geo, 2, T_big) > _lib.NOALLOC_SCRATCH_BYTES

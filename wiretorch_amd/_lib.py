@@ -35,7 +35,7 @@ class Side(ctypes.Structure):
 
 class Geometry(ctypes.Structure):
     _fields_ = [("groups", I64), ("R", I64), ("range_n", I64), ("frac_bits", I64),
-                ("max_list", I64)]
+                ("max_list", I64), ("bound", P)]
 
 
 class RunIO(ctypes.Structure):

@@ -384,7 +384,7 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
     return hipErrorInvalidValue;
   if (geo->groups < 1 || geo->groups > kMaxGroups || geo->R < 1 || geo->R > 256 ||
       geo->range_n < 32 || geo->range_n % 32 != 0 || geo->R * geo->range_n < tab->N ||
-      geo->frac_bits < 0 || geo->frac_bits > 60 || geo->max_list < 0 ||
+      (!geo->bound && (geo->frac_bits < 0 || geo->frac_bits > 60)) || geo->max_list < 0 ||
       geo->max_list > kMaxList || geo->max_list % kRunBlock != 0)
     return hipErrorInvalidValue;
   const int64_t tpg = run_tpg_max(geo, io->B);

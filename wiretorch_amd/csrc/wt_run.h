@@ -50,6 +50,7 @@ struct RunArgs {
 // rest of the workgroup's update, publication + event compaction + arrival, the barrier
 // wait, range lookups + scan + synapse push.
 constexpr int kPhases = 8;
+constexpr int kMaxFracBits = 40;  // fractional bits of the exact accumulators at most
 constexpr int kInCap = 64;  // inputs listed per (trial, step); denser rows are scanned
 constexpr int kMaxLdsTypes = 256;
 constexpr int kTypeCols = 6;  // global table: theta, U_reset, E_L, C_m, beta, n_ref; scale[K]
@@ -159,6 +160,20 @@ struct Fixed {
   float scale;  // 2^f
   double inv;   // 2^-f
 };
+// Fractional bits for activations of magnitude at most `bound`: every per-target sum
+// stays below 2^51 / 2^f, so the float64 accumulators stay exact (the host's rule, from a
+// bound the host need not read back). ceil(log2 bound) from the exponent: bound = m 2^e
+// with m in [0.5, 1) is below 2^e, and exactly 2^(e-1) when m = 0.5.
+__device__ inline int frac_bits_of(double bound) {
+  if (!(bound > 0.0)) return bound == 0.0 ? kMaxFracBits : 0;  // NaN: the coarsest
+  if (isinf(bound)) return 0;
+  int e = 0;
+  const double m = frexp(bound, &e);
+  const int up = m == 0.5 ? e - 1 : e;
+  const int f = 51 - up;
+  return f < 0 ? 0 : (f > kMaxFracBits ? kMaxFracBits : f);
+}
+
 __device__ inline void add_fixed(double* cell, float x, Fixed fx) {
   atomicAdd(cell, (double)rintf(x * fx.scale) * fx.inv);
 }
@@ -364,7 +379,8 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   const bool recurrent = A.tab.K_rec > 0 && A.rec.n_src > 0;
   const bool has_ff = A.ff.n_src > 0;
   const float dt = *A.tab.dt;
-  const Fixed fx{ldexpf(1.0f, (int)A.geo.frac_bits), ldexp(1.0, -(int)A.geo.frac_bits)};
+  const int frac = A.geo.bound ? frac_bits_of(*A.geo.bound) : (int)A.geo.frac_bits;
+  const Fixed fx{ldexpf(1.0f, frac), ldexp(1.0, -frac)};
   // the event list and its entry map
   constexpr int kList = BIG ? kMaxList : kRunBlock;
   __shared__ int64_t s_e0[kList];

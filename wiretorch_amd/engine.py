@@ -39,7 +39,6 @@ from wiretorch_amd.network import Drive, Physiology, Run
 
 #: Physiology the backward pass can differentiate, in ``Physiology`` names.
 PHYSIOLOGY = ("theta", "U_reset", "E_L", "C_m", "beta", "E_syn", "decay", "jump")
-MAX_FRAC_BITS = 40
 BLOCK = 1024
 #: Upper limit on trial groups (the kernel takes up to 64); ``geometry`` picks the count.
 MAX_GROUPS = 64
@@ -111,7 +110,8 @@ class _Side:
     #: For a side built from dense pathways: each source's row within its pathway.
     row_local: torch.Tensor | None = None
     dense_shapes: tuple = ()
-    max_in_sum: float = 0.0
+    #: the largest per-target sum of |weight| (0-d float64 on the device; 0 when empty)
+    max_in_sum: object = 0.0
     #: For a side built from dense pathways: per pathway, its edges (positions in edge
     #: order, a slice where they are consecutive) and their flat indices into the
     #: pathway's (rows, N) weight matrix.
@@ -212,12 +212,13 @@ def _empty_side(device) -> _Side:
     return _Side(conn, torch.zeros(1, dtype=torch.int32, device=device))
 
 
-def _max_in_sum(conn: Connectome, order=None) -> float:
-    """The largest per-target sum of |weight|, in float64: by atomic adds, or, given the
-    edges in target order (``_Side.target_order``), as differences of a running sum at
-    the targets' boundaries (no atomics: a few hundred edges share each target)."""
+def _max_in_sum(conn: Connectome, order=None) -> torch.Tensor:
+    """The largest per-target sum of |weight|, a 0-d float64 tensor on the connectome's
+    device (never read back by the host): by atomic adds, or, given the edges in target
+    order (``_Side.target_order``), as differences of a running sum at the targets'
+    boundaries (no atomics: a few hundred edges share each target)."""
     if conn.n_edges == 0:
-        return 0.0
+        return torch.zeros((), dtype=torch.float64, device=conn.device)
     w = conn.weights.detach()
     if order is None:
         per_target = torch.zeros(conn.n_targets, dtype=torch.float64, device=conn.device)
@@ -227,7 +228,7 @@ def _max_in_sum(conn: Connectome, order=None) -> float:
         running = torch.zeros(conn.n_edges + 1, dtype=torch.float64, device=conn.device)
         torch.cumsum(w[edge].abs().double(), 0, out=running[1:])
         per_target = running[indptr[1:]] - running[indptr[:-1]]
-    return float(per_target.max())
+    return per_target.max()
 
 
 def _from_connectome(conn: Connectome, device) -> _Side:
@@ -384,12 +385,17 @@ _GROUP_ROWS: OrderedDict = OrderedDict()
 
 
 def _group_order(made: torch.Tensor, ks: range) -> list[list[int]]:
-    """Pathways ``ks`` grouped by their row of ``made`` (first appearance first)."""
-    groups: dict[bytes, list[int]] = {}
-    rows = made.detach().to("cpu", torch.bool).numpy()
-    for k in ks:
-        groups.setdefault(rows[k].tobytes(), []).append(k)
-    return list(groups.values())
+    """Pathways ``ks`` grouped by their row of ``made`` (first appearance first); cached
+    per ``made`` tensor (reading it back is a host synchronisation)."""
+
+    def make():
+        groups: dict[bytes, list[int]] = {}
+        rows = made.detach().to("cpu", torch.bool).numpy()
+        for k in ks:
+            groups.setdefault(rows[k].tobytes(), []).append(k)
+        return list(groups.values())
+
+    return _cached(("groups", ks.start, ks.stop) + _key(made), (made,), make)
 
 
 def fold_pathways(drive: Drive) -> Drive:
@@ -529,13 +535,12 @@ def geometry(B: int, N: int, K: int, n_cu: int, max_lds: int) -> tuple[int, int,
         groups = groups // 2  # more workgroups per group for a larger network
 
 
-def _frac_bits(bound: float) -> int:
-    """Fractional bits of the fixed-point accumulator: every per-target sum stays below
-    2^51 / 2^frac, so the int64 accumulators stay below 2^53 (with each product's
-    rounding) and convert to float exactly once."""
-    if bound <= 0:
-        return MAX_FRAC_BITS
-    return max(0, min(MAX_FRAC_BITS, 51 - math.ceil(math.log2(bound))))
+def _device_scalar(value, device) -> torch.Tensor:
+    """A 0-d float64 tensor on ``device`` (a bound computed there, or a host zero)."""
+    if isinstance(value, torch.Tensor):
+        return value
+    return _cached(("zero", str(device)), (), lambda: torch.zeros((), dtype=torch.float64,
+                                                                   device=device))
 
 
 def _type_table(tables: dict, scale: torch.Tensor, device):
@@ -595,7 +600,8 @@ class _Plan:
     rec: _Side
     ff: _Side
     geo: tuple
-    frac_bits: int
+    #: 0-d float64 device tensor: the largest |activation| (the kernel's fixed point)
+    bound: torch.Tensor
     max_list: int
     refractory: bool
     probabilities: bool
@@ -609,6 +615,10 @@ class _Plan:
     @property
     def K(self) -> int:
         return self.K_rec + self.K_ff
+
+    def abi_geometry(self) -> _lib.Geometry:
+        groups, R, range_n = self.geo
+        return _lib.Geometry(groups, R, range_n, -1, self.max_list, self.bound.data_ptr())
 
     def abi_tables(self, scale: torch.Tensor) -> _lib.Tables:
         t = self.tables
@@ -647,11 +657,14 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
     groups, R, range_n = geometry(B, N, K_rec + K_ff, n_cu, max_lds)
     dt_ms = _cached(("dt",) + _key(p.dt), (p.dt,), lambda: float(p.dt))
     max_list = _list_size(B, N, groups, dt_ms)
-    bound = rec.max_in_sum
+    # the accumulators' bound stays on the device: the kernel derives its fractional bits
+    bound = _device_scalar(rec.max_in_sum, device)
     if ff.n_src and ff.conn.n_edges:
         xd = x.detach()
-        x_max = _cached(("x_max",) + _key(xd), (xd,), lambda: float(xd.abs().max()))
-        bound += ff.max_in_sum * x_max
+        x_max = _cached(("x_max",) + _key(xd), (xd,), lambda: xd.abs().max().double())
+        ff_max = _device_scalar(ff.max_in_sum, device)
+        bound = _cached(("bound",) + _key(bound, ff_max, x_max), (bound, ff_max, x_max),
+                        lambda: bound + ff_max * x_max)
     names = ("theta", "U_reset", "E_L", "C_m", "beta", "E_syn", "g_clip", "decay", "jump")
     sources = tuple(getattr(p, name) for name in names) + (
         drive.made, drive.scale, p.dt, p.surr_scale, p.n_ref)
@@ -670,7 +683,7 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
     tables = _cached(("tables", str(device)) + _key(*sources), sources, make_tables)
     return _Plan(
         B=B, T=T, N=N, S=S, K_rec=K_rec, K_ff=K_ff, n_in=n_in, tables=tables, rec=rec,
-        ff=ff, geo=(groups, R, range_n), frac_bits=_frac_bits(bound), max_list=max_list,
+        ff=ff, geo=(groups, R, range_n), bound=bound, max_list=max_list,
         refractory=p.n_ref is not None, probabilities=probabilities, track=track,
         track_b=(-1 if track_batch_idx is None else int(track_batch_idx)) if track else 0,
         stream=torch.cuda.current_stream(device).cuda_stream, device=device,
@@ -680,7 +693,7 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
 def _launch(L: _Plan, x, scale, v, g, counter, spikes, prob, saved, tracked,
             rec_weights=None, ff_weights=None) -> None:
     groups, R, range_n = L.geo
-    geo = _lib.Geometry(groups, R, range_n, L.frac_bits, L.max_list)
+    geo = L.abi_geometry()
     lib = _lib.load()
     scratch = torch.empty(int(lib.wt_cond_run_scratch_bytes(geo, L.B, L.T)),
                           dtype=torch.uint8, device=L.device)
@@ -715,9 +728,40 @@ def _launch(L: _Plan, x, scale, v, g, counter, spikes, prob, saved, tracked,
     if LAUNCH_EVENTS is not None:
         stop.record()
         LAUNCH_EVENTS.append((start, stop))
-    flags = int(scratch[:4].view(torch.int32).item())
-    if flags:
-        raise RuntimeError(f"wt_cond_run: a workgroup barrier timed out (flags {flags:#x})")
+    _watch(scratch[:4].view(torch.int32))
+
+
+#: Error words of launches not yet checked: (event after the copy, pinned host word).
+_PENDING: list = []
+
+
+def _watch(word: torch.Tensor) -> None:
+    """Copy a launch's error word to pinned host memory without waiting for it; it is
+    checked once the copy has landed (``check_errors``, run at the start of every call
+    and of every backward), so the host never stalls on the GPU here."""
+    host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+    host.copy_(word, non_blocking=True)
+    done = torch.cuda.Event()
+    done.record()
+    _PENDING.append((done, host))
+
+
+def check_errors(wait: bool = False) -> None:
+    """Raise if an earlier launch reported an error (a group barrier that timed out):
+    checks every launch whose error word has reached the host (with ``wait``, waits for
+    all of them)."""
+    still = []
+    failed = 0
+    for done, host in _PENDING:
+        if wait:
+            done.synchronize()
+        elif not done.query():
+            still.append((done, host))
+            continue
+        failed |= int(host[0])
+    _PENDING[:] = still
+    if failed:
+        raise RuntimeError(f"wt_cond_run: a workgroup barrier timed out (flags {failed:#x})")
 
 
 # =====================================================================
@@ -755,6 +799,7 @@ class _Run(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_spikes, grad_prob, _v, _g, _c):
+        check_errors(wait=True)  # the forward this backward differentiates is complete
         L, n_rec_w = ctx.L, ctx.n_rec_w
         scale, x, spikes, v_saved, G_saved, held, A_saved, g_init, *weights = ctx.saved_tensors
         needs = ctx.needs_input_grad
@@ -915,6 +960,7 @@ def simulate(
     """Simulate ``x.shape[1]`` steps from ``(v, g)`` on the GPU; see the module docstring."""
     if not x.is_cuda:
         raise RuntimeError(f"the HIP engine runs on a GPU; the input is on {x.device}")
+    check_errors()
     if retain is not None:
         raise NotImplementedError("per-step gradient retention (track_gradients)")
     if gating is not None or drive.gates or adaptation is not None or p.adapt is not None:

@@ -313,6 +313,12 @@ class ProjectionNetwork(nn.Module):
             self.register_buffer(side.mask_buffer, torch.from_numpy(self._mask(side)))
         self._register_physiology()
         self.pathways = self._build_pathways()
+        # what every call's Drive shares while nothing is learnt in it (the same tensors
+        # each call, so the engine's tables built from them are reused)
+        order = [p.index for p in self.pathways]
+        self.register_buffer("_made_in_order", self._made[order].clone(), persistent=False)
+        self.register_buffer("_unit_scale", torch.ones((len(order), self.n_neurons)),
+                             persistent=False)
         self.set_timestep(float(dt))
 
     # ------------------------------------------------------------------
@@ -463,7 +469,8 @@ class ProjectionNetwork(nn.Module):
     def _drive(self) -> Drive:
         """Per pathway: rows, current weights and kernel scale (``network.py:816-854``)."""
         scaling, assembled = {}, {}
-        ones = torch.ones(self.n_neurons, **self._float)
+        unit = self._unit_scale.to(self.dt.dtype)
+        ones = unit[0] if unit.shape[0] else torch.ones(self.n_neurons, **self._float)
         scales, recurrent, feedforward = [], [], []
         sparse = {}
         for pathway in self.pathways:
@@ -490,10 +497,13 @@ class ProjectionNetwork(nn.Module):
             rows = getattr(self, f"_rows_{pathway.index}")
             target = recurrent if self._sides[pathway.side].recurrent else feedforward
             target.append((rows, W))
-        order = [p.index for p in self.pathways]
+        if any(p.mode == "scaling_factors" for p in self.pathways):
+            scale = torch.stack(scales)
+        else:  # every kernel scale is 1: the same tensor each call
+            scale = unit
         return Drive(
-            made=self._made[order],
-            scale=torch.stack(scales) if scales else ones.new_zeros((0, self.n_neurons)),
+            made=self._made_in_order,
+            scale=scale,
             recurrent=recurrent,
             feedforward=feedforward,
             differentiable_inputs=self.differentiable_inputs,
