@@ -16,6 +16,8 @@ classes, parameterisations and caching modes) and ``:340-392``
 
 from __future__ import annotations
 
+from pathlib import Path
+
 import numpy as np
 import torch
 from torch import nn
@@ -222,6 +224,10 @@ def projection_mask(projection: Projection) -> np.ndarray:
 # ====================================================================
 
 
+#: Format tag of the ``.npz`` archives ``SparseProjection.save`` writes.
+SPARSE_FORMAT = "wiretorch_amd.sparse_projection/1"
+
+
 class SparseProjection(nn.Module):
     """Every synapse of one input side, compressed by source, with one scaling factor per
     (source cell type, target cell type) pair.
@@ -317,6 +323,56 @@ class SparseProjection(nn.Module):
     def _apply(self, fn, recurse=True):
         self._memo = None  # device or dtype moves invalidate the reused weights
         return super()._apply(fn, recurse)
+
+    def save(self, path):
+        """Write the connectome and the current factors to ``path`` (``.npz``, plain
+        arrays): ``SparseProjection.load`` rebuilds the projection without re-sorting."""
+        path = Path(path)
+        np.savez(
+            path, format=np.array(SPARSE_FORMAT), n_source=np.int64(self.n_source),
+            n_target=np.int64(self.n_target), n_source_types=np.int64(self.n_source_types),
+            n_target_types=np.int64(self.n_target_types),
+            indptr=self.indptr.cpu().numpy(), targets=self.targets.cpu().numpy(),
+            counts=self.counts.cpu().numpy(), pair=self.pair.cpu().numpy(),
+            sf=self.factors().detach().cpu().numpy(),
+            **({"log_sf": self.log_sf.detach().cpu().numpy()} if hasattr(self, "log_sf") else {}),
+        )  # fmt: skip
+        return path if path.suffix == ".npz" else path.with_name(path.name + ".npz")
+
+    @classmethod
+    def load(cls, path, learn_sf: bool = False, device="cpu") -> "SparseProjection":
+        """A projection written by ``save`` (its factors learnt from there if ``learn_sf``)."""
+        from wiretorch_amd.connectome import check_structure
+
+        with np.load(Path(path), allow_pickle=False) as f:
+            if str(f["format"]) != SPARSE_FORMAT:
+                raise ValueError(f"{path}: not a {SPARSE_FORMAT} archive")
+            arrays = {k: f[k] for k in ("indptr", "targets", "counts", "pair", "sf")}
+            log_sf = f["log_sf"] if "log_sf" in f.files else None
+            sizes = {k: int(f[k]) for k in ("n_source", "n_target", "n_source_types",
+                                             "n_target_types")}
+        n_src, n_tgt = sizes["n_source"], sizes["n_target"]
+        check_structure(n_src, n_tgt, arrays["indptr"], arrays["targets"], arrays["counts"],
+                        np.zeros(n_src, dtype=np.int64), 1)
+        n_pairs = sizes["n_source_types"] * sizes["n_target_types"]
+        if arrays["sf"].shape != (sizes["n_source_types"], sizes["n_target_types"]) or (
+                arrays["pair"].size and (arrays["pair"].min() < 0 or arrays["pair"].max() >= n_pairs)):
+            raise ValueError(f"{path}: scaling factors or pair indices do not match")
+        self = cls.__new__(cls)
+        nn.Module.__init__(self)
+        self.n_source, self.n_target = n_src, n_tgt
+        self.n_source_types, self.n_target_types = sizes["n_source_types"], sizes["n_target_types"]
+        for name in ("indptr", "targets", "counts", "pair"):
+            self.register_buffer(name, torch.from_numpy(arrays[name]).to(device))
+        table = torch.from_numpy(arrays["sf"]).float().to(device)
+        if learn_sf and log_sf is not None:  # the learnt logarithms themselves
+            self.log_sf = nn.Parameter(torch.from_numpy(log_sf).float().to(device))
+        elif learn_sf:
+            self.log_sf = nn.Parameter(torch.log(table.double() + 1e-8).float())
+        else:
+            self.register_buffer("sf", table)
+        self._memo = None
+        return self
 
     def dense(self) -> torch.Tensor:
         """``(n_source, n_target)`` weights, for small networks (tests, inspection)."""
