@@ -301,6 +301,17 @@ int wt_rate_backward(const wt_rate_tables* tab, const wt_rate_operand* op,
  * speed. No counterpart in the reference. n floats; x, hi, lo 16-byte aligned. */
 int wt_split_bf16(const float* x, int64_t n, void* hi, void* lo, wt_stream_t stream);
 
+/* wt_gemm_tn_split — C (M x N) = A^T B, or C += A^T B with accumulate != 0, for float32
+ * A (K x M, row pitch lda), B (K x N, pitch ldb), C (pitch ldc), all row-major: the rate
+ * networks' weight gradient sum over (trial, step) of rates x dL/da, a float32 product in
+ * the reference (rate/engine.py:365-377). Each operand element is split in registers into
+ * bf16 hi + lo (x = hi + lo to 2^-18) and the product taken as hi.hi + hi.lo + lo.hi on
+ * the bf16 matrix cores with float32 accumulation: every term within 3 * 2^-18 of
+ * |a_k b_k|. Deterministic. */
+int wt_gemm_tn_split(const float* A, int64_t lda, const float* B, int64_t ldb, float* C,
+                     int64_t ldc, int64_t K, int64_t M, int64_t N, int32_t accumulate,
+                     wt_stream_t stream);
+
 /* wt_edge_sources — edge_src[e] = the source of edge e (E = indptr[n_src]). */
 int wt_edge_sources(const int64_t* indptr, int64_t n_src, int64_t* edge_src,
                     wt_stream_t stream);

@@ -163,20 +163,26 @@ def test_split_bf16_matches_torch_rounding(n):
     assert torch.equal(lo.view(torch.int16), want_lo.view(torch.int16))
 
 
-@pytest.mark.parametrize("K", [300, 65_536])
-def test_split_product_error_bound(K):
-    """The weight gradient's product a^T b from bf16 (hi, lo) pairs: every entry within
-    3 * 2^-18 of sum |a_i b_i| of the float64 product, on top of float32 accumulation
-    (twice the float32 product's own distance to float64: both accumulate in float32, in
-    orders of their own), for a short (300) and a long (65,536) sum — no absolute
-    floor."""
-    from wiretorch_amd.rate_engine import _split, _split_product
+@pytest.mark.parametrize("K, M, N", [(300, 192, 160), (65_536, 192, 160), (1000, 512, 512),
+                                     (4133, 300, 700), (777, 301, 157)])
+def test_split_product_error_bound(K, M, N):
+    """The weight gradient's product a^T b on the bf16 matrix cores (``wt_gemm_tn_split``:
+    operands split in registers into bf16 hi + lo): every entry within 3 * 2^-18 of
+    sum |a_i b_i| of the float64 product, on top of float32 accumulation (twice the
+    float32 product's own distance to float64: both accumulate in float32, in orders of
+    their own), for short and long sums, whole and partial 256 x 256 tiles, a K that is
+    no multiple of the 32-step stage and odd widths — no absolute floor."""
+    from wiretorch_amd.rate_engine import _gemm_tn
     g = torch.Generator(device=DEV).manual_seed(5)
-    a = torch.tanh(torch.randn((K, 192), device=DEV, generator=g))
-    b = torch.randn((K, 160), device=DEV, generator=g) * 1e-3
+    a = torch.tanh(torch.randn((K, M), device=DEV, generator=g))
+    b = torch.randn((K, N), device=DEV, generator=g) * 1e-3
     exact = a.double().T @ b.double()
     magnitude = a.double().abs().T @ b.double().abs()
     f32 = (a.T @ b).double()
-    split = _split_product(*_split(a), *_split(b)).double()
+    split = _gemm_tn(a, b).double()
     allowed = 3 * 2.0**-18 * magnitude + 2 * (f32 - exact).abs().max()
     assert bool(((split - exact).abs() <= allowed).all()), float(((split - exact).abs() - allowed).max())
+    # strided views (row pitch above the width) give the same result
+    wide_a = torch.zeros((K, M + 37), device=DEV)
+    wide_a[:, :M] = a
+    assert torch.equal(_gemm_tn(wide_a[:, :M], b), _gemm_tn(a, b))

@@ -114,6 +114,8 @@ SIGNATURES = {
                                         ctypes.POINTER(RateOperand),
                                         ctypes.POINTER(RateBackIO), P]),
     "wt_edge_sources": (ctypes.c_int, [P, I64, P, P]),
+    "wt_gemm_tn_split": (ctypes.c_int, [P, I64, P, I64, P, I64, I64, I64, I64, ctypes.c_int32,
+                                        P]),
     "wt_split_bf16": (ctypes.c_int, [P, I64, P, P, P]),
     "wt_events_scratch_bytes": (I64, [I64, I64]),
     "wt_events_count": (ctypes.c_int, [P, I64, I64, P, P, P]),

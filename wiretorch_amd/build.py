@@ -17,7 +17,8 @@ from pathlib import Path
 PACKAGE = Path(__file__).resolve().parent
 LIBRARY = PACKAGE / "libwiretorch_amd.so"
 CSRC = PACKAGE / "csrc"
-SOURCES = ([CSRC / "wt_kernels.hip", CSRC / "wt_rate.hip", CSRC / "wt_filter.hip"]
+SOURCES = ([CSRC / "wt_kernels.hip", CSRC / "wt_rate.hip", CSRC / "wt_filter.hip",
+            CSRC / "wt_gemm.hip"]
            + [CSRC / f"wt_run_s{s}.hip" for s in range(1, 9)])
 OBJ_DIR = PACKAGE / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -289,15 +289,23 @@ def _split(x: torch.Tensor):
     return hi, lo
 
 
-def _split_product(a_hi, a_lo, b_hi, b_lo) -> torch.Tensor:
-    """``a^T b`` of float32 matrices given as bf16 (hi, lo) pairs: hi.hi + hi.lo + lo.hi on
-    the matrix cores, float32 accumulation and output. Each operand is hi + lo to 2^-18
-    relative and the dropped lo.lo is below 2^-18 of the product, so each product is off
-    by at most 3 * 2^-18 of |a_i b_i| (float32's product: 2^-24) before the float32
-    accumulation, which both products share."""
-    C = torch.mm(a_hi.T, b_hi, out_dtype=torch.float32)
-    C = torch.addmm(C, a_hi.T, b_lo, out_dtype=torch.float32)
-    return torch.addmm(C, a_lo.T, b_hi, out_dtype=torch.float32)
+def _gemm_tn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """``a^T b`` of float32 ``(K, M)`` and ``(K, N)`` matrices on the bf16 matrix cores
+    (``wt_gemm_tn_split``): each operand split in registers into bf16 hi + lo, the product
+    hi.hi + hi.lo + lo.hi accumulated in float32 — every term within 3 * 2^-18 of its
+    float32 value (float32's product: 2^-24), before the float32 accumulation both share."""
+    a, b = a.float(), b.float()
+    if a.stride(1) != 1:
+        a = a.contiguous()
+    if b.stride(1) != 1:
+        b = b.contiguous()
+    K, M = a.shape
+    N = b.shape[1]
+    C = torch.empty((M, N), dtype=torch.float32, device=a.device)
+    _lib.check(_lib.load().wt_gemm_tn_split(
+        a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), C.data_ptr(), N, K, M, N, 0,
+        torch.cuda.current_stream(a.device).cuda_stream), "wt_gemm_tn_split")
+    return C
 
 
 def _weight_and_input_grads(L: _Plan, out, x, grad_A, weights, w_needs, want_x):
@@ -313,7 +321,7 @@ def _weight_and_input_grads(L: _Plan, out, x, grad_A, weights, w_needs, want_x):
         if L.op.dtype == torch.float32:  # the reference's precision: its float32 product
             grad_w[k] = pre.T @ g
         else:  # reduced-precision storage: the split product on the bf16 matrix cores
-            grad_w[k] = _split_product(*_split(pre), *_split(g))
+            grad_w[k] = _gemm_tn(pre, g)
     grad_x = torch.zeros_like(x, dtype=torch.float32) if want_x else None
     for j, (rows, W) in enumerate(zip(L.rows_ff, weights[L.K_rec:])):
         k = L.K_rec + j
