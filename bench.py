@@ -441,6 +441,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=int(os.environ.get("BENCH_CPU_STEPS", 400)))
     ap.add_argument("--T", type=int, default=2000)
     ap.add_argument("--config", type=int, choices=(0, 1, 2, 3, 4), default=2)
+    ap.add_argument("--poisson", action="store_true",
+                    help="configuration 2 with its input drawn on the device")
     ap.add_argument("--filter", action="store_true",
                     help="measure the spike-train loss filter instead of a configuration")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -480,7 +482,13 @@ def main():
     t_build = time.perf_counter()
     wl = synthetic.config2(T=args.T, device=dev)
     model = wl.model
-    x = torch.from_numpy(wl.x).float().to(dev)
+    if args.poisson:  # the 10 Hz sensory drive drawn inside the forward (no input tensor)
+        from wiretorch_amd.inputs import PoissonInput
+
+        x = PoissonInput(np.full(model.n_inputs, 10.0), 0.1, wl.x.shape[0], wl.x.shape[1],
+                         seed=2)
+    else:
+        x = torch.from_numpy(wl.x).float().to(dev)
     B, T, N, S = x.shape[0], x.shape[1], wl.N, wl.S
     rec, ff = model.rec_projections, model.ff_projections
     print(f"# built config2 through ConductanceLIFNetwork in {time.perf_counter() - t_build:.1f} s: "
@@ -506,8 +514,9 @@ def main():
     kernel_ms = float(np.mean([a.elapsed_time(b) for a, b in launches]))
     out_rec = (rec.indptr[1:] - rec.indptr[:-1]).double()
     out_ff = (ff.indptr[1:] - ff.indptr[:-1]).double()
+    x_dense = x.materialize() if args.poisson else x
     events = float(spikes.double().sum(dim=(0, 1)) @ out_rec
-                   + (x != 0).double().sum(dim=(0, 1)) @ out_ff)
+                   + (x_dense != 0).double().sum(dim=(0, 1)) @ out_ff)
     ms_per_step = wall * 1e3 / args.steps
     neuron_steps = B * N * T
     value = neuron_steps / (ms_per_step / 1e3)
@@ -516,7 +525,8 @@ def main():
     rate_hz = float(spikes.mean()) / (0.1e-3)
     print(f"# kernel {kernel_ms:.3f} ms/launch, wall {ms_per_step:.3f} ms/step, "
           f"rate {rate_hz:.2f} Hz, events/step {events / T:.0f}", file=sys.stderr, flush=True)
-    cpu = _er_cpu_baseline(model, wl.x, args.cpu_steps, False) if args.cpu_steps > 0 else None
+    x_cpu = x.replay() if args.poisson else wl.x
+    cpu = _er_cpu_baseline(model, x_cpu, args.cpu_steps, False) if args.cpu_steps > 0 else None
     line = {
         "metric": METRIC,
         "value": value,
@@ -537,6 +547,8 @@ def main():
             "neurons": N, "synapses": int(rec.n_edges),
             "cell_types": int(model.n_cell_types), "batch": B, "time_steps": T, "dt_ms": 0.1,
             "built": "ConductanceLIFNetwork, SparseProjection sides",
+            "input": ("Poisson drawn on the device (Philox4x32-10)" if args.poisson
+                      else "spike tensor resident in HBM"),
             "parallelism": "single GPU",
         },
         "roofline": {

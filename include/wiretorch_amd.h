@@ -98,7 +98,8 @@ int wt_split_ranges(const int64_t* indptr, const int32_t* targets, int64_t n_src
  * K_rec = 0) and the per-step pair network_simulators/kernels.py:133-204
  * compact_spikes + conductance/kernels.py:572-700 recurrent_step launched by the host
  * loop conductance/engine.py:306-355 — here one persistent launch for all T steps.
- *   x (B,T,n_in) f32 input; rec/ff: recurrent side (sources = the N neurons) and
+ *   x (B,T,n_in) f32 input (or NULL with in_prob: on-device Poisson input); rec/ff:
+ *   recurrent side (sources = the N neurons) and
  *   feedforward side (sources = the n_in input columns), rec may have n_src = 0.
  *   State v, g, counter is updated in place. Outputs: spikes (required); prob,
  *   v_saved, G_saved, held, A_saved (K,B,T,N) and the tracked v/I/g of trial track_b
@@ -121,7 +122,23 @@ typedef struct {
   float* track_I;  /* (Bt,T,N,S+1) */
   float* track_g;  /* (Bt,T,N,2,S) */
   int64_t track_b;
+  /* On-device Poisson input instead of x (x NULL): channel j of trial b fires at step t
+   * with probability in_prob[j] (n_in floats), drawn from Philox4x32-10 under key
+   * in_seed at counter (j, in_t0 + t, b, 0) (see wt_poisson_fill); NULL: the input is x. */
+  const float* in_prob;
+  uint64_t in_seed;
+  int64_t in_t0;
 } wt_run_io;
+
+/* wt_poisson_fill — materialise on-device Poisson input: x[b, t, j] = 1 if channel j of
+ * trial b fires at absolute step t0 + t, else 0, (B, T, n_in) f32. A channel fires when
+ * u < prob[j], u = (w >> 8) * 2^-24 with w the first word of Philox4x32-10 (Salmon et al.
+ * 2011) of counter (j, t0 + t, b, 0) under key (seed low 32 bits, seed high 32 bits): the
+ * stream wt_cond_run draws from with in_prob/in_seed/in_t0, which the host can replay.
+ * Replaces the dense spike tensor the reference's Poisson dataset draws with torch.rand
+ * (dataloaders/unsupervised.py:85-90). */
+int wt_poisson_fill(const float* prob, int64_t n_in, uint64_t seed, int64_t t0, int64_t B,
+                    int64_t T, float* x, wt_stream_t stream);
 
 int64_t wt_cond_run_scratch_bytes(const wt_geometry* geo, int64_t B, int64_t T);
 /* Leading bytes of the scratch that must be zero at each launch (the rest need not). */

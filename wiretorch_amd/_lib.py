@@ -43,6 +43,7 @@ class RunIO(ctypes.Structure):
         ("x", P), ("B", I64), ("T", I64), ("n_in", I64), ("v", P), ("g", P), ("counter", P),
         ("spikes", P), ("prob", P), ("v_saved", P), ("G_saved", P), ("held", P),
         ("A_saved", P), ("track_v", P), ("track_I", P), ("track_g", P), ("track_b", I64),
+        ("in_prob", P), ("in_seed", ctypes.c_uint64), ("in_t0", I64),
     ]  # fmt: skip
 
 
@@ -114,6 +115,7 @@ SIGNATURES = {
                                         ctypes.POINTER(RateOperand),
                                         ctypes.POINTER(RateBackIO), P]),
     "wt_edge_sources": (ctypes.c_int, [P, I64, P, P]),
+    "wt_poisson_fill": (ctypes.c_int, [P, I64, ctypes.c_uint64, I64, I64, I64, P, P]),
     "wt_gemm_tn_split": (ctypes.c_int, [P, I64, P, I64, P, I64, I64, I64, I64, ctypes.c_int32,
                                         P]),
     "wt_split_bf16": (ctypes.c_int, [P, I64, P, P, P]),

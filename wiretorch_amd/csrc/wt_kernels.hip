@@ -34,6 +34,7 @@
 #include "wt_math.h"
 
 #include "wt_back.h"
+#include "wt_philox.h"
 #include "wt_run.h"
 
 namespace wt {
@@ -61,6 +62,40 @@ __global__ __launch_bounds__(256) void compact_input_kernel(const float* x, int6
   }
   __syncthreads();
   if (threadIdx.x == 0) count[row] = s_n;
+}
+
+// The same lists for on-device Poisson input: row (b, t) draws channel j's spike from
+// the counter-based stream (wt_philox.h) instead of reading x.
+__global__ __launch_bounds__(256) void poisson_lists_kernel(const float* prob, int64_t n_in,
+                                                            uint64_t seed, int64_t t0,
+                                                            int64_t T, int64_t rows,
+                                                            int32_t* count, int32_t* idx,
+                                                            float* val) {
+  __shared__ int32_t s_n;
+  const int64_t row = blockIdx.x;
+  if (row >= rows) return;
+  if (threadIdx.x == 0) s_n = 0;
+  __syncthreads();
+  const uint32_t b = (uint32_t)(row / T), t = (uint32_t)(t0 + row % T);
+  for (int64_t j = threadIdx.x; j < n_in; j += blockDim.x) {
+    if (poisson_fires(seed, b, t, (uint32_t)j, prob[j])) {
+      const int32_t pos = atomicAdd(&s_n, 1);
+      if (pos < kInCap) {
+        idx[row * kInCap + pos] = (int32_t)j;
+        val[row * kInCap + pos] = 1.0f;
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) count[row] = s_n;
+}
+
+__global__ void poisson_fill_kernel(const float* prob, int64_t n_in, uint64_t seed, int64_t t0,
+                                    int64_t B, int64_t T, float* x) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * T * n_in) return;
+  const int64_t j = i % n_in, bt = i / n_in, b = bt / T, t = bt - b * T;
+  x[i] = poisson_fires(seed, (uint32_t)b, (uint32_t)(t0 + t), (uint32_t)j, prob[j]) ? 1.0f : 0.0f;
 }
 
 // ---------------------------------------------------------------------------------
@@ -452,6 +487,15 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
                        (hipStream_t)stream, io->x, rows, io->n_in, in_count, in_idx, in_val);
     hipError_t ce = hipGetLastError();
     if (ce != hipSuccess) return ce;
+  } else if (ff->n_src > 0 && io->in_prob) {  // on-device Poisson input: no x at all
+    const int64_t rows = io->B * io->T;
+    hipLaunchKernelGGL(poisson_lists_kernel, dim3((unsigned)rows), dim3(256), 0,
+                       (hipStream_t)stream, io->in_prob, io->n_in, io->in_seed, io->in_t0,
+                       io->T, rows, in_count, in_idx, in_val);
+    hipError_t ce = hipGetLastError();
+    if (ce != hipSuccess) return ce;
+  } else if (ff->n_src > 0) {
+    return hipErrorInvalidValue;  // a feed-forward side needs x or in_prob
   }
   const bool coop = tab->K_rec > 0 && rec->n_src > 0 && geo->R > 1;
   return dispatch_S<RunLaunch>(tab->S, a, dyn, per_thread, (hipStream_t)stream, coop);
@@ -461,6 +505,19 @@ extern "C" int wt_cond_run(const wt_tables* tab, const wt_side* rec, const wt_si
                            const wt_geometry* geo, const wt_run_io* io, void* scratch,
                            wt_stream_t stream) {
   return run_impl(tab, rec, ff, geo, io, scratch, nullptr, stream);
+}
+
+extern "C" int wt_poisson_fill(const float* prob, int64_t n_in, uint64_t seed, int64_t t0,
+                               int64_t B, int64_t T, float* x, wt_stream_t stream) {
+  if (n_in < 0 || B < 0 || T < 0 || t0 < 0 || n_in > UINT32_MAX || B > UINT32_MAX ||
+      t0 + T > (int64_t)UINT32_MAX)
+    return hipErrorInvalidValue;
+  const int64_t n = B * T * n_in;
+  if (n == 0) return hipSuccess;
+  if (!prob || !x) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(poisson_fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, prob, n_in, seed, t0, B, T, x);
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------------

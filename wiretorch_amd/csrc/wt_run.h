@@ -22,6 +22,7 @@
 
 #include "../../include/wiretorch_amd.h"
 #include "wt_math.h"
+#include "wt_philox.h"
 
 namespace wt {
 
@@ -794,10 +795,14 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
         for (int64_t q = 0; q < tpg; ++q) {
           const int64_t bt = (g + q * groups) * T + t;
           if (gload(P->in_count + bt) <= kInCap) continue;  // uniform
-          const float* xrow = P->io.x + bt * n_in;
+          const float* xrow = P->io.x + bt * n_in;  // (null with Poisson input)
+          const bool drawn = P->io.x == nullptr;
+          const uint32_t pb = (uint32_t)(g + q * groups), pt = (uint32_t)(P->io.in_t0 + t);
           const int64_t row_base = (K_rec * tpg + q) * range_n;
           for (int64_t j = threadIdx.x; j < n_in; j += blockDim.x) {
-            const float xv = gload(xrow + j);
+            const float xv = drawn ? (poisson_fires(P->io.in_seed, pb, pt, (uint32_t)j,
+                                                    gload(P->io.in_prob + j)) ? 1.0f : 0.0f)
+                                   : gload(xrow + j);
             if (xv == 0.0f) continue;
             const int32_t k = gload(P->ff.pathway + j);
             if (k < 0) continue;

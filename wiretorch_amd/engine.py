@@ -35,6 +35,7 @@ import torch
 
 from wiretorch_amd import _lib
 from wiretorch_amd.connectome import Connectome, from_dense
+from wiretorch_amd.inputs import PoissonInput
 from wiretorch_amd.network import Drive, Physiology, Run
 
 #: Physiology the backward pass can differentiate, in ``Physiology`` names.
@@ -611,6 +612,8 @@ class _Plan:
     device: torch.device
     #: gradients flow back through the recurrent spikes (set by ``simulate``)
     recurrent_gradients: bool = False
+    #: on-device Poisson input in place of the input tensor (set by ``simulate``)
+    poisson: PoissonInput | None = None
 
     @property
     def K(self) -> int:
@@ -660,8 +663,12 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
     # the accumulators' bound stays on the device: the kernel derives its fractional bits
     bound = _device_scalar(rec.max_in_sum, device)
     if ff.n_src and ff.conn.n_edges:
-        xd = x.detach()
-        x_max = _cached(("x_max",) + _key(xd), (xd,), lambda: xd.abs().max().double())
+        if isinstance(x, PoissonInput):  # spikes: at most 1
+            x_max = _cached(("one", str(device)), (),
+                            lambda: torch.ones((), dtype=torch.float64, device=device))
+        else:
+            xd = x.detach()
+            x_max = _cached(("x_max",) + _key(xd), (xd,), lambda: xd.abs().max().double())
         ff_max = _device_scalar(ff.max_in_sum, device)
         bound = _cached(("bound",) + _key(bound, ff_max, x_max), (bound, ff_max, x_max),
                         lambda: bound + ff_max * x_max)
@@ -701,11 +708,14 @@ def _launch(L: _Plan, x, scale, v, g, counter, spikes, prob, saved, tracked,
     v_saved, G_saved, held, A_saved = saved if saved is not None else (None,) * 4
     tv, tI, tg = ((tracked["v"], tracked["I"], tracked["g"]) if tracked is not None
                   else (None, None, None))
+    pin = L.poisson
     io = _lib.RunIO(
-        x.data_ptr(), L.B, L.T, L.n_in, v.data_ptr(), g.data_ptr(),
-        _lib.ptr(counter) if L.refractory else None, spikes.data_ptr(), _lib.ptr(prob),
-        _lib.ptr(v_saved), _lib.ptr(G_saved), _lib.ptr(held), _lib.ptr(A_saved),
-        _lib.ptr(tv), _lib.ptr(tI), _lib.ptr(tg), L.track_b,
+        None if pin is not None else x.data_ptr(), L.B, L.T, L.n_in, v.data_ptr(),
+        g.data_ptr(), _lib.ptr(counter) if L.refractory else None, spikes.data_ptr(),
+        _lib.ptr(prob), _lib.ptr(v_saved), _lib.ptr(G_saved), _lib.ptr(held),
+        _lib.ptr(A_saved), _lib.ptr(tv), _lib.ptr(tI), _lib.ptr(tg), L.track_b,
+        pin.prob.data_ptr() if pin is not None else None, pin.seed if pin is not None else 0,
+        pin.t0 if pin is not None else 0,
     )  # fmt: skip
     rec = L.rec.abi(R, range_n, L.stream, rec_weights)
     ff = L.ff.abi(R, range_n, L.stream, ff_weights)
@@ -846,7 +856,9 @@ class _Run(torch.autograd.Function):
                 grad_w[:n_rec_w] = _weight_grads(L, L.rec, spikes, grad_A, 0,
                                                  weights[:n_rec_w], w_needs[:n_rec_w])
             if any(w_needs[n_rec_w:]):
-                grad_w[n_rec_w:] = _weight_grads(L, L.ff, x.detach().float(), grad_A, L.K_rec,
+                activity = (L.poisson.materialize(L.stream) if L.poisson is not None
+                            else x.detach().float())
+                grad_w[n_rec_w:] = _weight_grads(L, L.ff, activity, grad_A, L.K_rec,
                                                  weights[n_rec_w:], w_needs[n_rec_w:])
         grad_x = _input_grad(L, x, grad_A, weights[n_rec_w:]) if want_x else None
         return (None, None, grad_scale, grad_x, None, None, None, *grad_w, *grad_phys)
@@ -975,6 +987,9 @@ def simulate(
     if drive.K_rec + drive.K_ff > MAX_PATHWAYS:
         drive = fold_pathways(drive)
     L = _plan(v, x, drive, p, probabilities, track, track_batch_idx)
+    if isinstance(x, PoissonInput):  # drawn inside the forward; the tensor is a stand-in
+        L.poisson = x
+        x = torch.empty((0,), device=device)
     # The kernel updates the state in place: always work on copies, so the caller's
     # tensors keep their values (a permuted view may already be contiguous storage).
     v = v.detach().to(device=device, dtype=torch.float32).clone(

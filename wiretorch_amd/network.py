@@ -546,7 +546,10 @@ class ProjectionNetwork(nn.Module):
         """Keep the family's extra state from ``run``."""
 
     def _validate_forward(self, input_spikes: torch.Tensor) -> None:
-        assert isinstance(input_spikes, torch.Tensor), "input_spikes must be a Tensor"
+        from wiretorch_amd.inputs import PoissonInput
+
+        assert isinstance(input_spikes, (torch.Tensor, PoissonInput)), (
+            "input_spikes must be a Tensor (or an on-device PoissonInput)")
         assert input_spikes.device == self.device, (
             f"input_spikes on {input_spikes.device}, model on {self.device}"
         )
