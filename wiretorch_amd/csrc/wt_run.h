@@ -634,24 +634,23 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
             gd[i][s] = gd[i][s] * syn.decay_d[s];
           }
           // the item's pathways four at a time: their accumulators and scales read
-          // together, then cleared, then added in pathway order
+          // together, then cleared, then added in pathway order. The reads and clears
+          // take no branch: an index past the last pathway is clamped to it (read again,
+          // cleared again after its read: a wave's LDS operations complete in order).
           double* const cell = acc + __umul24(q, (uint32_t)range_n) + ln;
           for (int32_t k0 = 0; k0 < K; k0 += 4) {
             double ad[4];
             float sc[4];
+            uint32_t kc[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-              ad[j] = 0.0;
-              sc[j] = 0.0f;
-              if (k0 + j < K) {
-                ad[j] = cell[(uint32_t)(k0 + j) * acc_stride];
-                sc[j] = row[8 + k0 + j];
-              }
+              kc[j] = (uint32_t)(k0 + j < K ? k0 + j : K - 1);
+              ad[j] = cell[kc[j] * acc_stride];
+              sc[j] = row[8 + kc[j]];
             }
             if (valid) {
 #pragma unroll
-              for (int j = 0; j < 4; ++j)
-                if (k0 + j < K) cell[(uint32_t)(k0 + j) * acc_stride] = 0.0;
+              for (int j = 0; j < 4; ++j) cell[kc[j] * acc_stride] = 0.0;
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
