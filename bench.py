@@ -184,6 +184,7 @@ def bench_config3(args):
     T = args.T if args.T != 2000 else 500
     wl = synthetic.config3(T=T)
     model = wl.model.to(dev)
+    model.recurrent_gradients = bool(args.recurrent_gradients)
     x = torch.from_numpy(wl.x).float().to(dev)
     B, N, S = x.shape[0], wl.N, wl.S
     dt = float(model.dt)
@@ -213,11 +214,14 @@ def bench_config3(args):
     # algorithmic bytes: the forward moves the state and saves v, G, held, A; the backward
     # reads what was saved (and the spikes and dL/ds) and writes dL/dA; the weight
     # gradient reads dL/dA of each delivered event's target (and its index) and writes
-    # one gradient per synapse
+    # one gradient per synapse; with gradients through the recurrent spikes the backward
+    # also reads the recurrent synapses (target and weight) once per step
+    n_rec = int((wl.structure["w"] != 0).sum())
     nbytes = {
         "forward": T * (B * N * (8 + 16 * S + 8 + 4 + 4 + 4 * S + 1 + 4 * K) + 24 * N)
                    + 8 * events,
-        "backward": T * B * N * (4 + 4 + 4 + 4 * S + 1 + 4 * K + 4 * K),
+        "backward": T * B * N * (4 + 4 + 4 + 4 * S + 1 + 4 * K + 4 * K)
+                    + (T * 8 * n_rec if args.recurrent_gradients else 0),
         "weight_gradient": 8 * events + 4 * n_edges,
     }
     dominant = max(parts, key=parts.get)
@@ -229,13 +233,16 @@ def bench_config3(args):
     cpu = _er_cpu_baseline(model, wl.x, args.cpu_steps, True) if args.cpu_steps > 0 else None
     _line(B * N * T / (ms_per_step / 1e3), ms_per_step, args, "f32",
           {"workload": "config3: conductance-LIF training step (BPTT, surrogate gradient)",
-           "neurons": N, "synapses": int((wl.structure["w"] != 0).sum()), "batch": B,
+           "neurons": N, "synapses": n_rec, "batch": B,
            "time_steps": T, "dt_ms": dt, "learnt": "per-synapse weights, tau_mem, theta",
+           "recurrent_gradients": bool(args.recurrent_gradients),
            "loss": "MSE of 20 ms-binned rates vs gamma(2, 5 Hz) targets",
            "parallelism": "single GPU"},
           {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
            "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-           "kernel": {"forward": "wt_cond_run", "backward": "wt_cond_scan_backward",
+           "kernel": {"forward": "wt_cond_run",
+                      "backward": ("wt_cond_recurrent_backward" if args.recurrent_gradients
+                                   else "wt_cond_scan_backward"),
                       "weight_gradient": "wt_weight_gradient"}[dominant],
            "kernel_ms": parts[dominant], "algorithmic_bytes_per_launch": nbytes[dominant],
            "per_part_ms": parts},
@@ -441,6 +448,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=int(os.environ.get("BENCH_CPU_STEPS", 400)))
     ap.add_argument("--T", type=int, default=2000)
     ap.add_argument("--config", type=int, choices=(0, 1, 2, 3, 4), default=2)
+    ap.add_argument("--recurrent-gradients", action="store_true",
+                    help="configuration 3 with gradients through the recurrent spikes")
     ap.add_argument("--poisson", action="store_true",
                     help="configuration 2 with its input drawn on the device")
     ap.add_argument("--filter", action="store_true",

@@ -41,24 +41,35 @@ struct BackState {
 template <int S>
 constexpr int back_fields() { return 1 + 9 * S + WT_MAX_K + 5; }
 
-// Global layout of the recurrent path's state: field f of item idx at f * BN + idx.
+// Global layout of the recurrent path's state: field f of item idx at f * BN + idx. A
+// field that feeds no wanted gradient is neither read (it reads as zero) nor written:
+// the decay recursions and partials only with grad_decay, and so on.
 template <int S>
 __device__ inline void state_io(BackState<S>& st, float* base, int64_t BN, int64_t idx,
-                                bool store) {
+                                bool store, const wt_backward_io& io, int64_t K) {
   float* p = base + idx;
-  auto x = [&](float& v) {
-    if (store) *p = v; else v = *p;
+  auto y = [&](bool want, float& v) {
+    if (want) {
+      if (store) *p = v; else v = *p;
+    } else if (!store) {
+      v = 0.0f;
+    }
     p += BN;
   };
-  x(st.dv);
+  const bool decay = io.grad_decay != nullptr, jump = io.grad_jump != nullptr;
+  const bool esyn = io.grad_E_syn != nullptr, scale = io.grad_scale != nullptr;
+  y(true, st.dv);
 #pragma unroll
   for (int s = 0; s < S; ++s) {
-    x(st.lr[s]); x(st.ld[s]); x(st.Hr[s]); x(st.Hd[s]); x(st.accE[s]);
-    x(st.accDr[s]); x(st.accDd[s]); x(st.accJr[s]); x(st.accJd[s]);
+    y(true, st.lr[s]); y(true, st.ld[s]); y(decay, st.Hr[s]); y(decay, st.Hd[s]);
+    y(esyn, st.accE[s]); y(decay, st.accDr[s]); y(decay, st.accDd[s]);
+    y(jump, st.accJr[s]); y(jump, st.accJd[s]);
   }
 #pragma unroll
-  for (int k = 0; k < WT_MAX_K; ++k) x(st.acc_scale[k]);
-  x(st.acc_theta); x(st.acc_reset); x(st.acc_EL); x(st.acc_Cm); x(st.acc_beta);
+  for (int k = 0; k < WT_MAX_K; ++k) y(scale && k < K, st.acc_scale[k]);
+  y(io.grad_theta != nullptr, st.acc_theta); y(io.grad_reset != nullptr, st.acc_reset);
+  y(io.grad_E_L != nullptr, st.acc_EL); y(io.grad_C_m != nullptr, st.acc_Cm);
+  y(io.grad_beta != nullptr, st.acc_beta);
 }
 
 template <int S>
@@ -320,11 +331,11 @@ __global__ __launch_bounds__(256) void rg_membrane_kernel(BackArgs P, int64_t t)
 #pragma unroll
   for (int k = 0; k < WT_MAX_K; ++k) scale[k] = k < P.tab.K ? P.tab.scale[k * N + n] : 0.0f;
   BackState<S> st;
-  if (t == P.io.T - 1) state_zero(st); else state_io<S>(st, P.state, B * N, idx, false);
+  if (t == P.io.T - 1) state_zero(st); else state_io<S>(st, P.state, B * N, idx, false, P.io, P.tab.K);
   StepIn<S> in;
   load_step<S>(in, P, b, n, t);
   back_membrane_step<S>(st, P, syn, c, b, n, t, in, scale);
-  state_io<S>(st, P.state, B * N, idx, true);
+  state_io<S>(st, P.state, B * N, idx, true, P.io, P.tab.K);
 }
 
 // (2) Per (source j, trial b), threads b fastest: R gathered along j's synapses, then
@@ -338,17 +349,38 @@ __global__ __launch_bounds__(256) void rg_spike_kernel(BackArgs P, int64_t t) {
   float R = 0.0f;
   const int32_t k = j < P.rec.n_src ? P.rec.pathway[j] : -1;
   if (k >= 0 && k < P.tab.K_rec) {
+    // j's synapses sixteen at a time: their targets and weights, then the sixteen dL/da
+    // values, all in flight together (a synapse at a time left one dependent load pair
+    // in flight per thread); the products still added one by one in synapse order.
     const float* g = P.grad_now + (int64_t)k * N * B + b;
-    for (int64_t e = P.rec.indptr[j], e1 = P.rec.indptr[j + 1]; e < e1; ++e)
-      R += P.rec.weights[e] * g[(int64_t)P.rec.targets[e] * B];
+    const int32_t* tg = P.rec.targets;
+    const float* w = P.rec.weights;
+    int64_t e = P.rec.indptr[j];
+    const int64_t e1 = P.rec.indptr[j + 1];
+    constexpr int kU = 16;
+    for (; e + kU <= e1; e += kU) {
+      int32_t t8[kU];
+      float w8[kU], g8[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        t8[u] = tg[e + u];
+        w8[u] = w[e + u];
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) g8[u] = g[(int64_t)t8[u] * B];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) R += w8[u] * g8[u];
+    }
+    for (; e < e1; ++e) R += w[e] * g[(int64_t)tg[e] * B];
   }
   BackNeuron c;
   c.theta = P.tab.theta[j];
   c.k_surr = *P.tab.surr;
   const int64_t BN = B * N, item = b * N + j;
   BackState<S> st;
+  const bool want_theta = P.io.grad_theta != nullptr;
   st.dv = P.state[item];
-  st.acc_theta = P.state[(int64_t)(back_fields<S>() - 5) * BN + item];
+  st.acc_theta = want_theta ? P.state[(int64_t)(back_fields<S>() - 5) * BN + item] : 0.0f;
   StepIn<S> in;
   {
     const wt_backward_io& io = P.io;
@@ -360,7 +392,7 @@ __global__ __launch_bounds__(256) void rg_spike_kernel(BackArgs P, int64_t t) {
   }
   back_spike_step<S>(st, P, c, R, in);
   P.state[item] = st.dv;
-  P.state[(int64_t)(back_fields<S>() - 5) * BN + item] = st.acc_theta;
+  if (want_theta) P.state[(int64_t)(back_fields<S>() - 5) * BN + item] = st.acc_theta;
 }
 
 // After step 0: the partials from the global state.
@@ -370,7 +402,7 @@ __global__ __launch_bounds__(256) void rg_finish_kernel(BackArgs P) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= B * N) return;
   BackState<S> st;
-  state_io<S>(st, P.state, B * N, idx, false);
+  state_io<S>(st, P.state, B * N, idx, false, P.io, P.tab.K);
   back_finish<S>(st, P, idx / N, idx % N);
 }
 
