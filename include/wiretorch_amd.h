@@ -217,7 +217,7 @@ int wt_cond_scan_backward(const wt_tables* tab, const wt_backward_io* io,
  * to dL/ds_j before the surrogate. io as for wt_cond_scan_backward; rec is the
  * recurrent side (indptr, targets, weights, pathway; split unused), n_src == N.
  * scratch: wt_cond_recurrent_backward_scratch_bytes(S, K_rec, B, N) bytes, no zeroing
- * needed (adjoint state between the steps and the current step's dL/da).
+ * needed (adjoint state between the steps, the current step's dL/da and R).
  * Replaces: conductance/engine.py:386-438 _recurrent_backward — per step
  * conductance/kernels.py:704-823 inject_backward, network_simulators/engine.py:257-271
  * carry_to_sources, network_simulators/kernels.py:214-241 spike_backward. */

@@ -235,6 +235,9 @@ RG_CASES = {
     "scaling_factors": dict(scaling_factors=True),
     "learnt_weights": dict(learnt_weights=True),
     "refractory": dict(scaling_factors=True, tau_ref=2.0),
+    # trials filling whole waves: the wave-per-source gather (one and two waves a source)
+    "learnt_weights_b64": dict(learnt_weights=True, batch=64),
+    "refractory_b128": dict(scaling_factors=True, tau_ref=2.0, batch=128),
 }
 
 
@@ -245,10 +248,11 @@ def test_recurrent_gradients_on_gpu(case):
     autograd through the same steps: loss to 1e-4 relative, every gradient within 1e-4
     of its own scale. The reference holds no fixture for this path; the oracle's
     forward is pinned by the fixtures and the closed forms, its backward is autograd."""
-    kwargs = RG_CASES[case]
+    kwargs = dict(RG_CASES[case])
+    batch = kwargs.pop("batch", sc.BATCH_SIZE)
     results = {}
     for device, eng in (("cpu", oracle_engine), (DEV, engine)):
-        built = sc.recurrent(sc.BATCH_SIZE, sc.SEED, recurrent_gradients=True, **kwargs)
+        built = sc.recurrent(batch, sc.SEED, recurrent_gradients=True, **kwargs)
         sc.use_engine(built.model, eng)
         results[device] = sc.gradients(built, device=device)
     (loss_cpu, g_cpu), (loss_gpu, g_gpu) = results["cpu"], results[DEV]
@@ -258,7 +262,7 @@ def test_recurrent_gradients_on_gpu(case):
         scale = np.abs(value).max() or 1.0
         np.testing.assert_allclose(g_gpu[key], value, rtol=0, atol=1e-4 * scale, err_msg=key)
     # the path matters: without the recurrent term the gradients differ
-    built = sc.recurrent(sc.BATCH_SIZE, sc.SEED, recurrent_gradients=False, **kwargs)
+    built = sc.recurrent(batch, sc.SEED, recurrent_gradients=False, **kwargs)
     sc.use_engine(built.model, oracle_engine)
     _, g_plain = sc.gradients(built, device="cpu")
     assert any(not np.allclose(g_plain[k], g_cpu[k], rtol=1e-3, atol=1e-6) for k in g_cpu)

@@ -26,6 +26,7 @@ struct BackArgs {
   wt_side rec;      // recurrent side (recurrent path only)
   float* state;     // adjoint state, [back_fields<S>()][B * N] (recurrent path only)
   float* grad_now;  // dL/da of the current step, [K_rec][N][B] (recurrent path only)
+  float* R;         // the recurrent term of the current step, [N][B] (recurrent path only)
 };
 
 // The adjoint state of one (trial, neuron) between reverse steps.
@@ -144,13 +145,14 @@ __device__ inline float step_A(const StepIn<S>& in, const BackArgs& P, int k, in
 
 // Reverse step t, all but the spike of step t: the injections of step t (dL/da_k, the
 // jump and decay partials), the membrane update, and the conductances decaying into
-// step t+1. Leaves st.dv = dL/dv_t without the spike's term. When grad_now is set,
-// dL/da_k for the recurrent pathways is also written there, [k][n][b].
+// step t+1. Leaves st.dv = dL/dv_t without the spike's term. When ga_rec is given,
+// dL/da_k of the recurrent pathways (k < K_rec) is also left there.
 template <int S>
 __device__ inline void back_membrane_step(BackState<S>& st, const BackArgs& P,
                                           const Synapses<S>& syn, const BackNeuron& c,
                                           int64_t b, int64_t n, int64_t t,
-                                          const StepIn<S>& in, const float (&scale)[WT_MAX_K]) {
+                                          const StepIn<S>& in, const float (&scale)[WT_MAX_K],
+                                          float* ga_rec = nullptr) {
   const wt_tables& tab = P.tab;
   const wt_backward_io& io = P.io;
   const int64_t N = tab.N, K = tab.K, B = io.B, T = io.T;
@@ -202,7 +204,7 @@ __device__ inline void back_membrane_step(BackState<S>& st, const BackArgs& P,
     const int64_t ka = ((k * B + b) * T + t) * N + n;
     const float ga = qk * scale[k];
     if (want_A) io.grad_A[ka] = ga;
-    if (P.grad_now && k < tab.K_rec) P.grad_now[(k * N + n) * B + b] = ga;
+    if (ga_rec && k < tab.K_rec) ga_rec[k] = ga;
     if (want_scale) st.acc_scale[k] += qk * step_A<S>(in, P, k, b, n, t);
   }
   // Membrane.
@@ -317,41 +319,105 @@ __global__ __launch_bounds__(256) void cond_backward_kernel(BackArgs P) {
   back_finish<S>(st, P, b, n);
 }
 
-// Recurrent path, per step: (1) the membrane part, state in global memory.
+// Recurrent path. Per reverse step t: (1) the membrane kernel: for every item (b, n) the
+// spike part of step t + 1 (which needs R of step t + 1) and the membrane part of step t,
+// with the adjoint state in global memory between the steps, writing dL/da of step t;
+// (2) a gather kernel: R[j][b] = sum over source j's synapses e of w_e dL/da(t)[target e]
+// [b]. After step 0, the finish kernel: the spike part of step 0 and the partials.
+
+// The spike part of item (b, n) at step t, given R: only dv and the threshold partial.
 template <int S>
-__global__ __launch_bounds__(256) void rg_membrane_kernel(BackArgs P, int64_t t) {
-  const int64_t N = P.tab.N, B = P.io.B;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= B * N) return;
-  const int64_t b = idx / N, n = idx - b * N;
-  Synapses<S> syn;
-  load_synapses<S>(P.tab, syn);
-  const BackNeuron c = back_neuron(P.tab, n);
-  float scale[WT_MAX_K];
-#pragma unroll
-  for (int k = 0; k < WT_MAX_K; ++k) scale[k] = k < P.tab.K ? P.tab.scale[k * N + n] : 0.0f;
-  BackState<S> st;
-  if (t == P.io.T - 1) state_zero(st); else state_io<S>(st, P.state, B * N, idx, false, P.io, P.tab.K);
+__device__ inline void rg_spike_at(BackState<S>& st, const BackArgs& P, const BackNeuron& c,
+                                   int64_t b, int64_t n, int64_t t, float R) {
+  const wt_backward_io& io = P.io;
+  const int64_t out = (b * io.T + t) * P.tab.N + n;
   StepIn<S> in;
-  load_step<S>(in, P, b, n, t);
-  back_membrane_step<S>(st, P, syn, c, b, n, t, in, scale);
-  state_io<S>(st, P.state, B * N, idx, true, P.io, P.tab.K);
+  in.v = io.v_saved[out];
+  in.grad_spike = io.grad_spikes[out];
+  in.grad_prob = io.grad_prob ? io.grad_prob[out] : 0.0f;
+  in.held = io.held ? (float)io.held[out] : 0.0f;
+  back_spike_step<S>(st, P, c, R, in);
 }
 
-// (2) Per (source j, trial b), threads b fastest: R gathered along j's synapses, then
-// the spike term of item (b, j). Only dv and the threshold partial change.
+// Workgroup i runs on XCD i % 8. The logical index that gives each XCD one contiguous run
+// of the n workgroups (XCDs below r = n % 8 take q + 1 of them, the others q = n / 8).
+__device__ inline unsigned xcd_contiguous(unsigned i, unsigned n) {
+  const unsigned x = i & 7u, slot = i >> 3, q = n >> 3, r = n & 7u;
+  return x < r ? x * (q + 1) + slot : r * (q + 1) + (x - r) * q + slot;
+}
+
+// The membrane kernel's workgroup: a tile of 32 neurons x 8 trials, neurons fastest, so
+// the per-item rows (v, G, spikes, state: neuron fastest) are read in 128-byte runs; R
+// ([n][b]) comes in and dL/da ([k][n][b]) leaves through LDS in rows of 8 trials. The
+// tiles of one neuron range are consecutive (and on one XCD), so each 128-byte line of
+// dL/da is completed in one L2.
+constexpr int kRgTileN = 32, kRgTileB = 8;
+
 template <int S>
-__global__ __launch_bounds__(256) void rg_spike_kernel(BackArgs P, int64_t t) {
+__global__ __launch_bounds__(256) void rg_membrane_kernel(BackArgs P, int64_t t) {
+  __shared__ float ga_tile[WT_MAX_K][kRgTileN][kRgTileB + 1];
+  __shared__ float r_tile[kRgTileN][kRgTileB + 1];
+  const int64_t N = P.tab.N, B = P.io.B;
+  const int64_t tiles_b = (B + kRgTileB - 1) / kRgTileB;
+  const int64_t tile = xcd_contiguous(blockIdx.x, gridDim.x);
+  const int64_t tn = tile / tiles_b, tb = tile - tn * tiles_b;
+  const int nn = threadIdx.x % kRgTileN, bb = threadIdx.x / kRgTileN;
+  const int64_t n = tn * kRgTileN + nn, b = tb * kRgTileB + bb;
+  // the transposed position: trials fastest
+  const int wb = threadIdx.x % kRgTileB, wn = threadIdx.x / kRgTileB;
+  const int64_t n2 = tn * kRgTileN + wn, b2 = tb * kRgTileB + wb;
+  const int K_rec = (int)P.tab.K_rec;
+  const bool carry = t < P.io.T - 1;  // the spike part of step t + 1 is done here
+  if (carry) {
+    r_tile[wn][wb] = n2 < N && b2 < B ? P.R[n2 * B + b2] : 0.0f;
+    __syncthreads();
+  }
+  float ga[WT_MAX_K];
+#pragma unroll
+  for (int k = 0; k < WT_MAX_K; ++k) ga[k] = 0.0f;
+  if (n < N && b < B) {
+    const int64_t idx = b * N + n;
+    Synapses<S> syn;
+    load_synapses<S>(P.tab, syn);
+    const BackNeuron c = back_neuron(P.tab, n);
+    float scale[WT_MAX_K];
+#pragma unroll
+    for (int k = 0; k < WT_MAX_K; ++k) scale[k] = k < P.tab.K ? P.tab.scale[k * N + n] : 0.0f;
+    BackState<S> st;
+    if (!carry) {
+      state_zero(st);
+    } else {
+      state_io<S>(st, P.state, B * N, idx, false, P.io, P.tab.K);
+      rg_spike_at<S>(st, P, c, b, n, t + 1, r_tile[nn][bb]);
+    }
+    StepIn<S> in;
+    load_step<S>(in, P, b, n, t);
+    back_membrane_step<S>(st, P, syn, c, b, n, t, in, scale, ga);
+    state_io<S>(st, P.state, B * N, idx, true, P.io, P.tab.K);
+  }
+#pragma unroll
+  for (int k = 0; k < WT_MAX_K; ++k)
+    if (k < K_rec) ga_tile[k][nn][bb] = ga[k];
+  __syncthreads();
+  if (n2 < N && b2 < B) {
+#pragma unroll
+    for (int k = 0; k < WT_MAX_K; ++k)
+      if (k < K_rec) P.grad_now[((int64_t)k * N + n2) * B + b2] = ga_tile[k][wn][wb];
+  }
+}
+
+// The gather, any B: per (source j, trial b), threads b fastest. j's synapses sixteen at
+// a time: their targets and weights, then the sixteen dL/da values, all in flight
+// together; the products added one by one in synapse order.
+template <int S>
+__global__ __launch_bounds__(256) void rg_gather_kernel(BackArgs P) {
   const int64_t N = P.tab.N, B = P.io.B;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= B * N) return;
   const int64_t j = idx / B, b = idx - j * B;
   float R = 0.0f;
-  const int32_t k = j < P.rec.n_src ? P.rec.pathway[j] : -1;
+  const int32_t k = P.rec.pathway[j];
   if (k >= 0 && k < P.tab.K_rec) {
-    // j's synapses sixteen at a time: their targets and weights, then the sixteen dL/da
-    // values, all in flight together (a synapse at a time left one dependent load pair
-    // in flight per thread); the products still added one by one in synapse order.
     const float* g = P.grad_now + (int64_t)k * N * B + b;
     const int32_t* tg = P.rec.targets;
     const float* w = P.rec.weights;
@@ -373,37 +439,105 @@ __global__ __launch_bounds__(256) void rg_spike_kernel(BackArgs P, int64_t t) {
     }
     for (; e < e1; ++e) R += w[e] * g[(int64_t)tg[e] * B];
   }
-  BackNeuron c;
-  c.theta = P.tab.theta[j];
-  c.k_surr = *P.tab.surr;
-  const int64_t BN = B * N, item = b * N + j;
-  BackState<S> st;
-  const bool want_theta = P.io.grad_theta != nullptr;
-  st.dv = P.state[item];
-  st.acc_theta = want_theta ? P.state[(int64_t)(back_fields<S>() - 5) * BN + item] : 0.0f;
-  StepIn<S> in;
-  {
-    const wt_backward_io& io = P.io;
-    const int64_t out = (b * io.T + t) * N + j;
-    in.v = io.v_saved[out];
-    in.grad_spike = io.grad_spikes[out];
-    in.grad_prob = io.grad_prob ? io.grad_prob[out] : 0.0f;
-    in.held = io.held ? (float)io.held[out] : 0.0f;
-  }
-  back_spike_step<S>(st, P, c, R, in);
-  P.state[item] = st.dv;
-  if (want_theta) P.state[(int64_t)(back_fields<S>() - 5) * BN + item] = st.acc_theta;
+  P.R[j * B + b] = R;
 }
 
-// After step 0: the partials from the global state.
+// The gather with B a multiple of 64: each wave holds one source j (wave-uniform) and 64
+// consecutive trials, whose dL/da row of a target is 256 contiguous bytes. j's synapses
+// come in 32 at a time, one per lane (lanes 32-63 repeat 0-31); lane (q, g), q = lane %
+// 16, g = lane / 16, takes synapse 4i + g's target and weight from its lane (ds_bpermute)
+// and loads trials 4q .. 4q + 3 of its row, so one 16-byte-per-lane load brings four
+// synapses' rows and eight such loads are in flight. Lane group g sums every fourth
+// synapse in order; the four groups' sums are added at the end. The next 32 targets and
+// weights are requested before the current rows.
+constexpr int kRgChunk = 32;
+
+template <int S>
+__global__ __launch_bounds__(256) void rg_gather_wave_kernel(BackArgs P) {
+  const int64_t N = P.tab.N, B = P.io.B;
+  const int64_t per_j = B >> 6;  // waves per source
+  const unsigned wg = xcd_contiguous(blockIdx.x, gridDim.x);
+  const int64_t wave = (int64_t)wg * 4 + (threadIdx.x >> 6);
+  const int64_t j = __builtin_amdgcn_readfirstlane((int)(wave / per_j));
+  if (j >= N) return;
+  const int lane = threadIdx.x & 63, q = lane & 15, g = lane >> 4;
+  const int64_t b0 = (wave - j * per_j) * 64;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int32_t k = P.rec.pathway[j];
+  if (k >= 0 && k < P.tab.K_rec) {
+    const int64_t e0 = P.rec.indptr[j], e1 = P.rec.indptr[j + 1];
+    if (e1 > e0) {
+      const int32_t* __restrict__ tg = P.rec.targets;
+      const float* __restrict__ w = P.rec.weights;
+      // dL/da of pathway k, [N][B]: target row * B * 4 bytes, then the lane's trials
+      const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<float*>(P.grad_now + (int64_t)k * N * B), (short)0,
+          (int)(N * B * 4), 0x00020000);
+      const int voff = (int)(b0 * 4 + q * 16);
+      const int row = (int)(B * 4);
+      const int mine = lane & (kRgChunk - 1);
+      // the lane's synapse of the chunk at c; past j's last synapse, that one's target
+      // (a row in range) with weight 0, which adds exact zeros
+      auto load = [&](int64_t c, int32_t& tt, float& ww) {
+        const bool in = c + mine < e1;
+        const int64_t i = in ? c + mine : e1 - 1;
+        tt = tg[i];
+        ww = in ? w[i] : 0.0f;
+      };
+      int32_t tc;
+      float wc;
+      load(e0, tc, wc);
+      for (int64_t e = e0; e < e1; e += kRgChunk) {
+        int32_t tn;
+        float wn;
+        load(e + kRgChunk, tn, wn);
+        float4 gv[kRgChunk / 4];
+        float wv[kRgChunk / 4];
+#pragma unroll
+        for (int i = 0; i < kRgChunk / 4; ++i) {
+          const int from = (4 * i + g) * 4;  // byte address of the source lane
+          const int ti = __builtin_amdgcn_ds_bpermute(from, tc);
+          wv[i] = __builtin_bit_cast(
+              float, __builtin_amdgcn_ds_bpermute(from, __builtin_bit_cast(int, wc)));
+          gv[i] = __builtin_bit_cast(
+              float4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff + ti * row, 0, 0));
+        }
+#pragma unroll
+        for (int i = 0; i < kRgChunk / 4; ++i) {  // synapse order within the lane group
+          acc[0] += wv[i] * gv[i].x;
+          acc[1] += wv[i] * gv[i].y;
+          acc[2] += wv[i] * gv[i].z;
+          acc[3] += wv[i] * gv[i].w;
+        }
+        tc = tn;
+        wc = wn;
+      }
+    }
+  }
+  // (g0 + g1) + (g2 + g3), the same in every lane group
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    acc[c] += __shfl_xor(acc[c], 16);
+    acc[c] += __shfl_xor(acc[c], 32);
+  }
+  const float r = (g & 2) ? ((g & 1) ? acc[3] : acc[2]) : ((g & 1) ? acc[1] : acc[0]);
+  P.R[j * B + b0 + 4 * q + g] = r;
+}
+
+// After step 0: the spike part of step 0, then the partials from the global state.
 template <int S>
 __global__ __launch_bounds__(256) void rg_finish_kernel(BackArgs P) {
   const int64_t N = P.tab.N, B = P.io.B;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= B * N) return;
+  const int64_t b = idx / N, n = idx - b * N;
   BackState<S> st;
   state_io<S>(st, P.state, B * N, idx, false, P.io, P.tab.K);
-  back_finish<S>(st, P, idx / N, idx % N);
+  BackNeuron c;
+  c.theta = P.tab.theta[n];
+  c.k_surr = *P.tab.surr;
+  rg_spike_at<S>(st, P, c, b, n, 0, P.R[n * B + b]);
+  back_finish<S>(st, P, b, n);
 }
 
 template <int S>
@@ -423,12 +557,20 @@ hipError_t BackLaunch<S>::run(BackArgs& a, hipStream_t stream) {
 
 template <int S>
 hipError_t BackLaunch<S>::recurrent(BackArgs& a, hipStream_t stream) {
-  const int64_t total = a.io.B * a.tab.N;
+  const int64_t B = a.io.B, N = a.tab.N, total = B * N;
   const int block = 256;
   const dim3 grid((unsigned)((total + block - 1) / block));
+  const dim3 tiles((unsigned)(((N + kRgTileN - 1) / kRgTileN) * ((B + kRgTileB - 1) / kRgTileB)));
+  // one wave per (source, 64 trials) when the trials fill whole waves (and the dL/da
+  // rows of a pathway stay within the 32-bit offsets of a buffer load)
+  const bool by_wave = B % 64 == 0 && N * B * 4 < INT32_MAX;
+  const dim3 wave_grid((unsigned)((total / 64 + 3) / 4));
   for (int64_t t = a.io.T - 1; t >= 0; --t) {
-    hipLaunchKernelGGL(rg_membrane_kernel<S>, grid, dim3(block), 0, stream, a, t);
-    hipLaunchKernelGGL(rg_spike_kernel<S>, grid, dim3(block), 0, stream, a, t);
+    hipLaunchKernelGGL(rg_membrane_kernel<S>, tiles, dim3(block), 0, stream, a, t);
+    if (by_wave)
+      hipLaunchKernelGGL(rg_gather_wave_kernel<S>, wave_grid, dim3(block), 0, stream, a);
+    else
+      hipLaunchKernelGGL(rg_gather_kernel<S>, grid, dim3(block), 0, stream, a);
   }
   hipLaunchKernelGGL(rg_finish_kernel<S>, grid, dim3(block), 0, stream, a);
   return hipGetLastError();

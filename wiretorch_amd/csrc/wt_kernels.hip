@@ -630,7 +630,8 @@ static int64_t back_fields_of(int64_t S) { return 1 + 9 * S + WT_MAX_K + 5; }
 extern "C" int64_t wt_cond_recurrent_backward_scratch_bytes(int64_t S, int64_t K_rec, int64_t B,
                                                             int64_t N) {
   const int64_t state = (back_fields_of(S) * B * N * 4 + 255) / 256 * 256;
-  return state + K_rec * N * B * 4;
+  const int64_t grad_now = (K_rec * N * B * 4 + 255) / 256 * 256;
+  return state + grad_now + B * N * 4;
 }
 
 extern "C" int wt_cond_recurrent_backward(const wt_tables* tab, const wt_side* rec,
@@ -652,9 +653,10 @@ extern "C" int wt_cond_recurrent_backward(const wt_tables* tab, const wt_side* r
   a.io = *io;
   a.rec = *rec;
   a.state = static_cast<float*>(scratch);
-  a.grad_now = reinterpret_cast<float*>(
-      static_cast<char*>(scratch) +
-      (back_fields_of(tab->S) * io->B * tab->N * 4 + 255) / 256 * 256);
+  const int64_t state_bytes = (back_fields_of(tab->S) * io->B * tab->N * 4 + 255) / 256 * 256;
+  const int64_t grad_bytes = (tab->K_rec * tab->N * io->B * 4 + 255) / 256 * 256;
+  a.grad_now = reinterpret_cast<float*>(static_cast<char*>(scratch) + state_bytes);
+  a.R = reinterpret_cast<float*>(static_cast<char*>(scratch) + state_bytes + grad_bytes);
   return dispatch_S<BackRecurrent>(tab->S, a, (hipStream_t)stream);
 }
 
