@@ -275,6 +275,7 @@ typedef struct {
   float* A_saved;       /* (K, B, T, N) activations, or null */
   const float* A_ff;    /* (K - K_rec, B, T, N) input pathways' activations, float32 (null
                          * when K == K_rec) */
+  float* split;         /* wt_rate_split_bytes scratch for the split product, or null */
 } wt_rate_io;
 
 /* wt_rate_forward — T steps of a rate network: per step one fused launch (MFMA product
@@ -310,6 +311,14 @@ typedef struct {
  * Replaces: rate/kernels.py:228-465, rate/engine.py:336-383 (_RecurrentRun.backward). */
 int wt_rate_backward(const wt_rate_tables* tab, const wt_rate_operand* op,
                      const wt_rate_back_io* io, wt_stream_t stream);
+
+/* wt_rate_split_bytes — scratch bytes (no zeroing needed) that let wt_rate_forward of a
+ * drive with one recurrent pathway, every padded size a multiple of 128, take the split
+ * product: per step a 128 x 128-tile MFMA product over up to four k slices (float32
+ * partials), summed in slice order by the update that follows; 0 when the split does not
+ * apply (the fused per-step kernel runs). No counterpart in the reference (its product is
+ * one torch.matmul per step, rate/engine.py:157-300). */
+int64_t wt_rate_split_bytes(const wt_rate_tables* tab, const wt_rate_operand* op, int64_t B);
 
 /* wt_split_bf16 — hi = bf16(x), lo = bf16(x - hi), round to nearest even: x = hi + lo to
  * 2^-17 relative. The rate weight gradient's float32 product dL/dW = r^T dL/da

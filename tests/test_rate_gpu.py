@@ -14,6 +14,7 @@ import torch
 
 import oracle.rate as oracle_rate
 import scenarios as sc
+from wiretorch_amd import rate_engine
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -128,8 +129,9 @@ def _dense_run(device, engine, **shape):
 
 @pytest.mark.parametrize("shape", [
     dict(N=320, n_in=64, B=40, T=60, seed=7),       # ragged: N, B not multiples of 64
-    dict(N=4096, n_in=64, B=256, T=6, seed=4),      # configuration 4's full width
-], ids=["small", "config4_width"])
+    dict(N=384, n_in=64, B=128, T=60, seed=5),      # split products, two k slices
+    dict(N=4096, n_in=64, B=256, T=6, seed=4),      # configuration 4's full width (split, 4)
+], ids=["small", "split", "config4_width"])
 def test_dense_bfloat16_against_rounded_oracle(shape):
     """Every product of two bfloat16 operands is exact in float32, so the engine and the
     oracle differ only in the order of float32 sums — and in the operands whose bfloat16
@@ -186,3 +188,31 @@ def test_split_product_error_bound(K, M, N):
     wide_a = torch.zeros((K, M + 37), device=DEV)
     wide_a[:, :M] = a
     assert torch.equal(_gemm_tn(wide_a[:, :M], b), _gemm_tn(a, b))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+def test_split_products_match_fused(dtype, monkeypatch):
+    """The forward's split product (128 x 128 tiles over k slices, ``wt_rate_split_bytes``)
+    against the fused per-step kernel on the same network and input: the same rates and
+    gradients up to the order of float32 sums (rates within 1e-5 of their range over 8
+    steps, gradients within 1e-4 of their scale). A spy confirms that the split ran."""
+    shape = dict(N=384, n_in=64, B=128, T=8, seed=5, storage_dtype=dtype)
+    took = []
+    real = rate_engine._split_scratch
+
+    def spy(*args):
+        out = real(*args)
+        took.append(out is not None)
+        return out
+
+    monkeypatch.setattr(rate_engine, "_split_scratch", spy)
+    r_split, l_split, g_split = _dense_run(DEV, None, **shape)
+    assert took and all(took), took
+    monkeypatch.setattr(rate_engine, "SPLIT_PRODUCTS", False)
+    r_fused, l_fused, g_fused = _dense_run(DEV, None, **shape)
+    ptp = np.ptp(r_fused)
+    np.testing.assert_allclose(r_split, r_fused, rtol=0, atol=1e-5 * ptp)
+    np.testing.assert_allclose(l_split, l_fused, rtol=1e-5)
+    for key, value in g_fused.items():
+        scale = np.abs(value).max()
+        np.testing.assert_allclose(g_split[key], value, rtol=0, atol=1e-4 * scale, err_msg=key)

@@ -77,7 +77,7 @@ class RateIO(ctypes.Structure):
     _fields_ = [
         ("B", I64), ("T", I64), ("v", P), ("I", P), ("out", P), ("track_v", P),
         ("track_I", P), ("track_b", I64), ("v_saved", P), ("I_saved", P),
-        ("target_saved", P), ("A_saved", P), ("A_ff", P),
+        ("target_saved", P), ("A_saved", P), ("A_ff", P), ("split", P),
     ]  # fmt: skip
 
 
@@ -109,6 +109,8 @@ SIGNATURES = {
     "wt_cond_recurrent_backward_scratch_bytes": (I64, [I64, I64, I64, I64]),
     "wt_cond_recurrent_backward": (ctypes.c_int, [ctypes.POINTER(Tables), ctypes.POINTER(Side),
                                                   ctypes.POINTER(BackwardIO), P, P]),
+    "wt_rate_split_bytes": (I64, [ctypes.POINTER(RateTables), ctypes.POINTER(RateOperand),
+                                  I64]),
     "wt_rate_forward": (ctypes.c_int, [ctypes.POINTER(RateTables), ctypes.POINTER(RateOperand),
                                        ctypes.POINTER(RateIO), P]),
     "wt_rate_backward": (ctypes.c_int, [ctypes.POINTER(RateTables),

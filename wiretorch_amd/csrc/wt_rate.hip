@@ -29,6 +29,7 @@ typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 64;     // outputs per workgroup, per side
+constexpr int kMaxSlices = 4; // k slices of the forward's split product
 constexpr int kThreads = 256;
 constexpr int kMaxS = 8;
 constexpr int kMaxSeg = 16;
@@ -736,6 +737,228 @@ __global__ __launch_bounds__(kThreads) void rate_back_gemm_kernel(RateBackArgs a
   }
 }
 
+// ---------------------------------------------------------------------------------
+// The forward's split product, for a drive of one recurrent pathway: P[z] = A[:, slice z]
+// Bt[:, slice z]^T in float32, 128 x 128 outputs per workgroup and the k dimension cut
+// into KS slices of whole stages (grid: output columns / 128, rows / 128, KS). Against the
+// 64 x 64 tiles of the fused step, every staged byte feeds twice the matrix-core work
+// (each CU fetches 512 KB per step at configuration 4's shape instead of 1 MB), and the
+// KS slices keep every CU busy (256 x 4096 outputs: 64 tiles x 4 slices). The update
+// launch that follows sums the KS partials of an output in slice order.
+//
+// A stage is 128 bytes of k of 128 rows per operand (16 KB each): thread t fetches chunk
+// t % 8 of rows t / 8 + 32m, m < 4. Stages are fetched kSplitDepth ahead into a ring of
+// registers and stored to LDS in the swizzled layout of the fused tiles (row r's chunk c
+// in slot c ^ swz(r); rows r and r + 32m share swz). Wave w owns the 64 x 64 block (w / 2,
+// w % 2) of the tile — 2 x 2 MFMA blocks of 32 x 32 — over the whole stage, so no partials
+// cross waves. Three LDS buffers: stage s + 2 is stored while stage s is multiplied; one
+// barrier per stage.
+// ---------------------------------------------------------------------------------
+
+constexpr int kBig = 128;
+constexpr int kSplitDepth = 4;
+typedef u32x4 BigLds[kBuffers][2][kBig * 8];
+
+struct BigRegs {
+  u32x4 a[4], b[4];
+};
+
+struct SplitArgs {
+  const char* A;  // row m0 of the tile, column 0 of the slice (bytes)
+  const char* B;
+  int64_t lda, ldb;  // row pitches in bytes
+  float* P;          // [KS][M_pad][ldp]
+  int64_t ldp, M_pad;
+  int32_t stages;    // per slice
+};
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void split_product_kernel(SplitArgs sa) {
+  __shared__ BigLds lds;
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, wi = wave >> 1, wj = wave & 1;
+  const int64_t m0 = (int64_t)blockIdx.y * kBig, n0 = (int64_t)blockIdx.x * kBig;
+  const int n_st = sa.stages;
+  const int64_t k0 = (int64_t)blockIdx.z * n_st * kStageBytes;
+  const char* A = sa.A + m0 * sa.lda + k0;
+  const char* Bt = sa.B + n0 * sa.ldb + k0;
+  const int row = t >> 3, off = (t & 7) * 16, slot_w = (t & 7) ^ swz(row);
+  // a stage's operands (past the last stage: the last one again, never multiplied)
+  auto fetch = [&](BigRegs& r, int st) {
+    const int64_t c = (int64_t)(st < n_st ? st : n_st - 1) * kStageBytes + off;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      r.a[m] = gload16(A + (row + 32 * m) * sa.lda + c);
+      r.b[m] = gload16(Bt + (row + 32 * m) * sa.ldb + c);
+    }
+  };
+  auto store = [&](int buf, const BigRegs& r) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      lds[buf][0][(row + 32 * m) * 8 + slot_w] = r.a[m];
+      lds[buf][1][(row + 32 * m) * 8 + slot_w] = r.b[m];
+    }
+  };
+  // the wave's fragments: rows wi * 64 + 32 i + lane % 32 of A, wj * 64 + 32 j + lane % 32
+  // of Bt; k-step kk takes chunk 2 kk + lane / 32
+  const int r = lane & 31, h = lane >> 5, sw = swz(r);
+  // a stage's fragments, all four k-steps
+  auto read = [&](int buf, Frag (&f)[4]) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int slot = (2 * kk + h) ^ sw;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        f[kk].x[i] = lds[buf][0][(wi * 64 + 32 * i + r) * 8 + slot];
+        f[kk].y[i] = lds[buf][1][(wj * 64 + 32 * i + r) * 8 + slot];
+      }
+    }
+  };
+  Acc c = {};
+  BigRegs ring[kSplitDepth];
+#pragma unroll
+  for (int j = 0; j < kSplitDepth; ++j) fetch(ring[j], j);
+  store(0, ring[0]);
+  fetch(ring[0], kSplitDepth);
+  store(1, ring[1]);
+  fetch(ring[1], kSplitDepth + 1);
+  __syncthreads();
+  Frag cur[4];
+  read(0, cur);
+  // Whole trips of kSplitDepth stages; past the last stage the multiply takes zeros, so
+  // every path issues the same loads and each store's wait leaves the later stages'
+  // loads in flight. Stage s + 1's fragments (its buffer complete since the barrier
+  // before) are read while stage s's MFMAs run: with one wave per SIMD nothing else
+  // hides the LDS latency.
+  const int trips = (n_st + kSplitDepth - 1) / kSplitDepth;
+  for (int trip = 0; trip < trips; ++trip) {
+#pragma unroll
+    for (int j = 0; j < kSplitDepth; ++j) {
+      const int st = trip * kSplitDepth + j;
+      Frag nxt[4];
+      read((st + 1) % kBuffers, nxt);
+      if (st >= n_st) {  // a padding stage: A is zero (no branch around the MFMAs, which
+                         // would let the reads above sink below them)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+          for (int i = 0; i < 2; ++i) cur[kk].x[i] = u32x4{0u, 0u, 0u, 0u};
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) Mma<T>::stage(c, cur[kk]);
+      const int slot = (j + 2) % kSplitDepth;  // static once unrolled
+      store((st + 2) % kBuffers, ring[slot]);
+      fetch(ring[slot], st + 2 + kSplitDepth);
+      __syncthreads();
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) cur[kk] = nxt[kk];
+    }
+  }
+  float* P = sa.P + ((int64_t)blockIdx.z * sa.M_pad + m0) * sa.ldp + n0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        P[(int64_t)(wi * 64 + 32 * i + out_row(v, lane)) * sa.ldp + wj * 64 + 32 * j + (lane & 31)] =
+            c[i][j][v];
+}
+
+// The k slices of a split product of `tiles` output tiles over `stages` stages: doubled
+// while a slice keeps whole stages and the workgroups stay within one per CU (256), at
+// most 4.
+static int split_slices(int64_t tiles, int64_t stages) {
+  int ks = 1;
+  while (ks < kMaxSlices && tiles * ks * 2 <= 256 && stages % (ks * 2) == 0) ks *= 2;
+  return ks;
+}
+
+// Whether a call takes the split products: one recurrent pathway, every padded size a
+// multiple of the 128-wide tiles.
+static bool split_applies(const wt_rate_operand& op) {
+  return op.n_seg == 1 && op.K_rec_pad > 0 && op.B_pad % kBig == 0 && op.N_pad % kBig == 0 &&
+         op.K_rec_pad % kBig == 0;
+}
+
+template <typename T>
+static int forward_slices(const wt_rate_operand& op) {
+  constexpr int kStageK = kStageBytes / (int)sizeof(T);
+  return split_slices((op.N_pad / kBig) * (op.B_pad / kBig), op.K_rec_pad / kStageK);
+}
+
+// Step t after a split product: per (trial, neuron), the recurrent activation (the KS
+// partials summed in slice order), the input pathways', then the currents, voltage and
+// next rate — the fused step's epilogue, one element per thread (neurons fastest).
+template <typename T, int S>
+__global__ __launch_bounds__(kThreads) void rate_update_kernel(RateArgs a, const float* P,
+                                                               int KS) {
+  const wt_rate_tables& tb = a.tab;
+  const wt_rate_operand& op = a.op;
+  const wt_rate_io& io = a.io;
+  const int64_t N = tb.N, B = io.B, T_ = io.T, t = a.t;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= B * N) return;
+  const int64_t b = idx / N, n = idx - b * N;
+  const int64_t el = (b * T_ + t) * N + n;
+  const int64_t path = op.seg[0][2];
+  const float* q = P + b * op.N_pad + n;
+  const int64_t slice = op.B_pad * op.N_pad;
+  float p[kMaxSlices];  // every slice's load first, then the sum in slice order
+#pragma unroll
+  for (int ks = 0; ks < kMaxSlices; ++ks) p[ks] = ks < KS ? q[ks * slice] : 0.0f;
+  float act = p[0];
+#pragma unroll
+  for (int ks = 1; ks < kMaxSlices; ++ks)
+    if (ks < KS) act = act + p[ks];
+  float target[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) target[s] = 0.0f + act * tb.jump[(path * N + n) * S + s];
+  if (io.A_saved) io.A_saved[((path * B + b) * T_ + t) * N + n] = act;
+  for (int64_t k = tb.K_rec; k < tb.K; ++k) {  // the input pathways, in order
+    const float ak = io.A_ff[(k - tb.K_rec) * B * T_ * N + el];
+#pragma unroll
+    for (int s = 0; s < S; ++s) target[s] = target[s] + ak * tb.jump[(k * N + n) * S + s];
+    if (io.A_saved) io.A_saved[k * B * T_ * N + el] = ak;
+  }
+  const bool last = t + 1 == T_;
+  float I[S], I_syn = 0.0f;
+  float v = io.v_saved ? io.v_saved[el] : io.v[b * N + n];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const float d = tb.decay[s];
+    const float I_prev = d != 0.0f ? io.I[(b * S + s) * N + n] : 0.0f;
+    I[s] = d * I_prev + (1.0f - d) * target[s];
+    I_syn = I_syn + I[s] * tb.sign[s];
+  }
+  const float beta = tb.beta[n];
+  v = beta * v + (1.0f - beta) * I_syn;
+  const float r = tb.gain[n] * nonlin(tb.nonlinearity[n], v - tb.theta[n]);
+  if (!last) {
+    io.out[el + N] = r;
+    const int32_t pos = op.rpos ? op.rpos[n] : -1;
+    if (pos >= 0)
+      static_cast<T*>(op.rin)[(((t + 1) & 1) * op.B_pad + b) * op.K_rec_pad + pos] =
+          to_storage<T>(r);
+    if (io.v_saved) io.v_saved[el + N] = v;
+  }
+  if (!io.v_saved || last) io.v[b * N + n] = v;
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+    if (tb.decay[s] != 0.0f || last) io.I[(b * S + s) * N + n] = I[s];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    if (io.target_saved) io.target_saved[el * S + s] = target[s];
+    if (io.I_saved && !last) io.I_saved[(el + N) * S + s] = I[s];
+  }
+  if (io.track_v && (io.track_b < 0 || io.track_b == b)) {
+    const int64_t row = ((io.track_b < 0 ? b : 0) * T_ + t) * N + n;
+    io.track_v[row] = v;
+#pragma unroll
+    for (int s = 0; s < S; ++s) io.track_I[row * S + s] = I[s];
+  }
+}
+
 template <typename T>
 static hipError_t forward_impl(const RateArgs& base, hipStream_t stream) {
   RateArgs a = base;
@@ -755,6 +978,40 @@ static hipError_t forward_impl(const RateArgs& base, hipStream_t stream) {
     case 7: step = rate_step_kernel<T, 7>; break;
     case 8: step = rate_step_kernel<T, 8>; break;
     default: return hipErrorInvalidValue;
+  }
+  if (a.io.split && split_applies(a.op)) {
+    void (*update)(RateArgs, const float*, int) = nullptr;
+    switch (a.tab.S) {
+      case 1: update = rate_update_kernel<T, 1>; break;
+      case 2: update = rate_update_kernel<T, 2>; break;
+      case 3: update = rate_update_kernel<T, 3>; break;
+      case 4: update = rate_update_kernel<T, 4>; break;
+      case 5: update = rate_update_kernel<T, 5>; break;
+      case 6: update = rate_update_kernel<T, 6>; break;
+      case 7: update = rate_update_kernel<T, 7>; break;
+      case 8: update = rate_update_kernel<T, 8>; break;
+      default: return hipErrorInvalidValue;
+    }
+    constexpr int kStageK = kStageBytes / (int)sizeof(T);
+    const int KS = forward_slices<T>(a.op);
+    const dim3 sgrid((unsigned)(a.op.N_pad / kBig), (unsigned)(a.op.B_pad / kBig), (unsigned)KS);
+    const dim3 ugrid((unsigned)((BN + kThreads - 1) / kThreads));
+    SplitArgs sa = {};
+    sa.B = static_cast<const char*>(a.op.Wt);
+    sa.lda = sa.ldb = a.op.K_rec_pad * (int64_t)sizeof(T);
+    sa.P = a.io.split;
+    sa.ldp = a.op.N_pad;
+    sa.M_pad = a.op.B_pad;
+    sa.stages = (int32_t)(a.op.K_rec_pad / kStageK / KS);
+    for (int64_t t = 0; t < a.io.T; ++t) {
+      a.t = (int32_t)t;
+      sa.A = reinterpret_cast<const char*>(static_cast<const T*>(a.op.rin) +
+                                           (t & 1) * a.op.B_pad * a.op.K_rec_pad);
+      hipLaunchKernelGGL(split_product_kernel<T>, sgrid, dim3(kThreads), 0, stream, sa);
+      hipLaunchKernelGGL(update, ugrid, dim3(kThreads), 0, stream, a,
+                         static_cast<const float*>(a.io.split), KS);
+    }
+    return hipGetLastError();
   }
   for (int64_t t = 0; t < a.io.T; ++t) {
     a.t = (int32_t)t;
@@ -854,6 +1111,13 @@ extern "C" int wt_rate_backward(const wt_rate_tables* tab, const wt_rate_operand
   a.io = *io;
   return op->dtype == 1 ? backward_impl<__bf16>(a, (hipStream_t)stream)
                         : backward_impl<float>(a, (hipStream_t)stream);
+}
+
+extern "C" int64_t wt_rate_split_bytes(const wt_rate_tables* tab, const wt_rate_operand* op,
+                                       int64_t B) {
+  if (!tab || !op || !operand_ok(tab, op, B) || tab->K_rec < 1 || !split_applies(*op)) return 0;
+  const int64_t ks = op->dtype == 1 ? forward_slices<__bf16>(*op) : forward_slices<float>(*op);
+  return ks * op->B_pad * op->N_pad * 4;
 }
 
 // ---- hi = bf16(x), lo = bf16(x - hi): x = hi + lo to 2^-17 relative (x - hi is exact in

@@ -170,6 +170,19 @@ class _Plan:
         )  # fmt: skip
 
 
+#: Whether the forward's split product (``wt_rate_split_bytes``) may run where it applies;
+#: off, every step runs the fused kernel.
+SPLIT_PRODUCTS = True
+
+
+def _split_scratch(tables, op, B: int, device) -> torch.Tensor | None:
+    """The split product's scratch, or None where it does not apply."""
+    if not SPLIT_PRODUCTS:
+        return None
+    nbytes = int(_lib.load().wt_rate_split_bytes(tables, op, B))
+    return torch.empty(nbytes // 4, device=device) if nbytes else None
+
+
 def _forward(L: _Plan, x, v, I, track, track_b, saved):
     """One ``wt_rate_forward`` launch sequence; ``v`` ``(B, N)`` and ``I`` ``(B, S, N)`` are
     updated in place. Returns the rates and the tracked variables."""
@@ -182,13 +195,14 @@ def _forward(L: _Plan, x, v, I, track, track_b, saved):
     rin = torch.zeros((2, L.B_pad, max(L.op.K_rec_pad, 1)), dtype=L.op.dtype, device=dev)
     A_ff = _input_activations(L, x)
     v_s, I_s, tgt_s, A_s = saved if saved is not None else (None,) * 4
+    tables, op = L.tables(), L.op.abi(rin, L.B_pad)
+    split = _split_scratch(tables, op, B, dev)
     io = _lib.RateIO(B, T, v.data_ptr(), I.data_ptr(), out.data_ptr(), _lib.ptr(tv),
                      _lib.ptr(tI), track_b, _lib.ptr(v_s), _lib.ptr(I_s), _lib.ptr(tgt_s),
-                     _lib.ptr(A_s), _lib.ptr(A_ff))
+                     _lib.ptr(A_s), _lib.ptr(A_ff), _lib.ptr(split))
     stream = torch.cuda.current_stream(dev).cuda_stream
     with _timed("forward"):
-        _lib.check(_lib.load().wt_rate_forward(L.tables(), L.op.abi(rin, L.B_pad), io,
-                                               stream), "wt_rate_forward")
+        _lib.check(_lib.load().wt_rate_forward(tables, op, io, stream), "wt_rate_forward")
     tracked = {"v": tv, "I": tI} if track else None
     return out, tracked
 
