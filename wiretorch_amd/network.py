@@ -198,13 +198,13 @@ def _long(values) -> torch.Tensor:
 
 def _check_ids(params, key, what):
     ids = sorted(p[key] for p in params)
-    assert ids == list(range(len(ids))), f"{what} must be 0-indexed contiguous, got {ids}"
+    assert ids == list(range(len(ids))), f"{what}: ids {ids} are not 0, 1, 2, ..."
 
 
 def validate(dt, cell_params, cell_type_indices, sides) -> None:
     """Construction checks with messages naming what is wrong (``network.py:1059-1109``)."""
-    assert isinstance(dt, (int, float)) and dt > 0, f"dt must be positive, got {dt}"
-    assert dt <= 100.0, f"dt unusually large ({dt} ms), check units"
+    assert isinstance(dt, (int, float)) and dt > 0, f"time step {dt!r} is not a positive number"
+    assert dt <= 100.0, f"time step {dt} ms exceeds 100 ms (milliseconds expected)"
     _check_ids(cell_params, "cell_id", "cell_ids in cell_params")
     assert cell_type_indices.ndim == 1 and cell_type_indices.shape[0] > 0
     assert np.all((cell_type_indices >= 0) & (cell_type_indices < len(cell_params)))
@@ -212,7 +212,7 @@ def validate(dt, cell_params, cell_type_indices, sides) -> None:
     n_target = np.bincount(cell_type_indices, minlength=len(cell_params))
     for side in sides:
         _check_ids(side.cell_params, "cell_id", f"{side.attribute} source cell_ids")
-        assert side.synapse_params, f"{side.attribute}: synapse_params must not be empty"
+        assert side.synapse_params, f"{side.attribute}: no synapse types given"
         _check_ids(side.synapse_params, "synapse_id", f"{side.attribute} synapse_ids")
         types = side.cell_type_indices
         assert types.ndim == 1 and np.all((types >= 0) & (types < len(side.cell_params)))
@@ -224,8 +224,8 @@ def validate(dt, cell_params, cell_type_indices, sides) -> None:
             assert got == want, f"{side.attribute}: sparse projection {got} != {want}"
             continue
         for (src, tgt), projection in side.projections.items():
-            assert src in sources, f"{side.attribute}: source {src!r} not in its cell_params"
-            assert tgt in targets, f"{side.attribute}: target {tgt!r} not in cell_params"
+            assert src in sources, f"{side.attribute}: no source cell type {src!r}"
+            assert tgt in targets, f"{side.attribute}: no target cell type {tgt!r}"
             want = (int(n_source[sources[src]]), int(n_target[targets[tgt]]))
             got = (projection.n_source, projection.n_target)
             assert got == want, f"{side.attribute} projection ({src!r}, {tgt!r}) {got} != {want}"
@@ -334,7 +334,7 @@ class ProjectionNetwork(nn.Module):
     def storage_dtype(self, dtype) -> None:
         dtype = getattr(torch, dtype) if isinstance(dtype, str) else dtype
         if dtype not in STORAGE_DTYPES:
-            raise ValueError(f"storage_dtype must be one of {STORAGE_DTYPES}, got {dtype}")
+            raise ValueError(f"storage dtype {dtype} not supported (supported: {STORAGE_DTYPES})")
         self._storage_dtype = dtype
 
     def _block(self, side: InputSide, src: str, tgt: str):
@@ -553,14 +553,14 @@ class ProjectionNetwork(nn.Module):
         assert input_spikes.device == self.device, (
             f"input_spikes on {input_spikes.device}, model on {self.device}"
         )
-        assert input_spikes.ndim == 3, f"input_spikes must be 3D, got {input_spikes.shape}"
+        assert input_spikes.ndim == 3, f"input of shape {tuple(input_spikes.shape)}: expected (batch, steps, inputs)"
         assert input_spikes.shape[2] == self.n_inputs, (
-            f"input_spikes shape[2]={input_spikes.shape[2]}, expected {self.n_inputs}"
+            f"input has {input_spikes.shape[2]} channels, the network {self.n_inputs}"
         )
         if input_spikes.shape[0] != self.batch_size:
             raise ValueError(
-                f"Input batch size {input_spikes.shape[0]} != model batch size "
-                f"{self.batch_size}; call reset_state(batch_size=...) first"
+                f"the input holds {input_spikes.shape[0]} trials but the state holds "
+                f"{self.batch_size}: reset the state for the new batch size first"
             )
 
     # ------------------------------------------------------------------
@@ -645,7 +645,7 @@ class ConductanceNetwork(ProjectionNetwork):
     def _register_learnt(self) -> None:
         learn = self.learn
         unknown = set(learn) - set(LEARNABLE) - set(LEARNABLE_SYNAPSE)
-        assert not unknown, f"learn: unknown parameters {sorted(unknown)}"
+        assert not unknown, f"nothing named {sorted(unknown)} can be learnt"
         cells = sorted(self.cell_params, key=lambda c: c["cell_id"])
         names = [c["name"] for c in cells]
         learnt = {

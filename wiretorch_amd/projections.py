@@ -57,7 +57,7 @@ class FrozenProjection(Projection):
     def __init__(self, weights):
         w = _float32(weights)
         if w.ndim != 2:
-            raise ValueError(f"weights must be 2D, got shape {tuple(w.shape)}")
+            raise ValueError(f"weights of shape {tuple(w.shape)}: a (source, target) matrix expected")
         super().__init__(*w.shape)
         self.register_buffer("_weights", w)
 
@@ -75,7 +75,7 @@ class ScalingFactorProjection(Projection):
     def __init__(self, connectome, init_sf: float = 1.0):
         c = _float32(connectome)
         if c.ndim != 2:
-            raise ValueError(f"connectome must be 2D, got shape {tuple(c.shape)}")
+            raise ValueError(f"connectome of shape {tuple(c.shape)}: a (source, target) matrix expected")
         super().__init__(*c.shape)
         self.register_buffer("connectome", c)
         self.log_sf = nn.Parameter(
@@ -99,12 +99,12 @@ class FullRankProjection(Projection):
     def __init__(self, init_weights, mask=None):
         w = _float32(init_weights)
         if w.ndim != 2:
-            raise ValueError(f"init_weights must be 2D, got shape {tuple(w.shape)}")
+            raise ValueError(f"initial weights of shape {tuple(w.shape)}: a (source, target) matrix expected")
         super().__init__(*w.shape)
         self.log_weights = nn.Parameter(torch.log(w + 1e-8))
         m = torch.ones_like(w) if mask is None else _float32(mask)
         if m.shape != w.shape:
-            raise ValueError(f"mask shape {tuple(m.shape)} != {tuple(w.shape)}")
+            raise ValueError(f"mask {tuple(m.shape)} and weights {tuple(w.shape)} differ in shape")
         self.register_buffer("mask", m)
 
     @property
@@ -121,7 +121,7 @@ class LowRankProjection(Projection):
     def __init__(self, n_source, n_target, rank, U_init=None, V_init=None, mask=None):
         super().__init__(n_source, n_target)
         if rank <= 0:
-            raise ValueError(f"rank must be positive, got {rank}")
+            raise ValueError(f"rank {rank} is not a positive number")
         spread = 1.0 / np.sqrt(rank)
         U = torch.randn(n_source, rank) * spread if U_init is None else _float32(U_init)
         V = torch.randn(rank, n_target) * spread if V_init is None else _float32(V_init)
@@ -131,7 +131,7 @@ class LowRankProjection(Projection):
         self.V = nn.Parameter(V)
         m = torch.ones(n_source, n_target) if mask is None else _float32(mask)
         if tuple(m.shape) != (n_source, n_target):
-            raise ValueError(f"mask shape {tuple(m.shape)} != ({n_source}, {n_target})")
+            raise ValueError(f"mask {tuple(m.shape)} is not ({n_source}, {n_target})")
         self.register_buffer("mask", m)
 
     @property
@@ -154,13 +154,13 @@ class SignedProjection(Projection):
     def __init__(self, init_weights, mask=None):
         w = _float32(init_weights)
         if w.ndim != 2:
-            raise ValueError(f"init_weights must be 2D, got shape {tuple(w.shape)}")
+            raise ValueError(f"initial weights of shape {tuple(w.shape)}: a (source, target) matrix expected")
         super().__init__(*w.shape)
         self.weights = nn.Parameter(w.clone())
         if mask is not None:
             m = _float32(mask)
             if m.shape != w.shape:
-                raise ValueError(f"mask shape {tuple(m.shape)} != {tuple(w.shape)}")
+                raise ValueError(f"mask {tuple(m.shape)} and weights {tuple(w.shape)} differ in shape")
             self.register_buffer("mask", m)
         else:
             self.mask = None

@@ -62,7 +62,7 @@ class RatePhysiology:
 def _check_parameters(params: list[dict], required, what: str) -> None:
     for p in params:
         missing = [k for k in required if k not in p]
-        assert not missing, f"{what}: {p.get('name', p)} is missing {missing}"
+        assert not missing, f"{what}: {p.get('name', p)} lacks {missing}"
 
 
 class RateNetwork(ProjectionNetwork):
@@ -83,7 +83,7 @@ class RateNetwork(ProjectionNetwork):
                 f"cell type {cell['name']!r}: nonlinearity must be one of "
                 f"{sorted(NONLINEARITIES)}, got {cell['nonlinearity']!r}"
             )
-            assert cell["tau_mem"] >= 0, f"cell type {cell['name']!r}: tau_mem < 0"
+            assert cell["tau_mem"] >= 0, f"cell type {cell['name']!r}: negative tau_mem"
         for side in sides:
             _check_parameters(side.synapse_params, SYNAPSE_PARAMETERS, side.attribute)
             for synapse in side.synapse_params:
@@ -111,7 +111,7 @@ class RateNetwork(ProjectionNetwork):
     def storage_dtype(self, dtype) -> None:
         dtype = getattr(torch, dtype) if isinstance(dtype, str) else dtype
         if dtype not in STORAGE_DTYPES:
-            raise ValueError(f"storage_dtype must be one of {STORAGE_DTYPES}, got {dtype}")
+            raise ValueError(f"storage dtype {dtype} not supported (supported: {STORAGE_DTYPES})")
         self._storage_dtype = dtype
 
     def _register_physiology(self) -> None:
