@@ -50,11 +50,16 @@ typedef struct {
   const float* scale;    /* (K,N) */
   const float* dt;       /* 0-d */
   const float* surr;     /* 0-d */
-  /* The same per-neuron values deduplicated (used by wt_cond_run): n_types <= 256 rows
-   * of (theta, U_reset, E_L, C_m, beta, n_ref, scale[0..K-1]); type_of (N,) picks a row. */
+  /* The same per-neuron values deduplicated (used by wt_cond_run): rows of (theta,
+   * U_reset, E_L, C_m, beta, n_ref, scale[0..K-1]). Without range_rows: n_types <= 256
+   * rows, type_of (N,) picks a row. With range_rows (n_ranges, 256), the rows of the
+   * target range of geometry range_n holding neuron n are range_rows[n / range_n][0 ..
+   * n_types), n_types <= 256 then being the largest count over the ranges, and type_of[n]
+   * indexes that list. */
   const float* types;
   const int32_t* type_of;
   int64_t n_types;
+  const int32_t* range_rows;
   int64_t N, S, K, K_rec;
 } wt_tables;
 

@@ -11,6 +11,8 @@
   same step's spikes (bit for bit).
 """
 
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -175,6 +177,42 @@ def test_sparse_network_matches_oracle(B):
     assert s_ref[:, :200].sum() > 0
     differs = (s_gpu[:, :200] != s_ref[:, :200]).any(axis=(0, 2))
     assert not differs.any(), f"rasters differ from step {int(np.argmax(differs))}"
+
+
+def test_more_parameter_rows_than_one_table(monkeypatch):
+    """Per-neuron thresholds in 500 blocks of 10 neurons: more distinct parameter rows
+    than one workgroup's LDS table holds (256), at most about 100 in each target range, so
+    every workgroup stages its own range's rows (``engine._range_types``). The raster over
+    200 steps equals the oracle's and the final voltages agree within 1e-5 relative."""
+    B, T = 2, 200
+    wl = synthetic.fly_scale(N=5000, n_types=200, mean_degree=120, k_max=1500, B=B, T=T,
+                             frac_sensory=0.1, rate_hz=100.0)
+    x = torch.from_numpy(wl.x).float()
+    dtheta = torch.from_numpy(np.random.default_rng(5).uniform(-1.5, 1.5, 500)
+                              .astype(np.float32))[torch.arange(wl.N) // 10]
+    p_cpu = dataclasses.replace(wl.physiology, theta=wl.physiology.theta + dtheta)
+    v, g, counter = synthetic.rest_state(B, wl.N, 2)
+    ref = oracle_engine.simulate(v, g, x, wl.drive, p_cpu, refractory=counter)
+    drive_gpu, p_gpu = synthetic.sparse_drive(wl.drive.sparse_recurrent.to(DEV),
+                                              wl.drive.sparse_feedforward.to(DEV), wl.N, 0.1, DEV)
+    p_gpu = dataclasses.replace(p_gpu, theta=p_gpu.theta + dtheta.to(DEV))
+    seen = []
+    real = engine._range_types
+
+    def spy(*args):
+        out = real(*args)
+        seen.append(out[1] is not None)
+        return out
+
+    monkeypatch.setattr(engine, "_range_types", spy)
+    v_gpu, g_gpu, counter_gpu = synthetic.rest_state(B, wl.N, 2, DEV)
+    out = engine.simulate(v_gpu, g_gpu, x.to(DEV), drive_gpu, p_gpu, refractory=counter_gpu)
+    assert seen == [True], seen
+    s_ref, s_gpu = ref.spikes.numpy(), out.spikes.cpu().numpy()
+    assert s_ref.sum() > 0
+    differs = (s_gpu != s_ref).any(axis=(0, 2))
+    assert not differs.any(), f"rasters differ from step {int(np.argmax(differs))}"
+    np.testing.assert_allclose(out.v.cpu().numpy(), ref.v.numpy(), rtol=1e-5, atol=1e-4)
 
 
 @pytest.mark.slow

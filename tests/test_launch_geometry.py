@@ -52,3 +52,47 @@ def test_group_limit(monkeypatch):
     assert engine.geometry(32, 10_000, 3, N_CU, MAX_LDS) == (8, 32, 320)
     with pytest.raises(ValueError):
         engine.geometry(64, 10_000_000, 3, N_CU, MAX_LDS)
+
+
+# ---------------------------------------------------------------------------------
+# Per-range parameter rows (engine._range_types): more distinct rows than one LDS table
+# holds, as long as each target range holds at most MAX_TYPES of them.
+# ---------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("N,block,range_n", [(5000, 10, 1024), (4321, 7, 640), (3000, 3, 768)])
+def test_range_rows_cover_every_neuron(N, block, range_n):
+    """Rows in contiguous blocks of neurons (shuffled row ids): each neuron finds its own
+    row through its range's list, the lists ascend, and none exceeds MAX_TYPES."""
+    import torch
+
+    n_rows = -(-N // block)
+    ids = torch.randperm(n_rows, generator=torch.Generator().manual_seed(N))
+    type_of = ids[torch.arange(N) // block].to(torch.int32)
+    local, range_rows, most = engine._range_types(type_of, n_rows, range_n)
+    assert n_rows > engine.MAX_TYPES and range_rows is not None
+    assert range_rows.shape == (-(-N // range_n), engine.MAX_TYPES)
+    assert 1 <= most <= engine.MAX_TYPES
+    rng = torch.arange(N) // range_n
+    assert torch.equal(range_rows[rng, local.long()], type_of)
+    assert bool((local >= 0).all()) and bool((local < most).all())
+    for r in range(range_rows.shape[0]):
+        n_r = int(torch.unique(type_of[rng == r]).numel())
+        assert bool((range_rows[r, 1:n_r] > range_rows[r, : n_r - 1]).all())
+
+
+def test_few_rows_keep_the_global_table():
+    import torch
+
+    type_of = torch.randint(0, 200, (3000,), dtype=torch.int32)
+    local, range_rows, most = engine._range_types(type_of, 200, 512)
+    assert range_rows is None and most == 200 and local is type_of
+
+
+def test_interleaved_rows_are_refused():
+    """Distinct rows spread over a range beyond MAX_TYPES: refused, with the reason."""
+    import torch
+
+    type_of = (torch.arange(4000) % 1000).to(torch.int32)
+    with pytest.raises(NotImplementedError, match="distinct per-neuron parameter rows"):
+        engine._range_types(type_of, 1000, 1024)

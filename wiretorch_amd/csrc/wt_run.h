@@ -405,8 +405,10 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   for (int64_t i = threadIdx.x; i < acc_len; i += blockDim.x) acc[i] = 0.0;
   {
     const int64_t cols = kTypeCols + K;
+    // this range's rows: all of them, or its own list (range_rows)
+    const int32_t* own = A.tab.range_rows ? A.tab.range_rows + (int64_t)r * kMaxLdsTypes : nullptr;
     for (int64_t ty = threadIdx.x; ty < A.tab.n_types; ty += blockDim.x) {
-      const float* src = A.tab.types + ty * cols;
+      const float* src = A.tab.types + (own ? (int64_t)own[ty] : ty) * cols;
       float* dst = s_types + ty * kRow;
       const Leak lk = leak(src[3], src[4], dt);
       dst[0] = src[0];

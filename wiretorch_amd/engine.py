@@ -547,19 +547,44 @@ def _device_scalar(value, device) -> torch.Tensor:
 def _type_table(tables: dict, scale: torch.Tensor, device):
     """The per-neuron values the forward reads — theta, U_reset, E_L, C_m, beta, n_ref
     and each pathway's kernel scale — as rows of distinct values and each neuron's row:
-    networks built from cell types have a handful, which the kernel keeps in LDS."""
+    networks built from cell types have few, which the kernel keeps in LDS."""
     N = tables["theta"].shape[0]
     n_ref = (tables["n_ref"].float() if tables["n_ref"] is not None
              else torch.zeros(N, device=device))
     cols = [tables[n] for n in ("theta", "U_reset", "E_L", "C_m", "beta")] + [n_ref]
     rows = torch.cat([torch.stack(cols, dim=1), _f32(scale, device).T], dim=1)
     types, type_of = torch.unique(rows, dim=0, return_inverse=True)
-    if types.shape[0] > MAX_TYPES:
-        raise NotImplementedError(
-            f"{types.shape[0]} distinct per-neuron parameter rows (at most {MAX_TYPES}: "
-            "physiology and kernel scales are expected to follow cell types)"
-        )
     return types.contiguous(), type_of.to(torch.int32).contiguous()
+
+
+def _range_types(type_of: torch.Tensor, n_rows: int, range_n: int):
+    """The rows each workgroup stages in LDS. With at most ``MAX_TYPES`` distinct rows,
+    all of them: ``(type_of, None, n_rows)``. Otherwise per target range of ``range_n``
+    neurons its own rows (at most ``MAX_TYPES``: networks whose neurons are grouped by
+    cell type meet this with thousands of types): ``(local, range_rows, n_local)``, where
+    ``range_rows[r, j]`` is the j-th row of range r (rows ascending, the rest padded with
+    row 0), ``local[n]`` the index of neuron n's row there and ``n_local`` the largest
+    count."""
+    if n_rows <= MAX_TYPES:
+        return type_of, None, n_rows
+    N = type_of.numel()
+    n_ranges = -(-N // range_n)
+    rng = torch.arange(N, device=type_of.device) // range_n
+    keys, inv = torch.unique(rng * n_rows + type_of.long(), return_inverse=True)
+    key_range = keys // n_rows
+    counts = torch.bincount(key_range, minlength=n_ranges)
+    most = int(counts.max())
+    if most > MAX_TYPES:
+        raise NotImplementedError(
+            f"a range of {range_n} neurons holds {most} distinct per-neuron parameter rows "
+            f"(at most {MAX_TYPES}: physiology and kernel scales are expected to follow cell "
+            "types, with the neurons of a type next to each other)")
+    first = torch.cumsum(counts, 0) - counts  # each range's first key
+    local = (inv - first[rng]).to(torch.int32).contiguous()
+    range_rows = torch.zeros((n_ranges, MAX_TYPES), dtype=torch.int32, device=type_of.device)
+    j = torch.arange(keys.numel(), device=type_of.device) - first[key_range]
+    range_rows[key_range, j] = (keys % n_rows).to(torch.int32)
+    return local, range_rows, most
 
 
 def _key(*tensors) -> tuple:
@@ -601,6 +626,8 @@ class _Plan:
     rec: _Side
     ff: _Side
     geo: tuple
+    #: (type_of, range_rows or None, n_types) of ``_range_types`` for this geometry
+    range_types: tuple
     #: 0-d float64 device tensor: the largest |activation| (the kernel's fixed point)
     bound: torch.Tensor
     max_list: int
@@ -625,6 +652,7 @@ class _Plan:
 
     def abi_tables(self, scale: torch.Tensor) -> _lib.Tables:
         t = self.tables
+        type_of, range_rows, n_types = self.range_types
         return _lib.Tables(
             t["theta"].data_ptr(), t["U_reset"].data_ptr(), t["E_L"].data_ptr(),
             t["C_m"].data_ptr(), t["beta"].data_ptr(),
@@ -632,7 +660,8 @@ class _Plan:
             t["E_syn"].data_ptr(), t["g_clip"].data_ptr(), t["decay"].data_ptr(),
             t["jump"].data_ptr(), t["made"].data_ptr(), scale.data_ptr(),
             t["dt"].data_ptr(), t["surr"].data_ptr(), t["types"].data_ptr(),
-            t["type_of"].data_ptr(), int(t["types"].shape[0]), self.N, self.S, self.K, self.K_rec,
+            type_of.data_ptr(), n_types, _lib.ptr(range_rows), self.N, self.S, self.K,
+            self.K_rec,
         )  # fmt: skip
 
 
@@ -688,9 +717,13 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
 
     # the tables (and the distinct-row search) are rebuilt only when a source changes
     tables = _cached(("tables", str(device)) + _key(*sources), sources, make_tables)
+    types, type_of = tables["types"], tables["type_of"]
+    range_types = _cached(("range_types", range_n) + _key(types, type_of), (types, type_of),
+                          lambda: _range_types(type_of, int(types.shape[0]), range_n))
     return _Plan(
         B=B, T=T, N=N, S=S, K_rec=K_rec, K_ff=K_ff, n_in=n_in, tables=tables, rec=rec,
-        ff=ff, geo=(groups, R, range_n), bound=bound, max_list=max_list,
+        ff=ff, geo=(groups, R, range_n), range_types=range_types, bound=bound,
+        max_list=max_list,
         refractory=p.n_ref is not None, probabilities=probabilities, track=track,
         track_b=(-1 if track_batch_idx is None else int(track_batch_idx)) if track else 0,
         stream=torch.cuda.current_stream(device).cuda_stream, device=device,
