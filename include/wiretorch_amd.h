@@ -60,6 +60,11 @@ typedef struct {
   const int32_t* type_of;
   int64_t n_types;
   const int32_t* range_rows;
+  /* The NMDA Mg block (conductance/dynamics.py:110-129): each synapse type's current
+   * scaled by B(v) = sigmoid(mg_a v - mg_lc), mg_lc = log(mg / mg_k), -inf for a type
+   * without one; both (S,), or NULL when no type has a block. */
+  const float* mg_a;
+  const float* mg_lc;
   int64_t N, S, K, K_rec;
 } wt_tables;
 

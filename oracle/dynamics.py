@@ -7,7 +7,8 @@ bit for bit (same torch CPU kernels, same association order):
 * ``SurrGradSpike`` — ``src/wiretorch/training_utils/surrogate_gradients.py:9-33``;
 * ``jumps`` — ``conductance/dynamics.py:95-100``;
 * ``spike`` — ``conductance/dynamics.py:103-107``;
-* ``membrane`` — ``conductance/dynamics.py:116-143`` (no Mg block, no adaptation);
+* ``mg_block`` — ``conductance/dynamics.py:110-113``;
+* ``membrane`` — ``conductance/dynamics.py:116-143`` (the Mg block, no adaptation);
 * ``simulate`` — ``conductance/dynamics.py:146-237`` (no gating, no adaptation);
 * ``refractory_mask`` / ``held_at_reset`` / ``count_down`` —
   ``network_simulators/network.py:294-318``;
@@ -86,9 +87,17 @@ def spike(v, p, held=None):
     return s if held is None else s * (1 - held)
 
 
+def mg_block(v, mg_c, mg_a):
+    """``(B, N, S)``: each synapse type's Mg block at ``v``, ``1 / (1 + mg_c exp(-mg_a
+    v))`` evaluated as ``sigmoid(mg_a v - log mg_c)`` (exactly 1 where ``mg_c = 0``)."""
+    return torch.sigmoid(mg_a * v[:, :, None] - torch.log(mg_c))
+
+
 def membrane(v, s, g, p):
     """Currents and the voltage after the exponential-Euler step, reset where ``s``."""
     g_total = torch.minimum(g.sum(dim=2).clamp(min=0.0), p.g_clip)
+    if getattr(p, "mg_c", None) is not None:  # the block scales each type's conductance
+        g_total = g_total * mg_block(v, p.mg_c, p.mg_a)
     I = g_total * (v[:, :, None] - p.E_syn)
     rate = -torch.log1p(p.beta - 1) / p.dt
     g_L = p.C_m * rate

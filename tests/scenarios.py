@@ -67,6 +67,14 @@ GRAD_STEPS = 100
 READOUT_SEED = 7
 
 
+def mg_block(synapses, mg):
+    """``synapses`` with a Mg block of ``mg`` mM on the NMDA types (unchanged for None;
+    reference ``tests/networks.py:113-117``)."""
+    if mg is None:
+        return synapses
+    return [{**s, "mg": mg} if s["name"] == "NMDA" else s for s in synapses]
+
+
 def combined_physiology():
     cells = [dict(c) for c in MITRAL_CELLS]
     cells += [{**c, "cell_id": c["cell_id"] + 1} for c in CELLS]
@@ -155,9 +163,10 @@ def _input_rng(seed, input_seed):
 
 def recurrent(batch_size, seed, scaling_factors=False, n=N, n_ff=N_FF, n_steps=200,
               input_seed=0, learn=None, learnt_weights=False, tau_ref=None,
-              recurrent_gradients=False, dt=DT, surrgrad_scale=5.0):
+              recurrent_gradients=False, dt=DT, surrgrad_scale=5.0, mg=None):
     """``ConductanceLIFNetwork``: frozen weights, perturbed scaling factors, or learnt
-    recurrent weights (reference ``tests/networks.py:276-355``)."""
+    recurrent weights; ``mg`` mM of Mg block on the NMDA types (reference
+    ``tests/networks.py:276-355``)."""
     rng, types, w_rec, w_ff = _structure(seed, n, n_ff)
     ff_types = np.zeros(n_ff, dtype=np.int64)
     rec_blocks = per_type_blocks(w_rec, types, types, REC_NAMES, REC_NAMES)
@@ -174,7 +183,7 @@ def recurrent(batch_size, seed, scaling_factors=False, n=N, n_ff=N_FF, n_steps=2
         dt=dt, rec_projections=rec, ff_projections=ff,
         cell_type_indices=types, cell_type_indices_FF=ff_types,
         cell_params=with_refractory(CELLS, tau_ref), cell_params_FF=MITRAL_CELLS,
-        synapse_params=SYNAPSES, synapse_params_FF=MITRAL_SYNAPSES,
+        synapse_params=mg_block(SYNAPSES, mg), synapse_params_FF=mg_block(MITRAL_SYNAPSES, mg),
         surrgrad_scale=surrgrad_scale, batch_size=batch_size, learn=learn,
         recurrent_gradients=recurrent_gradients,
     )  # fmt: skip
@@ -189,11 +198,12 @@ def recurrent(batch_size, seed, scaling_factors=False, n=N, n_ff=N_FF, n_steps=2
 
 
 def feedforward(batch_size, seed, learnt_weights=False, probabilities=False, n=N,
-                n_ff=N_FF, n_steps=200, input_seed=0, learn=None, tau_ref=None):
+                n_ff=N_FF, n_steps=200, input_seed=0, learn=None, tau_ref=None, mg=None):
     """``FeedforwardConductanceLIFNetwork`` on external inputs and a recurrent network's
-    neurons (reference ``tests/networks.py:358-429``)."""
+    neurons; ``mg`` as for ``recurrent`` (reference ``tests/networks.py:358-429``)."""
     rng, types, w_rec, w_ff = _structure(seed, n, n_ff)
     cells, synapses = combined_physiology()
+    synapses = mg_block(synapses, mg)
     names = [c["name"] for c in cells]
     row_types = np.concatenate([np.zeros(n_ff, dtype=np.int64), types + 1])
     weights = np.concatenate([w_ff, w_rec])

@@ -22,7 +22,8 @@ class Tables(ctypes.Structure):
         ("theta", P), ("U_reset", P), ("E_L", P), ("C_m", P), ("beta", P), ("n_ref", P),
         ("E_syn", P), ("g_clip", P), ("decay", P), ("jump", P), ("made", P), ("scale", P),
         ("dt", P), ("surr", P), ("types", P), ("type_of", P), ("n_types", I64),
-        ("range_rows", P), ("N", I64), ("S", I64), ("K", I64), ("K_rec", I64),
+        ("range_rows", P), ("mg_a", P), ("mg_lc", P), ("N", I64), ("S", I64), ("K", I64),
+        ("K_rec", I64),
     ]  # fmt: skip
 
 

@@ -41,11 +41,22 @@ __host__ __device__ inline Leak leak(float C_m, float beta, float dt) {
   return {rate, C_m * rate};
 }
 
-// Synapse tables of one call, held by every thread (S entries each).
+// Synapse tables of one call, held by every thread (S entries each). With `mg`, each
+// type's conductance is scaled by its Mg block B(v) = sigmoid(mg_a v - mg_lc), mg_lc =
+// log(mg / mg_k) (-inf for a type without one: B = 1 exactly).
 template <int S>
 struct Synapses {
   float E[S], clip[S], decay_r[S], decay_d[S], jump_r[S], jump_d[S];
+  float mg_a[S], mg_lc[S];
+  bool mg;
 };
+
+// The Mg block at v (conductance/dynamics.py:110-113): 1 / (1 + exp(-(mg_a v - mg_lc))),
+// the product and the difference rounded as torch rounds them.
+__host__ __device__ inline float mg_block(float v, float mg_a, float mg_lc) {
+  const float z = mg_a * v - mg_lc;
+  return 1.0f / (1.0f + expf(-z));
+}
 
 // Spike and refractory part of a step (dynamics.py:103-107, network.py:294-318):
 // returns the spike; r is what holds the voltage at reset, held the refractory mask.
@@ -79,6 +90,7 @@ __host__ __device__ inline float membrane(float v, float r, const float (&gr)[S]
   for (int s = 0; s < S; ++s) {
     G[s] = gr[s] + gd[s];
     Gc[s] = fminf(fmaxf(G[s], 0.0f), syn.clip[s]);
+    if (syn.mg) Gc[s] = Gc[s] * mg_block(v, syn.mg_a[s], syn.mg_lc[s]);
     I[s] = Gc[s] * (v - syn.E[s]);
   }
   I_leak = lk.g_L * (v - E_L);
@@ -95,7 +107,8 @@ __host__ __device__ inline float membrane(float v, float r, const float (&gr)[S]
 // a = exp(-x), x = dt (rate + Gt / C_m):
 //   d v_next / d v   = a                      (J' = g_L + Gt, 1 - phi (g_L + Gt) = a)
 //   d v_next / d Gc_s = -(phi_G J + phi (v - E_s)),  phi_G = (a dt / C_m - phi) / (g_L + Gt)
-// and the physiology terms below.
+// and the physiology terms below. With the Mg block Gc_s = C_s B_s(v) (C_s the clipped
+// conductance): dL/dC_s = dL/dGc_s B_s, and v gains dL/dGc_s C_s mg_a_s B_s (1 - B_s).
 struct MembraneAdjoint {
   float dv;      // dL/dv entering the step (membrane part)
   float phi, a, inv_g, J, Gt;
@@ -105,10 +118,12 @@ template <int S>
 __host__ __device__ inline MembraneAdjoint membrane_adjoint(
     float gx, float v, const float (&G)[S], const Synapses<S>& syn, float E_L, float C_m,
     Leak lk, float dt, float (&dG)[S], float (&Gc_out)[S]) {
-  float Gc[S], I[S];
+  float Gc[S], I[S], C[S], Bm[S];
 #pragma unroll
   for (int s = 0; s < S; ++s) {
-    Gc[s] = fminf(fmaxf(G[s], 0.0f), syn.clip[s]);
+    C[s] = fminf(fmaxf(G[s], 0.0f), syn.clip[s]);
+    Bm[s] = syn.mg ? mg_block(v, syn.mg_a[s], syn.mg_lc[s]) : 1.0f;
+    Gc[s] = syn.mg ? C[s] * Bm[s] : C[s];
     I[s] = Gc[s] * (v - syn.E[s]);
     Gc_out[s] = Gc[s];
   }
@@ -122,15 +137,20 @@ __host__ __device__ inline MembraneAdjoint membrane_adjoint(
   float phi_G = (a * dt / C_m - phi) * inv_g;
   float k0 = -gx * (phi_G * J + phi * v);
   float k1 = gx * phi;
+  float dv = gx * a;
 #pragma unroll
   for (int s = 0; s < S; ++s) {
-    float d = k0 + k1 * syn.E[s];
+    float d = k0 + k1 * syn.E[s];  // dL/dGc_s
+    if (syn.mg) {  // through B_s(v), then on to the clipped conductance
+      dv = dv + d * C[s] * (Bm[s] * (1.0f - Bm[s])) * syn.mg_a[s];
+      d = d * Bm[s];
+    }
     // torch: clamp(min=0) passes the gradient where G >= 0; minimum(., clip) splits it
     // evenly where G == clip.
     float pass = G[s] < syn.clip[s] ? 1.0f : (G[s] == syn.clip[s] ? 0.5f : 0.0f);
     dG[s] = G[s] >= 0.0f ? d * pass : 0.0f;
   }
-  return {gx * a, phi, a, inv_g, J, Gt};
+  return {dv, phi, a, inv_g, J, Gt};
 }
 
 // Surrogate gradient of the spike at x = v - theta (surrogate_gradients.py:30-33).

@@ -151,6 +151,12 @@ __device__ inline void load_synapses(const wt_tables& tab, Synapses<S>& syn) {
     syn.jump_r[s] = tab.jump[s];
     syn.jump_d[s] = tab.jump[S + s];
   }
+  syn.mg = tab.mg_a != nullptr;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    syn.mg_a[s] = syn.mg ? tab.mg_a[s] : 0.0f;
+    syn.mg_lc[s] = syn.mg ? tab.mg_lc[s] : 0.0f;
+  }
 }
 
 // Exact accumulation of activations. Each product is rounded to a multiple of 2^-f and

@@ -21,8 +21,9 @@ What differs from the reference is underneath:
 
 The engine runs only on a GPU with the library built; it raises otherwise. Not
 supported (raising ``NotImplementedError``): per-step gradient retention
-(``retain``), float16 storage, sampled spikes, presynaptic dynamics, Mg block,
-adaptation.
+(``retain``), float16 storage, sampled spikes, presynaptic dynamics, adaptation. The
+NMDA Mg block (``Physiology.mg_c`` / ``mg_a``) is evaluated in the forward and both
+backward passes.
 """
 
 from __future__ import annotations
@@ -660,8 +661,8 @@ class _Plan:
             t["E_syn"].data_ptr(), t["g_clip"].data_ptr(), t["decay"].data_ptr(),
             t["jump"].data_ptr(), t["made"].data_ptr(), scale.data_ptr(),
             t["dt"].data_ptr(), t["surr"].data_ptr(), t["types"].data_ptr(),
-            type_of.data_ptr(), n_types, _lib.ptr(range_rows), self.N, self.S, self.K,
-            self.K_rec,
+            type_of.data_ptr(), n_types, _lib.ptr(range_rows), _lib.ptr(t["mg_a"]),
+            _lib.ptr(t["mg_lc"]), self.N, self.S, self.K, self.K_rec,
         )  # fmt: skip
 
 
@@ -703,7 +704,7 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
                         lambda: bound + ff_max * x_max)
     names = ("theta", "U_reset", "E_L", "C_m", "beta", "E_syn", "g_clip", "decay", "jump")
     sources = tuple(getattr(p, name) for name in names) + (
-        drive.made, drive.scale, p.dt, p.surr_scale, p.n_ref)
+        drive.made, drive.scale, p.dt, p.surr_scale, p.n_ref, p.mg_c, p.mg_a)
 
     def make_tables():
         tables = {name: _f32(getattr(p, name), device) for name in names}
@@ -713,6 +714,12 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
         tables["n_ref"] = (None if p.n_ref is None
                            else p.n_ref.to(device=device, dtype=torch.int32).contiguous())
         tables["types"], tables["type_of"] = _type_table(tables, drive.scale, device)
+        if p.mg_c is not None:  # the Mg block: log(mg_c) taken by torch on the CPU, as
+            # the reference's CPU path takes it (-inf for a type without a block)
+            tables["mg_a"] = _f32(p.mg_a, device)
+            tables["mg_lc"] = torch.log(p.mg_c.detach().cpu().float()).to(device)
+        else:
+            tables["mg_a"] = tables["mg_lc"] = None
         return tables
 
     # the tables (and the distinct-row search) are rebuilt only when a source changes
@@ -1010,8 +1017,6 @@ def simulate(
         raise NotImplementedError("per-step gradient retention (track_gradients)")
     if gating is not None or drive.gates or adaptation is not None or p.adapt is not None:
         raise NotImplementedError("presynaptic dynamics and adaptation")
-    if p.mg_c is not None:
-        raise NotImplementedError("the NMDA Mg block")
     if p.spike_mode != "deterministic":
         raise NotImplementedError("sampled spikes")
     if p.storage_dtype != torch.float32:

@@ -24,9 +24,10 @@ bit-identical inputs:
 * state at rest (``v = U_reset``, ``g = 0`` laid out ``(B, 2, S, N)``):
   ``conductance/network.py:248-255``.
 
-Presynaptic dynamics (short-term plasticity, receptor saturation), the NMDA Mg block
-and spike-frequency adaptation are not part of this build: a network configured with
-any of them raises ``NotImplementedError``.
+The NMDA Mg block is built (``synapses.mg_block_tables``; ``conductance/network.py:
+138-141``). Presynaptic dynamics (short-term plasticity, receptor saturation) and
+spike-frequency adaptation are not part of this build: a network configured with any of
+them raises ``NotImplementedError``.
 
 ``Drive`` also accepts a sparse form (``connectome.Connectome``) for connectomes too
 large for the reference's dense per-pathway rows (fly scale).
@@ -42,7 +43,7 @@ from torch import nn
 
 from wiretorch_amd.connectome import Connectome
 from wiretorch_amd.projections import Projection, SparseProjection, projection_mask
-from wiretorch_amd.synapses import SynapseRegistry
+from wiretorch_amd.synapses import SynapseRegistry, mg_block_tables
 from wiretorch_amd.type_parameters import (
     TypeParameters,
     learnt_synapses,
@@ -242,8 +243,6 @@ def _unsupported(cell_params, synapse_lists, stp) -> None:
             raise NotImplementedError("spike-frequency adaptation is not supported")
     for synapses in synapse_lists:
         for syn in synapses:
-            if syn.get("mg", 0.0):
-                raise NotImplementedError("the NMDA Mg block is not supported")
             if syn.get("saturation", 0.0):
                 raise NotImplementedError("saturating synapses are not supported")
     if any(stp):
@@ -634,6 +633,11 @@ class ConductanceNetwork(ProjectionNetwork):
         for name in SYNAPSE_PARAMETERS:
             self.register_buffer(name, self.registry.table(name))
         self.register_buffer("g_clip", self.registry.table("g_clip", default=float("inf")))
+        # from the synapse parameters, not saved with the module (state dicts load between
+        # networks with and without a block)
+        for name, table in mg_block_tables(self.registry).items():
+            self.register_buffer(name, table, persistent=False)
+        self._mg_block = bool(self.mg_c.any())
         tau_ref = self._per_neuron("tau_ref", 0.0)
         assert bool((tau_ref >= 0).all()), "cell_params: tau_ref must be >= 0"
         self.register_buffer("tau_ref", tau_ref, persistent=False)
@@ -731,6 +735,8 @@ class ConductanceNetwork(ProjectionNetwork):
             spike_mode=self.spike_mode,
             storage_dtype=self.storage_dtype,
             n_ref=self.n_ref if self._refractory else None,
+            mg_c=self.mg_c if self._mg_block else None,
+            mg_a=self.mg_a if self._mg_block else None,
         )
 
     def _initial_state(self):

@@ -92,3 +92,20 @@ def _listed(syn: dict) -> bool:
 def _makers(syn: dict) -> list[int]:
     """The source cell types an entry names: one ``cell_id``, or a list of them."""
     return [int(c) for c in syn["cell_id"]] if _listed(syn) else [int(syn["cell_id"])]
+
+
+#: The Mg block's parameter defaults: no block (``mg``, mM), the Jahr-Stevens voltage
+#: slope (``mg_slope``, 1/mV) and dissociation constant (``mg_k``, mM)
+#: (``conductance/synapses.py:39-41``).
+MG, MG_SLOPE, MG_K = 0.0, 0.062, 3.57
+
+
+def mg_block_tables(registry: "SynapseRegistry") -> dict[str, torch.Tensor]:
+    """Per synapse type the voltage-dependent Mg block ``B(v) = 1 / (1 + mg_c exp(-mg_a
+    v))`` that scales its current: ``mg_c = mg / mg_k``, ``mg_a = mg_slope``; ``mg = 0``
+    (a type without one) gives ``B = 1`` (``conductance/synapses.py:44-56``)."""
+    mg = registry.table("mg", default=MG)
+    if bool((mg < 0).any()):
+        raise ValueError("synapse params: a negative Mg concentration")
+    return {"mg_c": mg / registry.table("mg_k", default=MG_K),
+            "mg_a": registry.table("mg_slope", default=MG_SLOPE)}
