@@ -10,7 +10,8 @@
   bars of configurations 1 and 3, both ways.
 * Two training steps of configuration 3's network with the learnt weights changed in
   between: the second takes the new weights through the cached layout of the dense
-  pathways (no new compression), to the same bar.
+  pathways (no new compression), to the same bar; and the network's synapse-by-synapse
+  form of those weights (what the engine is given by default) following a changed mask.
 * Configuration 3 (training step: per-synapse learnt weights, learnt per-type tau_mem and
   theta, fast-sigmoid surrogate of slope 10, squared error of 20 ms-binned rates against
   gamma(2, 5 Hz) targets, dt 1 ms): over 100 steps, the same raster, the loss within 1e-5
@@ -24,6 +25,7 @@ import torch
 import oracle.dynamics as oracle_engine
 import scenarios as sc
 from wiretorch_amd import engine, synthetic
+from wiretorch_amd.connectome import Connectome
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -137,7 +139,11 @@ def test_dense_firing_training_step_matches_oracle(max_list):
 
 
 def test_learnt_weights_update_reuses_layout(monkeypatch):
+    """The engine's dense path (rows of learnt weights, compressed once and gathered
+    again while the nonzero pattern holds), taken here by turning off the network's
+    synapse-by-synapse form (``_edge_sides``)."""
     wl = synthetic.config3(B=2, T=60)
+    monkeypatch.setattr(type(wl.model), "_edge_sides", lambda self: [])
     x = torch.from_numpy(wl.x).float()
     target = torch.from_numpy(synthetic.gamma_targets(3, wl.N, 3))
     _training_step(wl, x, target, engine, DEV)
@@ -172,6 +178,41 @@ def test_learnt_weights_update_reuses_layout(monkeypatch):
     assert np.array_equal(s_gpu, s_ref)
 
 
+def test_learnt_weights_by_synapse_follow_the_mask(monkeypatch):
+    """The network's synapse-by-synapse form of learnt recurrent weights (what the HIP
+    engine is given for config 3): one synapse fewer in a mask rebuilds the plan; the
+    training step then gives the dense path's raster, loss and gradients (the same
+    per-synapse gradient kernel: equal to float32 rounding) and the oracle's raster and
+    loss."""
+    wl = synthetic.config3(B=2, T=60)
+    x = torch.from_numpy(wl.x).float()
+    target = torch.from_numpy(synthetic.gamma_targets(3, wl.N, 3))
+    model = wl.model
+    _training_step(wl, x, target, engine, DEV)
+    side = model._edge_sides()
+    assert side, "config 3's recurrent side is not formed synapse by synapse"
+    before = model._edge_connectome(side[0]).n_edges
+    with torch.no_grad():
+        mask = dict(model.named_buffers())["rec_projections.E__E.mask"]
+        flat = mask.view(-1)
+        flat[int(torch.nonzero(flat)[0])] = 0.0
+    s_gpu, l_gpu, g_gpu = _training_step(wl, x, target, engine, DEV)
+    assert model._edge_connectome(side[0]).n_edges == before - 1
+    with monkeypatch.context() as m:
+        m.setattr(type(model), "_edge_sides", lambda self: [])
+        s_dense, l_dense, g_dense = _training_step(wl, x, target, engine, DEV)
+    assert np.array_equal(s_gpu, s_dense)
+    np.testing.assert_allclose(l_gpu, l_dense, rtol=1e-6)
+    assert g_gpu.keys() == g_dense.keys()
+    for key, value in g_dense.items():
+        scale = np.abs(value).max()
+        np.testing.assert_allclose(g_gpu[key], value, rtol=0, atol=1e-6 * scale, err_msg=key)
+    s_ref, l_ref, _ = _training_step(wl, x, target, oracle_engine, "cpu")
+    differs = (s_gpu != s_ref).any(axis=(0, 2))
+    assert not differs.any(), f"rasters differ from step {int(np.argmax(differs))}"
+    np.testing.assert_allclose(l_gpu, l_ref, rtol=1e-5)
+
+
 # ---------------------------------------------------------------------------------
 # The launch geometries the benchmarks run
 # ---------------------------------------------------------------------------------
@@ -189,6 +230,8 @@ def _to(obj, device):
 
     def move(value):
         if torch.is_tensor(value):
+            return value.to(device)
+        if isinstance(value, Connectome):
             return value.to(device)
         if isinstance(value, list):
             return [move(v) for v in value]

@@ -201,6 +201,9 @@ class _Side:
     def abi(self, R: int, range_n: int, stream, weights: torch.Tensor | None = None) -> _lib.Side:
         c = self.conn
         w = c.weights if weights is None else weights
+        if w.device != c.indptr.device or w.dtype != torch.float32 or not w.is_contiguous():
+            raise ValueError(f"connectome weights on {w.device} ({w.dtype}) for a side on "
+                             f"{c.indptr.device}: the kernels take float32 on the side's device")
         return _lib.Side(
             c.indptr.data_ptr(), self.split(R, range_n, stream).data_ptr(),
             c.targets.data_ptr(), w.data_ptr(), self.pathway32.data_ptr(), c.n_sources,
@@ -1039,10 +1042,12 @@ def simulate(
     counter = refractory.to(device=device, dtype=torch.int32).clone(
         memory_format=torch.contiguous_format)
 
-    rec_w = ([drive.sparse_recurrent.weights] if drive.sparse_recurrent is not None
+    # a compressed side's weights are read by the kernels themselves: on the launch device
+    # (a differentiable copy where they were built elsewhere)
+    rec_w = ([drive.sparse_recurrent.weights.to(device)] if drive.sparse_recurrent is not None
              else [W for _, W in drive.recurrent])
-    ff_w = ([drive.sparse_feedforward.weights] if drive.sparse_feedforward is not None
-            else [W for _, W in drive.feedforward])
+    ff_w = ([drive.sparse_feedforward.weights.to(device)]
+            if drive.sparse_feedforward is not None else [W for _, W in drive.feedforward])
     physiology = [getattr(p, name) for name in PHYSIOLOGY]
     grad = torch.is_grad_enabled() and (
         drive.scale.requires_grad or x.requires_grad

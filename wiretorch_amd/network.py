@@ -465,14 +465,90 @@ class ProjectionNetwork(nn.Module):
                 sf[src_ids[src], tgt_ids[tgt]] = projection.kernel_factor()
         return sf
 
+    def _edge_sides(self) -> list[int]:
+        """The sides whose weights the HIP engine takes synapse by synapse: the recurrent
+        side when every one of its pathways is learnt (``weights``) from blocks that form
+        their entries one at a time (``Projection.edge_values``). Those entries are then
+        computed for the synapses only — the blocks' values there, bit for bit — instead
+        of as dense blocks assembled into rows and gathered again; the CPU oracle keeps the
+        dense form (its float32 products are what the recorded fixtures hold)."""
+        if getattr(self._engine, "__name__", "") != "wiretorch_amd.engine":
+            return []
+        out = []
+        for side_no, side in enumerate(self._sides):
+            if not side.recurrent or is_sparse(side):
+                continue
+            pathways = [p for p in self.pathways if p.side == side_no]
+            projections = getattr(self, side.attribute)
+            if (pathways and all(p.mode == "weights" for p in pathways)
+                    and all(p.edge_mask() is not None for p in projections.values())):
+                out.append(side_no)
+        return out
+
+    def _edge_plan(self, side_no: int) -> dict:
+        """The compressed structure of an edge side (``_edge_sides``), cached while its
+        masks and rows are unchanged: CSR by source (``indptr``, ``targets`` ascending),
+        each source's pathway within the side, and per block the row-major positions of
+        its synapses plus the permutation from the blocks' concatenation to CSR order."""
+        side = self._sides[side_no]
+        projections = getattr(self, side.attribute)
+        pathways = [p for p in self.pathways if p.side == side_no]
+        rows = [getattr(self, f"_rows_{p.index}") for p in pathways]
+        key = tuple((t.data_ptr(), t._version) for t in rows) + tuple(
+            (m.data_ptr(), m._version) for m in (q.edge_mask() for q in projections.values()))
+        plans = self.__dict__.setdefault("_edge_plans", {})
+        hit = plans.get(side_no)
+        if hit is not None and hit["key"] == key:
+            return hit
+        N, dev = self.n_neurons, self.device
+        pathway_of = torch.full((N,), -1, dtype=torch.int64, device=dev)
+        srcs, tgts, parts = [], [], []
+        for k, (pw, src_rows) in enumerate(zip(pathways, rows)):
+            pathway_of[src_rows] = k
+            src = next(c["name"] for c in side.cell_params if c["cell_id"] == pw.cell_type)
+            for tgt_id, tgt in self._names.items():
+                if f"{src}__{tgt}" not in projections:
+                    continue
+                block = projections[f"{src}__{tgt}"]
+                cols = (self.cell_type_indices == tgt_id).nonzero(as_tuple=True)[0]
+                if not cols.numel():
+                    continue
+                r, c = (block.edge_mask() != 0).nonzero(as_tuple=True)
+                srcs.append(src_rows[r])
+                tgts.append(cols[c])
+                parts.append((block, r * block.n_target + c))
+        src = torch.cat(srcs) if srcs else torch.zeros(0, dtype=torch.int64, device=dev)
+        tgt = torch.cat(tgts) if tgts else torch.zeros(0, dtype=torch.int64, device=dev)
+        order = torch.argsort(src * N + tgt)
+        indptr = torch.zeros(N + 1, dtype=torch.int64, device=dev)
+        indptr[1:] = torch.cumsum(torch.bincount(src, minlength=N), 0)
+        plan = dict(key=key, indptr=indptr, targets=tgt[order].to(torch.int32).contiguous(),
+                    pathway=pathway_of, parts=parts, order=order, K=len(pathways))
+        plans[side_no] = plan
+        return plan
+
+    def _edge_connectome(self, side_no: int) -> Connectome:
+        """An edge side's connectome with this call's weights (differentiable in the
+        blocks' parameters)."""
+        plan = self._edge_plan(side_no)
+        if plan["parts"]:
+            w = torch.cat([block.edge_values(flat) for block, flat in plan["parts"]])[plan["order"]]
+        else:
+            w = torch.zeros(0, **self._float)
+        return Connectome(self.n_neurons, self.n_neurons, plan["indptr"], plan["targets"], w,
+                          plan["pathway"], plan["K"])
+
     def _drive(self) -> Drive:
         """Per pathway: rows, current weights and kernel scale (``network.py:816-854``)."""
         scaling, assembled = {}, {}
         unit = self._unit_scale.to(self.dt.dtype)
         ones = unit[0] if unit.shape[0] else torch.ones(self.n_neurons, **self._float)
         scales, recurrent, feedforward = [], [], []
-        sparse = {}
+        sparse = {side_no: self._edge_connectome(side_no) for side_no in self._edge_sides()}
         for pathway in self.pathways:
+            if pathway.side in sparse and pathway.mode == "weights":
+                scales.append(ones)
+                continue
             if pathway.mode == "sparse":
                 scales.append(ones)
                 if pathway.side not in sparse:

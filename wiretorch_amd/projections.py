@@ -50,6 +50,16 @@ class Projection(nn.Module):
         """A factor the network applies to the synaptic kernel (None: none)."""
         return None
 
+    def edge_mask(self) -> torch.Tensor | None:
+        """The entries the block can hold (nonzero), if ``edge_values`` forms entries one
+        at a time; None if the block is only formed whole."""
+        return None
+
+    def edge_values(self, flat: torch.Tensor) -> torch.Tensor:
+        """The block's entries at row-major positions ``flat``, formed for those entries
+        only: equal, entry for entry, to ``self()`` there (and differentiable alike)."""
+        raise NotImplementedError
+
 
 class FrozenProjection(Projection):
     """Constant weights (a buffer)."""
@@ -114,6 +124,12 @@ class FullRankProjection(Projection):
     def forward(self) -> torch.Tensor:
         return torch.exp(self.log_weights) * self.mask
 
+    def edge_mask(self) -> torch.Tensor:
+        return self.mask
+
+    def edge_values(self, flat: torch.Tensor) -> torch.Tensor:
+        return torch.exp(self.log_weights.reshape(-1)[flat]) * self.mask.reshape(-1)[flat]
+
 
 class LowRankProjection(Projection):
     """Low-rank log-weights: ``exp(U @ V) * mask``."""
@@ -171,6 +187,12 @@ class SignedProjection(Projection):
 
     def forward(self) -> torch.Tensor:
         return self.weights if self.mask is None else self.weights * self.mask
+
+    def edge_mask(self) -> torch.Tensor | None:
+        return self.mask
+
+    def edge_values(self, flat: torch.Tensor) -> torch.Tensor:
+        return self.weights.reshape(-1)[flat] * self.mask.reshape(-1)[flat]
 
 
 def _members(types: np.ndarray, names: list[str]) -> dict[str, np.ndarray]:
