@@ -655,6 +655,9 @@ class _Plan:
         return _lib.Geometry(groups, R, range_n, -1, self.max_list, self.bound.data_ptr())
 
     def abi_tables(self, scale: torch.Tensor) -> _lib.Tables:
+        if scale.device != self.device or scale.dtype != torch.float32 or not scale.is_contiguous():
+            raise ValueError(f"kernel scales on {scale.device} ({scale.dtype}): the kernels take "
+                             f"float32 on {self.device}")
         t = self.tables
         type_of, range_rows, n_types = self.range_types
         return _lib.Tables(
@@ -1049,15 +1052,16 @@ def simulate(
     ff_w = ([drive.sparse_feedforward.weights.to(device)]
             if drive.sparse_feedforward is not None else [W for _, W in drive.feedforward])
     physiology = [getattr(p, name) for name in PHYSIOLOGY]
+    scale = drive.scale.to(device)  # the kernels read it: on the launch device
     grad = torch.is_grad_enabled() and (
-        drive.scale.requires_grad or x.requires_grad
+        scale.requires_grad or x.requires_grad
         or any(W.requires_grad for W in rec_w + ff_w)
         or any(t.requires_grad for t in physiology)
     )  # fmt: skip
     L.recurrent_gradients = bool(drive.recurrent_gradients and L.K_rec and L.rec.n_src)
     if grad:
         spikes, prob, v, g_state, counter = _Run.apply(
-            L, len(rec_w), drive.scale, x, v, g_state, counter, *rec_w, *ff_w, *physiology
+            L, len(rec_w), scale, x, v, g_state, counter, *rec_w, *ff_w, *physiology
         )
         tracked = None
         if track:  # the buffers live on the autograd context; rebuild from the last run
@@ -1069,7 +1073,7 @@ def simulate(
         with torch.no_grad():
             rw, fw = _sparse_weights(L, rec_w + ff_w, len(rec_w))
             _launch(L, x.detach().float().contiguous(),
-                    drive.scale.detach().float().contiguous(), v, g_state, counter, spikes,
+                    scale.detach().float().contiguous(), v, g_state, counter, spikes,
                     prob, None, tracked, rw, fw)
     return Run(
         output=spikes,
