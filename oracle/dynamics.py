@@ -8,8 +8,9 @@ bit for bit (same torch CPU kernels, same association order):
 * ``jumps`` — ``conductance/dynamics.py:95-100``;
 * ``spike`` — ``conductance/dynamics.py:103-107``;
 * ``mg_block`` — ``conductance/dynamics.py:110-113``;
-* ``membrane`` — ``conductance/dynamics.py:116-143`` (the Mg block, no adaptation);
-* ``simulate`` — ``conductance/dynamics.py:146-237`` (no gating, no adaptation);
+* ``membrane`` — ``conductance/dynamics.py:116-143`` (the Mg block and the adaptation
+  conductance);
+* ``simulate`` — ``conductance/dynamics.py:146-237`` (adaptation; no gating);
 * ``refractory_mask`` / ``held_at_reset`` / ``count_down`` —
   ``network_simulators/network.py:294-318``;
 * ``recurrent_activations`` — ``network_simulators/network.py:260-271``;
@@ -93,8 +94,9 @@ def mg_block(v, mg_c, mg_a):
     return torch.sigmoid(mg_a * v[:, :, None] - torch.log(mg_c))
 
 
-def membrane(v, s, g, p):
-    """Currents and the voltage after the exponential-Euler step, reset where ``s``."""
+def membrane(v, s, g, p, g_a=None):
+    """Currents and the voltage after the exponential-Euler step, reset where ``s``;
+    ``g_a`` ``(B, N)`` the adaptation conductance (by ``E_adapt``), if any."""
     g_total = torch.minimum(g.sum(dim=2).clamp(min=0.0), p.g_clip)
     if getattr(p, "mg_c", None) is not None:  # the block scales each type's conductance
         g_total = g_total * mg_block(v, p.mg_c, p.mg_a)
@@ -104,6 +106,9 @@ def membrane(v, s, g, p):
     I_leak = g_L * (v - p.E_L)
     G = g_total.sum(dim=2)
     J = I.sum(dim=2) + I_leak
+    if g_a is not None:
+        G = G + g_a
+        J = J + g_a * (v - p.E_adapt)
     x = p.dt * rate + p.dt * G / p.C_m
     step = -torch.expm1(-x) / (g_L + G)
     s = s.detach()
@@ -196,8 +201,8 @@ def simulate(
     """Simulate ``x.shape[1]`` steps from ``(v, g)``; returns a ``Run``."""
     from wiretorch_amd.network import Run
 
-    if gating is not None or adaptation is not None or p.adapt is not None:
-        raise NotImplementedError("gating and adaptation are not restated")
+    if gating is not None:
+        raise NotImplementedError("presynaptic gating is not restated")
     A_ff = feedforward_activations(drive, x)
     kernels = jumps(drive, p.jump)
     keep = (
@@ -205,7 +210,10 @@ def simulate(
         if track_batch_idx is None
         else slice(track_batch_idx, track_batch_idx + 1)
     )
-    spikes, probs, tracked = [], [], {"v": [], "I": [], "g": []}
+    spikes, probs, tracked = [], [], {"v": [], "I": [], "g": [], "a": []}
+    g_a = adaptation if getattr(p, "adapt", None) is not None else None
+    if g_a is None and getattr(p, "adapt", None) is not None:
+        g_a = torch.zeros_like(v)
     if refractory is None:
         refractory = torch.zeros(v.shape, dtype=torch.int32, device=v.device)
     for t in range(x.shape[1]):
@@ -214,8 +222,10 @@ def simulate(
         if probabilities:
             prob = torch.sigmoid(p.surr_scale * (v - p.theta))
             probs.append(prob if held is None else prob * (1 - held))
-        v_next, I, I_leak = membrane(v, held_at_reset(s, held), g, p)
+        v_next, I, I_leak = membrane(v, held_at_reset(s, held), g, p, g_a)
         refractory = count_down(s, refractory, p.n_ref)
+        if g_a is not None:  # the neuron's own spike raises it (no gradient, as reset)
+            g_a = g_a * p.adapt_decay + p.adapt * s.detach()
         s_rec = s if drive.recurrent_gradients else s.detach()
         activations = recurrent_activations(drive, s_rec)
         activations += list(A_ff[:, :, t])
@@ -233,6 +243,8 @@ def simulate(
             tracked["v"].append(v[keep].detach())
             tracked["I"].append(torch.cat([I, I_leak[..., None]], dim=-1)[keep].detach())
             tracked["g"].append(g[keep].detach())
+            if g_a is not None:
+                tracked["a"].append(g_a[keep].detach())
     return Run(
         output=torch.stack(spikes, dim=1),
         v=v,
@@ -240,4 +252,5 @@ def simulate(
         probabilities=torch.stack(probs, dim=1) if probabilities else None,
         tracked={k: stack_steps(val) for k, val in tracked.items() if val} if track else None,
         refractory=refractory,
+        adaptation=g_a,
     )

@@ -75,6 +75,15 @@ def mg_block(synapses, mg):
     return [{**s, "mg": mg} if s["name"] == "NMDA" else s for s in synapses]
 
 
+def adapting(cells, adapt, tau_adapt=200.0):
+    """``cells`` whose excitatory type adapts by ``adapt`` per spike (unchanged for None;
+    reference ``tests/networks.py:145-155``)."""
+    if adapt is None:
+        return cells
+    return [{**c, "adapt": adapt, "tau_adapt": tau_adapt} if c["name"] == "excitatory" else c
+            for c in cells]
+
+
 def combined_physiology():
     cells = [dict(c) for c in MITRAL_CELLS]
     cells += [{**c, "cell_id": c["cell_id"] + 1} for c in CELLS]
@@ -163,10 +172,10 @@ def _input_rng(seed, input_seed):
 
 def recurrent(batch_size, seed, scaling_factors=False, n=N, n_ff=N_FF, n_steps=200,
               input_seed=0, learn=None, learnt_weights=False, tau_ref=None,
-              recurrent_gradients=False, dt=DT, surrgrad_scale=5.0, mg=None):
+              recurrent_gradients=False, dt=DT, surrgrad_scale=5.0, mg=None, adapt=None):
     """``ConductanceLIFNetwork``: frozen weights, perturbed scaling factors, or learnt
-    recurrent weights; ``mg`` mM of Mg block on the NMDA types (reference
-    ``tests/networks.py:276-355``)."""
+    recurrent weights; ``mg`` mM of Mg block on the NMDA types, ``adapt`` the excitatory
+    cells' adaptation (reference ``tests/networks.py:276-355``)."""
     rng, types, w_rec, w_ff = _structure(seed, n, n_ff)
     ff_types = np.zeros(n_ff, dtype=np.int64)
     rec_blocks = per_type_blocks(w_rec, types, types, REC_NAMES, REC_NAMES)
@@ -182,7 +191,7 @@ def recurrent(batch_size, seed, scaling_factors=False, n=N, n_ff=N_FF, n_steps=2
     model = ConductanceLIFNetwork(
         dt=dt, rec_projections=rec, ff_projections=ff,
         cell_type_indices=types, cell_type_indices_FF=ff_types,
-        cell_params=with_refractory(CELLS, tau_ref), cell_params_FF=MITRAL_CELLS,
+        cell_params=adapting(with_refractory(CELLS, tau_ref), adapt), cell_params_FF=MITRAL_CELLS,
         synapse_params=mg_block(SYNAPSES, mg), synapse_params_FF=mg_block(MITRAL_SYNAPSES, mg),
         surrgrad_scale=surrgrad_scale, batch_size=batch_size, learn=learn,
         recurrent_gradients=recurrent_gradients,
@@ -198,7 +207,8 @@ def recurrent(batch_size, seed, scaling_factors=False, n=N, n_ff=N_FF, n_steps=2
 
 
 def feedforward(batch_size, seed, learnt_weights=False, probabilities=False, n=N,
-                n_ff=N_FF, n_steps=200, input_seed=0, learn=None, tau_ref=None, mg=None):
+                n_ff=N_FF, n_steps=200, input_seed=0, learn=None, tau_ref=None, mg=None,
+                adapt=None):
     """``FeedforwardConductanceLIFNetwork`` on external inputs and a recurrent network's
     neurons; ``mg`` as for ``recurrent`` (reference ``tests/networks.py:358-429``)."""
     rng, types, w_rec, w_ff = _structure(seed, n, n_ff)
@@ -226,7 +236,7 @@ def feedforward(batch_size, seed, learnt_weights=False, probabilities=False, n=N
             projections[(src, tgt)] = ScalingFactorProjection(block)
     model = FeedforwardConductanceLIFNetwork(
         dt=DT, projections=projections, cell_type_indices=types,
-        cell_type_indices_FF=row_types, cell_params=with_refractory(CELLS, tau_ref),
+        cell_type_indices_FF=row_types, cell_params=adapting(with_refractory(CELLS, tau_ref), adapt),
         cell_params_FF=cells, synapse_params_FF=synapses, surrgrad_scale=5.0,
         batch_size=batch_size, return_probabilities=probabilities, learn=learn,
     )  # fmt: skip

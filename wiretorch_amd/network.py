@@ -24,10 +24,10 @@ bit-identical inputs:
 * state at rest (``v = U_reset``, ``g = 0`` laid out ``(B, 2, S, N)``):
   ``conductance/network.py:248-255``.
 
-The NMDA Mg block is built (``synapses.mg_block_tables``; ``conductance/network.py:
-138-141``). Presynaptic dynamics (short-term plasticity, receptor saturation) and
-spike-frequency adaptation are not part of this build: a network configured with any of
-them raises ``NotImplementedError``.
+The NMDA Mg block (``synapses.mg_block_tables``; ``conductance/network.py:138-141``) and
+spike-frequency adaptation (``network.py:530-551``) are built. Presynaptic dynamics
+(short-term plasticity, receptor saturation) are not part of this build: a network
+configured with them raises ``NotImplementedError``.
 
 ``Drive`` also accepts a sparse form (``connectome.Connectome``) for connectomes too
 large for the reference's dense per-pathway rows (fly scale).
@@ -54,9 +54,12 @@ NEURON_PARAMETERS = ("tau_mem", "theta", "U_reset", "E_L", "g_L")
 SYNAPSE_PARAMETERS = ("tau_rise", "tau_decay", "E_syn", "g_bar")
 #: Learnable physiology: cell parameters (default value, None if required) and
 #: synapse parameters; positive ones are learnt as logarithms.
-LEARNABLE = {"tau_mem": None, "theta": None, "U_reset": None, "E_L": None, "g_L": None}
+#: Cell parameters ``learn`` can train, with their defaults (None: required); the
+#: adaptation's have defaults (``conductance/network.py:35-41``).
+LEARNABLE = {"tau_mem": None, "theta": None, "U_reset": None, "E_L": None, "g_L": None,
+             "adapt": 0.0, "tau_adapt": 100.0, "E_adapt": -90.0}
 LEARNABLE_SYNAPSE = SYNAPSE_PARAMETERS
-POSITIVE = {"tau_mem", "g_L", "tau_rise", "tau_decay", "g_bar"}
+POSITIVE = {"tau_mem", "g_L", "tau_rise", "tau_decay", "g_bar", "adapt", "tau_adapt"}
 STORAGE_DTYPES = (torch.float32, torch.float16)
 
 
@@ -238,9 +241,6 @@ def is_sparse(side: InputSide) -> bool:
 
 
 def _unsupported(cell_params, synapse_lists, stp) -> None:
-    for cell in cell_params:
-        if cell.get("adapt", 0.0):
-            raise NotImplementedError("spike-frequency adaptation is not supported")
     for synapses in synapse_lists:
         for syn in synapses:
             if syn.get("saturation", 0.0):
@@ -717,6 +717,18 @@ class ConductanceNetwork(ProjectionNetwork):
         tau_ref = self._per_neuron("tau_ref", 0.0)
         assert bool((tau_ref >= 0).all()), "cell_params: tau_ref must be >= 0"
         self.register_buffer("tau_ref", tau_ref, persistent=False)
+        # Spike-frequency adaptation (network.py:530-551): per cell type, its rise at each
+        # of the neuron's spikes (adapt, 0: none), its time constant (tau_adapt, ms) and
+        # reversal potential (E_adapt, mV); from the cell parameters, not saved.
+        adapt = self._per_neuron("adapt", LEARNABLE["adapt"])
+        tau_adapt = self._per_neuron("tau_adapt", LEARNABLE["tau_adapt"])
+        assert bool((adapt >= 0).all()), "cell_params: a negative adaptation rise (adapt)"
+        assert bool((tau_adapt[adapt > 0] > 0).all()), "cell_params: tau_adapt not positive"
+        self.register_buffer("adapt", adapt, persistent=False)
+        self.register_buffer("tau_adapt", tau_adapt, persistent=False)
+        self.register_buffer("E_adapt", self._per_neuron("E_adapt", LEARNABLE["E_adapt"]),
+                             persistent=False)
+        self._adapting = bool(adapt.any())
         self.register_buffer(
             "surrgrad_scale", torch.tensor(self._surrgrad_scale, dtype=torch.float32)
         )
@@ -734,7 +746,8 @@ class ConductanceNetwork(ProjectionNetwork):
             if learn.get(name)
         }
         if learnt:
-            values = {name: [c[name] for c in cells] for name in learnt}
+            values = {name: [c[name] if LEARNABLE[name] is None else c.get(name, LEARNABLE[name])
+                             for c in cells] for name in learnt}
             self.cell_parameters = TypeParameters(
                 values, learnt=learnt, positive=POSITIVE & set(learnt)
             )
@@ -784,6 +797,8 @@ class ConductanceNetwork(ProjectionNetwork):
         n_ref = torch.round(self.tau_ref / self.dt).to(torch.int32)
         self.register_buffer("n_ref", n_ref, persistent=False)
         self._refractory = bool(n_ref.any())
+        self.register_buffer("adapt_decay", torch.exp(-self.dt / self.tau_adapt),
+                             persistent=False)
 
     def _physiology(self) -> Physiology:
         """The engine's parameters for one call (``conductance/network.py:210-246``)."""
@@ -813,6 +828,9 @@ class ConductanceNetwork(ProjectionNetwork):
             n_ref=self.n_ref if self._refractory else None,
             mg_c=self.mg_c if self._mg_block else None,
             mg_a=self.mg_a if self._mg_block else None,
+            **(dict(adapt=learnt("adapt", self.adapt),
+                    adapt_decay=learnt("tau_adapt", self.adapt_decay, decay=True),
+                    E_adapt=learnt("E_adapt", self.E_adapt)) if self._adapting else {}),
         )
 
     def _initial_state(self):
@@ -823,21 +841,28 @@ class ConductanceNetwork(ProjectionNetwork):
         return v, g
 
     def _engine_kwargs(self) -> dict:
-        return {"refractory": self.refractory}
+        return {"refractory": self.refractory,
+                **({"adaptation": self.adaptation} if self._adapting else {})}
 
     def _after_run(self, run: Run) -> None:
         if run.refractory is not None:
             self.refractory = run.refractory
+        if run.adaptation is not None:  # the next chunk starts from it, without its graph
+            self.adaptation = run.adaptation.detach()
 
     def _reset_extra(self) -> None:
         counter = torch.zeros((self.batch_size, self.n_neurons), dtype=torch.int32,
                               device=self.device)
         self.register_buffer("refractory", counter, persistent=False)
+        self.register_buffer("adaptation", torch.zeros((self.batch_size, self.n_neurons),
+                                                       device=self.device), persistent=False)
 
     def get_checkpoint_state(self) -> dict[str, np.ndarray]:
         state = super().get_checkpoint_state()
         if self._refractory:
             state["refractory"] = self.refractory.cpu().numpy()
+        if self._adapting:
+            state["adaptation"] = self.adaptation.cpu().numpy()
         return state
 
     def load_checkpoint_state(self, state: dict[str, np.ndarray]) -> None:
@@ -847,6 +872,8 @@ class ConductanceNetwork(ProjectionNetwork):
             if "refractory" in state
             else torch.zeros_like(self.v, dtype=torch.int32)
         )
+        self.adaptation = (torch.from_numpy(state["adaptation"]).to(self.device)
+                           if "adaptation" in state else torch.zeros_like(self.v))
 
 
 def _engine_module():
@@ -936,6 +963,7 @@ class ConductanceLIFNetwork(ConductanceNetwork):
             "currents": run.tracked["I"][..., :S],
             "currents_leak": run.tracked["I"][..., S],
             "conductances": run.tracked["g"],
+            **({"adaptation": run.tracked["a"]} if "a" in run.tracked else {}),
         }
 
     @property
@@ -1015,6 +1043,7 @@ class FeedforwardConductanceLIFNetwork(ConductanceNetwork):
                 "currents_feedforward": run.tracked["I"][..., :S],
                 "currents_leak": run.tracked["I"][..., S],
                 "conductances_feedforward": run.tracked["g"],
+                **({"adaptation": run.tracked["a"]} if "a" in run.tracked else {}),
             }
             if self.return_probabilities:
                 out["probabilities"] = run.probabilities
