@@ -65,6 +65,13 @@ typedef struct {
    * without one; both (S,), or NULL when no type has a block. */
   const float* mg_a;
   const float* mg_lc;
+  /* Spike-frequency adaptation (conductance/kernels.py:163-281, dynamics.py:116-143): a
+   * neuron's adaptation conductance g_a (by E_adapt) adds g_a to the step's total
+   * conductance and g_a (v - E_adapt) to its current, and after the step becomes g_a
+   * adapt_decay + adapt s. All three (N,), or NULL when no neuron adapts. */
+  const float* adapt;
+  const float* adapt_decay;
+  const float* E_adapt;
   int64_t N, S, K, K_rec;
 } wt_tables;
 
@@ -138,6 +145,12 @@ typedef struct {
   const float* in_prob;
   uint64_t in_seed;
   int64_t in_t0;
+  /* With adaptation (tab.adapt): the adaptation conductances (B,N), updated in place;
+   * a_saved (B,T,N) each step's g_a entering it, and track_a (Bt,T,N) g_a after it, may
+   * be NULL. Without, all three are ignored. */
+  float* adaptation;
+  float* a_saved;
+  float* track_a;
 } wt_run_io;
 
 /* wt_poisson_fill — materialise on-device Poisson input: x[b, t, j] = 1 if channel j of
@@ -216,6 +229,12 @@ typedef struct {
   float* grad_E_syn;
   float* grad_decay;
   float* grad_jump;
+  /* With adaptation (tab.adapt): a_saved (B,T,N) from the forward, and the per-(trial,
+   * neuron) partials (B,N) of adapt, adapt_decay and E_adapt (each may be NULL). */
+  const float* a_saved;
+  float* grad_adapt;
+  float* grad_adapt_decay;
+  float* grad_E_adapt;
 } wt_backward_io;
 
 int wt_cond_scan_backward(const wt_tables* tab, const wt_backward_io* io,

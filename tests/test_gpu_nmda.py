@@ -73,6 +73,7 @@ def _engine_vs_oracle(builder):
         err_k = (g_k[key] - g_64[key]).abs().max().item()
         err_r = (g_r[key] - g_64[key]).abs().max().item()
         assert err_k <= 2 * err_r + 1e-4 * scale, (key, err_k, err_r, scale)
+    return g_k
 
 
 def _with_flag(builder, recurrent_gradients):

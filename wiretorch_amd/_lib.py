@@ -22,7 +22,8 @@ class Tables(ctypes.Structure):
         ("theta", P), ("U_reset", P), ("E_L", P), ("C_m", P), ("beta", P), ("n_ref", P),
         ("E_syn", P), ("g_clip", P), ("decay", P), ("jump", P), ("made", P), ("scale", P),
         ("dt", P), ("surr", P), ("types", P), ("type_of", P), ("n_types", I64),
-        ("range_rows", P), ("mg_a", P), ("mg_lc", P), ("N", I64), ("S", I64), ("K", I64),
+        ("range_rows", P), ("mg_a", P), ("mg_lc", P), ("adapt", P), ("adapt_decay", P),
+        ("E_adapt", P), ("N", I64), ("S", I64), ("K", I64),
         ("K_rec", I64),
     ]  # fmt: skip
 
@@ -44,7 +45,8 @@ class RunIO(ctypes.Structure):
         ("x", P), ("B", I64), ("T", I64), ("n_in", I64), ("v", P), ("g", P), ("counter", P),
         ("spikes", P), ("prob", P), ("v_saved", P), ("G_saved", P), ("held", P),
         ("A_saved", P), ("track_v", P), ("track_I", P), ("track_g", P), ("track_b", I64),
-        ("in_prob", P), ("in_seed", ctypes.c_uint64), ("in_t0", I64),
+        ("in_prob", P), ("in_seed", ctypes.c_uint64), ("in_t0", I64), ("adaptation", P),
+        ("a_saved", P), ("track_a", P),
     ]  # fmt: skip
 
 
@@ -54,7 +56,8 @@ class BackwardIO(ctypes.Structure):
         ("G_saved", P), ("held", P), ("A", P), ("g_init", P), ("B", I64), ("T", I64),
         ("grad_A", P), ("grad_scale", P), ("grad_theta", P), ("grad_reset", P),
         ("grad_E_L", P), ("grad_C_m", P), ("grad_beta", P), ("grad_E_syn", P),
-        ("grad_decay", P), ("grad_jump", P),
+        ("grad_decay", P), ("grad_jump", P), ("a_saved", P), ("grad_adapt", P),
+        ("grad_adapt_decay", P), ("grad_E_adapt", P),
     ]  # fmt: skip
 
 

@@ -38,14 +38,17 @@ struct BackState {
   float accE[S], accDr[S], accDd[S], accJr[S], accJd[S];
   float acc_scale[WT_MAX_K];
   float acc_theta, acc_reset, acc_EL, acc_Cm, acc_beta;
+  float la;                          // dL/dg_a (adaptation) entering the step after
+  float acc_adapt, acc_adecay, acc_Ea;
 };
 template <int S>
-constexpr int back_fields() { return 1 + 9 * S + WT_MAX_K + 5; }
+constexpr int back_fields() { return 1 + 9 * S + WT_MAX_K + 5 + 4; }
 
 // Global layout of the recurrent path's state: field f of item idx at f * BN + idx. A
 // field that feeds no wanted gradient is neither read (it reads as zero) nor written:
-// the decay recursions and partials only with grad_decay, and so on.
-template <int S>
+// the decay recursions and partials only with grad_decay, and so on; the adaptation's
+// only with AD (the network adapts).
+template <int S, bool AD>
 __device__ inline void state_io(BackState<S>& st, float* base, int64_t BN, int64_t idx,
                                 bool store, const wt_backward_io& io, int64_t K) {
   float* p = base + idx;
@@ -71,6 +74,11 @@ __device__ inline void state_io(BackState<S>& st, float* base, int64_t BN, int64
   y(io.grad_theta != nullptr, st.acc_theta); y(io.grad_reset != nullptr, st.acc_reset);
   y(io.grad_E_L != nullptr, st.acc_EL); y(io.grad_C_m != nullptr, st.acc_Cm);
   y(io.grad_beta != nullptr, st.acc_beta);
+  // the adaptation's adjoint feeds only the gradients of its rise and decay
+  y(AD && (io.grad_adapt != nullptr || io.grad_adapt_decay != nullptr), st.la);
+  y(AD && io.grad_adapt != nullptr, st.acc_adapt);
+  y(AD && io.grad_adapt_decay != nullptr, st.acc_adecay);
+  y(AD && io.grad_E_adapt != nullptr, st.acc_Ea);
 }
 
 template <int S>
@@ -83,14 +91,19 @@ __device__ inline void state_zero(BackState<S>& st) {
 #pragma unroll
   for (int k = 0; k < WT_MAX_K; ++k) st.acc_scale[k] = 0.0f;
   st.acc_theta = st.acc_reset = st.acc_EL = st.acc_Cm = st.acc_beta = 0.0f;
+  st.la = st.acc_adapt = st.acc_adecay = st.acc_Ea = 0.0f;
 }
 
 // One neuron's constants of the backward.
 struct BackNeuron {
   float theta, E_L, C_m, beta, dt, k_surr;
   Leak lk;
+  float a_decay, E_a;  // adaptation (0 without)
 };
 
+// AD: the network adapts (tab.adapt set). The backward kernels are compiled with and
+// without it, so that a network without adaptation carries none of its registers.
+template <bool AD>
 __device__ inline BackNeuron back_neuron(const wt_tables& tab, int64_t n) {
   BackNeuron c;
   c.theta = tab.theta[n];
@@ -100,6 +113,8 @@ __device__ inline BackNeuron back_neuron(const wt_tables& tab, int64_t n) {
   c.dt = *tab.dt;
   c.k_surr = *tab.surr;
   c.lk = leak(c.C_m, c.beta, c.dt);
+  c.a_decay = AD ? tab.adapt_decay[n] : 0.0f;
+  c.E_a = AD ? tab.E_adapt[n] : 0.0f;
   return c;
 }
 
@@ -111,11 +126,12 @@ constexpr int kPreK = 4;  // pathways whose activations are loaded ahead (the re
 template <int S>
 struct StepIn {
   float v, spike, held, grad_spike, grad_prob;
+  float ga;  // the adaptation conductance entering the step (0 without)
   float G[S];
   float A[kPreK];  // the injected activations (when their partials are wanted)
 };
 
-template <int S>
+template <int S, bool AD>
 __device__ inline void load_step(StepIn<S>& in, const BackArgs& P, int64_t b, int64_t n,
                                  int64_t t) {
   const wt_tables& tab = P.tab;
@@ -127,6 +143,7 @@ __device__ inline void load_step(StepIn<S>& in, const BackArgs& P, int64_t b, in
   in.held = io.held ? (float)io.held[out] : 0.0f;
   in.grad_spike = io.grad_spikes[out];
   in.grad_prob = io.grad_prob ? io.grad_prob[out] : 0.0f;
+  in.ga = AD ? io.a_saved[out] : 0.0f;
 #pragma unroll
   for (int s = 0; s < S; ++s) in.G[s] = io.G_saved[out * S + s];
   const bool want_A = io.grad_decay || io.grad_jump || io.grad_scale;
@@ -147,7 +164,7 @@ __device__ inline float step_A(const StepIn<S>& in, const BackArgs& P, int k, in
 // jump and decay partials), the membrane update, and the conductances decaying into
 // step t+1. Leaves st.dv = dL/dv_t without the spike's term. When ga_rec is given,
 // dL/da_k of the recurrent pathways (k < K_rec) is also left there.
-template <int S>
+template <int S, bool AD>
 __device__ inline void back_membrane_step(BackState<S>& st, const BackArgs& P,
                                           const Synapses<S>& syn, const BackNeuron& c,
                                           int64_t b, int64_t n, int64_t t,
@@ -207,11 +224,22 @@ __device__ inline void back_membrane_step(BackState<S>& st, const BackArgs& P,
     if (ga_rec && k < tab.K_rec) ga_rec[k] = ga;
     if (want_scale) st.acc_scale[k] += qk * step_A<S>(in, P, k, b, n, t);
   }
+  // The adaptation after step t, g_a(t) adapt_decay + adapt s_t: st.la is its adjoint
+  // (conductance/kernels.py:498-504).
+  constexpr bool adapting = AD;
+  if (adapting) {
+    if (io.grad_adapt) st.acc_adapt += st.la * s_sp;
+    if (io.grad_adapt_decay) st.acc_adecay += st.la * in.ga;
+  }
   // Membrane.
   const float gx = st.dv * (1.0f - r);
   float dG[S], Gc[S];
-  const MembraneAdjoint m =
-      membrane_adjoint<S>(gx, v, G, syn, c.E_L, c.C_m, c.lk, c.dt, dG, Gc);
+  const MembraneAdjoint m = membrane_adjoint<S>(gx, v, G, syn, c.E_L, c.C_m, c.lk, c.dt, dG,
+                                                Gc, adapting, in.ga, c.E_a);
+  if (adapting) {
+    if (io.grad_E_adapt) st.acc_Ea += gx * m.phi * in.ga;
+    st.la = st.la * c.a_decay + m.d_ga;
+  }
   st.acc_reset += st.dv * r;
   st.acc_EL += gx * m.phi * c.lk.g_L;
   if (io.grad_C_m || io.grad_beta) {
@@ -277,6 +305,9 @@ __device__ inline void back_finish(const BackState<S>& st, const BackArgs& P, in
   if (io.grad_E_L) io.grad_E_L[idx] = st.acc_EL;
   if (io.grad_C_m) io.grad_C_m[idx] = st.acc_Cm;
   if (io.grad_beta) io.grad_beta[idx] = st.acc_beta;
+  if (io.grad_adapt) io.grad_adapt[idx] = st.acc_adapt;
+  if (io.grad_adapt_decay) io.grad_adapt_decay[idx] = st.acc_adecay;
+  if (io.grad_E_adapt) io.grad_E_adapt[idx] = st.acc_Ea;
 #pragma unroll
   for (int s = 0; s < S; ++s) {
     if (io.grad_E_syn) io.grad_E_syn[(b * S + s) * N + n] = st.accE[s];
@@ -294,7 +325,7 @@ __device__ inline void back_finish(const BackState<S>& st, const BackArgs& P, in
 }
 
 // Recurrent activations as inputs: one thread per (trial, neuron), all steps.
-template <int S>
+template <int S, bool AD>
 __global__ __launch_bounds__(256) void cond_backward_kernel(BackArgs P) {
   const int64_t N = P.tab.N, B = P.io.B, T = P.io.T;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -302,17 +333,17 @@ __global__ __launch_bounds__(256) void cond_backward_kernel(BackArgs P) {
   const int64_t b = idx / N, n = idx - b * N;
   Synapses<S> syn;
   load_synapses<S>(P.tab, syn);
-  const BackNeuron c = back_neuron(P.tab, n);
+  const BackNeuron c = back_neuron<AD>(P.tab, n);
   float scale[WT_MAX_K];
 #pragma unroll
   for (int k = 0; k < WT_MAX_K; ++k) scale[k] = k < P.tab.K ? P.tab.scale[k * N + n] : 0.0f;
   BackState<S> st;
   state_zero(st);
   StepIn<S> cur, next;
-  if (T > 0) load_step<S>(cur, P, b, n, T - 1);
+  if (T > 0) load_step<S, AD>(cur, P, b, n, T - 1);
   for (int64_t t = T - 1; t >= 0; --t) {
-    if (t > 0) load_step<S>(next, P, b, n, t - 1);  // a step ahead
-    back_membrane_step<S>(st, P, syn, c, b, n, t, cur, scale);
+    if (t > 0) load_step<S, AD>(next, P, b, n, t - 1);  // a step ahead
+    back_membrane_step<S, AD>(st, P, syn, c, b, n, t, cur, scale);
     back_spike_step<S>(st, P, c, 0.0f, cur);
     cur = next;
   }
@@ -353,7 +384,7 @@ __device__ inline unsigned xcd_contiguous(unsigned i, unsigned n) {
 // dL/da is completed in one L2.
 constexpr int kRgTileN = 32, kRgTileB = 8;
 
-template <int S>
+template <int S, bool AD>
 __global__ __launch_bounds__(256) void rg_membrane_kernel(BackArgs P, int64_t t) {
   __shared__ float ga_tile[WT_MAX_K][kRgTileN][kRgTileB + 1];
   __shared__ float r_tile[kRgTileN][kRgTileB + 1];
@@ -379,7 +410,7 @@ __global__ __launch_bounds__(256) void rg_membrane_kernel(BackArgs P, int64_t t)
     const int64_t idx = b * N + n;
     Synapses<S> syn;
     load_synapses<S>(P.tab, syn);
-    const BackNeuron c = back_neuron(P.tab, n);
+    const BackNeuron c = back_neuron<AD>(P.tab, n);
     float scale[WT_MAX_K];
 #pragma unroll
     for (int k = 0; k < WT_MAX_K; ++k) scale[k] = k < P.tab.K ? P.tab.scale[k * N + n] : 0.0f;
@@ -387,13 +418,13 @@ __global__ __launch_bounds__(256) void rg_membrane_kernel(BackArgs P, int64_t t)
     if (!carry) {
       state_zero(st);
     } else {
-      state_io<S>(st, P.state, B * N, idx, false, P.io, P.tab.K);
+      state_io<S, AD>(st, P.state, B * N, idx, false, P.io, P.tab.K);
       rg_spike_at<S>(st, P, c, b, n, t + 1, r_tile[nn][bb]);
     }
     StepIn<S> in;
-    load_step<S>(in, P, b, n, t);
-    back_membrane_step<S>(st, P, syn, c, b, n, t, in, scale, ga);
-    state_io<S>(st, P.state, B * N, idx, true, P.io, P.tab.K);
+    load_step<S, AD>(in, P, b, n, t);
+    back_membrane_step<S, AD>(st, P, syn, c, b, n, t, in, scale, ga);
+    state_io<S, AD>(st, P.state, B * N, idx, true, P.io, P.tab.K);
   }
 #pragma unroll
   for (int k = 0; k < WT_MAX_K; ++k)
@@ -532,7 +563,7 @@ __global__ __launch_bounds__(256) void rg_finish_kernel(BackArgs P) {
   if (idx >= B * N) return;
   const int64_t b = idx / N, n = idx - b * N;
   BackState<S> st;
-  state_io<S>(st, P.state, B * N, idx, false, P.io, P.tab.K);
+  state_io<S, true>(st, P.state, B * N, idx, false, P.io, P.tab.K);  // (null grads: no read)
   BackNeuron c;
   c.theta = P.tab.theta[n];
   c.k_surr = *P.tab.surr;
@@ -550,8 +581,11 @@ template <int S>
 hipError_t BackLaunch<S>::run(BackArgs& a, hipStream_t stream) {
   const int64_t total = a.io.B * a.tab.N;
   const int block = 256;
-  hipLaunchKernelGGL(cond_backward_kernel<S>, dim3((unsigned)((total + block - 1) / block)),
-                     dim3(block), 0, stream, a);
+  const dim3 grid((unsigned)((total + block - 1) / block));
+  if (a.tab.adapt)
+    hipLaunchKernelGGL((cond_backward_kernel<S, true>), grid, dim3(block), 0, stream, a);
+  else
+    hipLaunchKernelGGL((cond_backward_kernel<S, false>), grid, dim3(block), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -566,7 +600,10 @@ hipError_t BackLaunch<S>::recurrent(BackArgs& a, hipStream_t stream) {
   const bool by_wave = B % 64 == 0 && N * B * 4 < INT32_MAX;
   const dim3 wave_grid((unsigned)((total / 64 + 3) / 4));
   for (int64_t t = a.io.T - 1; t >= 0; --t) {
-    hipLaunchKernelGGL(rg_membrane_kernel<S>, tiles, dim3(block), 0, stream, a, t);
+    if (a.tab.adapt)
+      hipLaunchKernelGGL((rg_membrane_kernel<S, true>), tiles, dim3(block), 0, stream, a, t);
+    else
+      hipLaunchKernelGGL((rg_membrane_kernel<S, false>), tiles, dim3(block), 0, stream, a, t);
     if (by_wave)
       hipLaunchKernelGGL(rg_gather_wave_kernel<S>, wave_grid, dim3(block), 0, stream, a);
     else

@@ -415,6 +415,8 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
   if (!tab || !rec || !ff || !geo || !io || !scratch || !io->spikes || !io->v || !io->g)
     return hipErrorInvalidValue;
   if (tab->n_ref && !io->counter) return hipErrorInvalidValue;
+  if (tab->adapt && (!tab->adapt_decay || !tab->E_adapt || !io->adaptation))
+    return hipErrorInvalidValue;
   if (tab->S < 1 || tab->S > WT_MAX_S || tab->K < 0 || tab->K > WT_MAX_K || tab->K_rec > tab->K)
     return hipErrorInvalidValue;
   if (geo->groups < 1 || geo->groups > kMaxGroups || geo->R < 1 || geo->R > 256 ||
@@ -474,8 +476,10 @@ static int run_impl(const wt_tables* tab, const wt_side* rec, const wt_side* ff,
   const int64_t per_thread = (tpg * geo->range_n + kRunBlock - 1) / kRunBlock;
   // the kMaxList-entry list where the accumulator leaves room for it (and the workgroup
   // has at most kBigMaxi items per thread); else kRunBlock entries
-  int32_t cap = kRunBlock;  // (a timed launch keeps it: its kernels have this list only)
-  if (!timing && per_thread <= kBigMaxi && (geo->max_list == 0 || geo->max_list >= kMaxList) &&
+  // (a timed launch keeps it, and so does an adapting network's: their kernels have this
+  // list only)
+  int32_t cap = kRunBlock;
+  if (!timing && !tab->adapt && per_thread <= kBigMaxi && (geo->max_list == 0 || geo->max_list >= kMaxList) &&
       static_lds + (size_t)list_bytes(kMaxList) + lds <= (size_t)max_lds)
     cap = kMaxList;
   if (static_lds + (size_t)list_bytes(cap) + lds > (size_t)max_lds) return hipErrorInvalidValue;
@@ -618,6 +622,8 @@ extern "C" int wt_cond_scan_backward(const wt_tables* tab, const wt_backward_io*
     return hipErrorInvalidValue;
   if ((io->grad_decay || io->grad_jump || io->grad_scale) && !io->A) return hipErrorInvalidValue;
   if (io->grad_decay && !io->g_init) return hipErrorInvalidValue;
+  if (tab->adapt && (!tab->adapt_decay || !tab->E_adapt || !io->a_saved))
+    return hipErrorInvalidValue;
   if (io->B * tab->N == 0 || io->T == 0) return hipSuccess;
   BackArgs a = {};
   a.tab = *tab;
@@ -625,7 +631,7 @@ extern "C" int wt_cond_scan_backward(const wt_tables* tab, const wt_backward_io*
   return dispatch_S<BackRun>(tab->S, a, (hipStream_t)stream);
 }
 
-static int64_t back_fields_of(int64_t S) { return 1 + 9 * S + WT_MAX_K + 5; }
+static int64_t back_fields_of(int64_t S) { return 1 + 9 * S + WT_MAX_K + 5 + 4; }
 
 extern "C" int64_t wt_cond_recurrent_backward_scratch_bytes(int64_t S, int64_t K_rec, int64_t B,
                                                             int64_t N) {
@@ -645,6 +651,8 @@ extern "C" int wt_cond_recurrent_backward(const wt_tables* tab, const wt_side* r
     return hipErrorInvalidValue;
   if ((io->grad_decay || io->grad_jump || io->grad_scale) && !io->A) return hipErrorInvalidValue;
   if (io->grad_decay && !io->g_init) return hipErrorInvalidValue;
+  if (tab->adapt && (!tab->adapt_decay || !tab->E_adapt || !io->a_saved))
+    return hipErrorInvalidValue;
   if (rec->n_src != tab->N) return hipErrorInvalidValue;
   if (io->B * tab->N == 0 || io->T == 0) return hipSuccess;
   if (!rec->indptr || !rec->pathway) return hipErrorInvalidValue;

@@ -78,13 +78,15 @@ __host__ __device__ inline float spike_step(float v, float theta, int32_t& count
 
 // The exponential-Euler membrane step (dynamics.py:127-142). G (summed rise + decay
 // per synapse type, before clipping) and the currents are returned for saving and
-// tracking.
+// tracking. With `adapting`, the adaptation conductance ga (by E_a) is one more term of
+// the total conductance and of the current, added after the synapses' sums.
 template <int S>
 __host__ __device__ inline float membrane(float v, float r, const float (&gr)[S],
                                           const float (&gd)[S], const Synapses<S>& syn,
                                           float E_L, float C_m, float U_reset, Leak lk,
                                           float dt, float (&G)[S], float (&I)[S],
-                                          float& I_leak) {
+                                          float& I_leak, bool adapting = false,
+                                          float ga = 0.0f, float E_a = 0.0f) {
   float Gc[S];
 #pragma unroll
   for (int s = 0; s < S; ++s) {
@@ -96,6 +98,10 @@ __host__ __device__ inline float membrane(float v, float r, const float (&gr)[S]
   I_leak = lk.g_L * (v - E_L);
   float Gt = row_sum<S>(Gc);
   float J = row_sum<S>(I) + I_leak;
+  if (adapting) {
+    Gt = Gt + ga;
+    J = J + ga * (v - E_a);
+  }
   float x = dt * lk.rate + dt * Gt / C_m;
   float step = -expm1f(-x) / (lk.g_L + Gt);
   return (v - step * J) * (1.0f - r) + U_reset * r;
@@ -109,15 +115,20 @@ __host__ __device__ inline float membrane(float v, float r, const float (&gr)[S]
 //   d v_next / d Gc_s = -(phi_G J + phi (v - E_s)),  phi_G = (a dt / C_m - phi) / (g_L + Gt)
 // and the physiology terms below. With the Mg block Gc_s = C_s B_s(v) (C_s the clipped
 // conductance): dL/dC_s = dL/dGc_s B_s, and v gains dL/dGc_s C_s mg_a_s B_s (1 - B_s).
+// The adaptation conductance ga (by E_a) enters as a synapse type would, unclipped:
+// dL/dga = -(phi_G J + phi (v - E_a)) gx, and dL/dE_a = gx phi ga; d v_next / d v stays
+// a (J' = g_L + Gt with ga in Gt).
 struct MembraneAdjoint {
   float dv;      // dL/dv entering the step (membrane part)
   float phi, a, inv_g, J, Gt;
+  float d_ga;    // dL/dga (0 without adaptation)
 };
 
 template <int S>
 __host__ __device__ inline MembraneAdjoint membrane_adjoint(
     float gx, float v, const float (&G)[S], const Synapses<S>& syn, float E_L, float C_m,
-    Leak lk, float dt, float (&dG)[S], float (&Gc_out)[S]) {
+    Leak lk, float dt, float (&dG)[S], float (&Gc_out)[S], bool adapting = false,
+    float ga = 0.0f, float E_a = 0.0f) {
   float Gc[S], I[S], C[S], Bm[S];
 #pragma unroll
   for (int s = 0; s < S; ++s) {
@@ -129,6 +140,10 @@ __host__ __device__ inline MembraneAdjoint membrane_adjoint(
   }
   float Gt = row_sum<S>(Gc);
   float J = row_sum<S>(I) + lk.g_L * (v - E_L);
+  if (adapting) {
+    Gt = Gt + ga;
+    J = J + ga * (v - E_a);
+  }
   float x = dt * lk.rate + dt * Gt / C_m;
   float em = expm1f(-x);
   float a = 1.0f + em;
@@ -150,7 +165,8 @@ __host__ __device__ inline MembraneAdjoint membrane_adjoint(
     float pass = G[s] < syn.clip[s] ? 1.0f : (G[s] == syn.clip[s] ? 0.5f : 0.0f);
     dG[s] = G[s] >= 0.0f ? d * pass : 0.0f;
   }
-  return {dv, phi, a, inv_g, J, Gt};
+  const float d_ga = adapting ? k0 + k1 * E_a : 0.0f;
+  return {dv, phi, a, inv_g, J, Gt, d_ga};
 }
 
 // Surrogate gradient of the spike at x = v - theta (surrogate_gradients.py:30-33).

@@ -350,7 +350,9 @@ __device__ inline void run_events(const EventList& L, int m, int32_t total, doub
 // the whole launch.
 // BIG: the event list holds kMaxList entries, otherwise kRunBlock (static LDS, fixed
 // addresses either way; the host takes BIG where the accumulator leaves room).
-template <int S, int MAXI, bool EXTRA, bool REFR, bool BIG, bool TIMED>
+// ADAPT: the network adapts (tab.adapt set); kernels of their own, so that the others
+// carry none of its registers.
+template <int S, int MAXI, bool EXTRA, bool REFR, bool BIG, bool TIMED, bool ADAPT>
 __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   static_assert(MAXI <= 8, "the overflow note holds one bit per preloaded word");
   extern __shared__ __align__(16) double acc[];  // [K][tpg][range_n]
@@ -385,6 +387,9 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   constexpr bool refractory = REFR;  // the network has refractory periods
   const bool recurrent = A.tab.K_rec > 0 && A.rec.n_src > 0;
   const bool has_ff = A.ff.n_src > 0;
+  // spike-frequency adaptation: each item's g_a lives in io.adaptation, read and written
+  // by its owning thread each step (no register is held for it across the loop)
+  constexpr bool adapting = ADAPT;
   const float dt = *A.tab.dt;
   const int frac = A.geo.bound ? frac_bits_of(*A.geo.bound) : (int)A.geo.frac_bits;
   const Fixed fx{ldexpf(1.0f, frac), ldexp(1.0, -frac)};
@@ -691,9 +696,24 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
         const float held_t = (float)((masks >> (8 + i)) & 1u);
         const float r_hold = refractory ? fmaxf(s_t, held_t) : s_t;
         if (valid) spikes[out] = s_t;
+        // the adaptation conductance entering step t (dynamics.py:134-137)
+        const int64_t sidx = (g + (int64_t)q * groups) * N + n;
+        float ga = 0.0f, E_a = 0.0f;
+        if (adapting && valid) {
+          ga = gload(A.io.adaptation + sidx);
+          E_a = gload(A.tab.E_adapt + n);
+        }
         float G[S], I[S], I_leak;
         const float v_next = membrane<S>(v[i], r_hold, gr[i], gd[i], syn, p0.z, p0.w, p0.y,
-                                         Leak{p1.y, p1.z}, dt, G, I, I_leak);
+                                         Leak{p1.y, p1.z}, dt, G, I, I_leak, adapting, ga,
+                                         E_a);
+        if (adapting && valid) {  // it decays, and rises by the neuron's own spike
+          const float ga_next = ga * gload(A.tab.adapt_decay + n) + gload(A.tab.adapt + n) * s_t;
+          A.io.adaptation[sidx] = ga_next;
+          if (EXTRA && A.io.a_saved) A.io.a_saved[out] = ga;
+          if (EXTRA && A.io.track_a && (A.io.track_b < 0 || A.io.track_b == b))
+            A.io.track_a[((A.io.track_b < 0 ? b : 0) * T + t) * N + n] = ga_next;
+        }
         if (EXTRA && valid && A.io.v_saved) {
           A.io.v_saved[out] = v[i];
 #pragma unroll
@@ -1072,17 +1092,18 @@ __global__ __launch_bounds__(kRunBlock) void cond_run_kernel(RunArgs A) {
   if (TIMED && threadIdx.x < kPhases) A.timing[wg * kPhases + threadIdx.x] = s_time[threadIdx.x];
 }
 
-template <int S, int MAXI, bool EXTRA, bool REFR, bool BIG, bool TIMED = false>
+template <int S, int MAXI, bool EXTRA, bool REFR, bool BIG, bool TIMED = false,
+          bool ADAPT = false>
 inline hipError_t launch_one(RunArgs& a, size_t lds, hipStream_t stream, bool coop) {
   const void* fn =
-      reinterpret_cast<const void*>(&cond_run_kernel<S, MAXI, EXTRA, REFR, BIG, TIMED>);
+      reinterpret_cast<const void*>(&cond_run_kernel<S, MAXI, EXTRA, REFR, BIG, TIMED, ADAPT>);
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   dim3 grid((unsigned)(a.geo.groups * a.geo.R)), blk((unsigned)kRunBlock);
   void* params[] = {&a};
   if (coop) return hipLaunchCooperativeKernel(fn, grid, blk, params, (unsigned)lds, stream);
-  hipLaunchKernelGGL((cond_run_kernel<S, MAXI, EXTRA, REFR, BIG, TIMED>), grid, blk, lds, stream,
-                     a);
+  hipLaunchKernelGGL((cond_run_kernel<S, MAXI, EXTRA, REFR, BIG, TIMED, ADAPT>), grid, blk, lds,
+                     stream, a);
   return hipGetLastError();
 }
 
@@ -1090,6 +1111,15 @@ template <int S, int MAXI, bool BIG>
 inline hipError_t launch_flags(RunArgs& a, size_t lds, hipStream_t stream, bool coop) {
   const bool extra = a.io.prob || a.io.v_saved || a.io.A_saved || a.io.track_v || a.io.track_g;
   const bool refr = a.tab.n_ref != nullptr;
+  if (a.tab.adapt) {  // adapting networks: the saving kernels with the 1024-entry list
+    if constexpr (BIG) {
+      return hipErrorInvalidValue;
+    } else {
+      if (a.timing) return hipErrorInvalidValue;
+      return refr ? launch_one<S, MAXI, true, true, false, false, true>(a, lds, stream, coop)
+                  : launch_one<S, MAXI, true, false, false, false, true>(a, lds, stream, coop);
+    }
+  }
   if (a.timing) {  // timed kernels: lean outputs and the 1024-entry list only
     if (extra || BIG) return hipErrorInvalidValue;
     return refr ? launch_one<S, MAXI, false, true, false, true>(a, lds, stream, coop)

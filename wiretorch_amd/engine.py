@@ -21,9 +21,10 @@ What differs from the reference is underneath:
 
 The engine runs only on a GPU with the library built; it raises otherwise. Not
 supported (raising ``NotImplementedError``): per-step gradient retention
-(``retain``), float16 storage, sampled spikes, presynaptic dynamics, adaptation. The
-NMDA Mg block (``Physiology.mg_c`` / ``mg_a``) is evaluated in the forward and both
-backward passes.
+(``retain``), float16 storage, sampled spikes, presynaptic dynamics. The NMDA Mg block
+(``Physiology.mg_c`` / ``mg_a``) and spike-frequency adaptation (``Physiology.adapt`` /
+``adapt_decay`` / ``E_adapt``, its conductances entering as ``adaptation`` and leaving as
+``Run.adaptation``) are evaluated in the forward and both backward passes.
 """
 
 from __future__ import annotations
@@ -40,7 +41,8 @@ from wiretorch_amd.inputs import PoissonInput
 from wiretorch_amd.network import Drive, Physiology, Run
 
 #: Physiology the backward pass can differentiate, in ``Physiology`` names.
-PHYSIOLOGY = ("theta", "U_reset", "E_L", "C_m", "beta", "E_syn", "decay", "jump")
+PHYSIOLOGY = ("theta", "U_reset", "E_L", "C_m", "beta", "E_syn", "decay", "jump", "adapt",
+              "adapt_decay", "E_adapt")
 BLOCK = 1024
 #: Upper limit on trial groups (the kernel takes up to 64); ``geometry`` picks the count.
 MAX_GROUPS = 64
@@ -636,6 +638,8 @@ class _Plan:
     bound: torch.Tensor
     max_list: int
     refractory: bool
+    #: spike-frequency adaptation (the physiology's adapt is set)
+    adapting: bool
     probabilities: bool
     track: bool
     track_b: int
@@ -668,7 +672,8 @@ class _Plan:
             t["jump"].data_ptr(), t["made"].data_ptr(), scale.data_ptr(),
             t["dt"].data_ptr(), t["surr"].data_ptr(), t["types"].data_ptr(),
             type_of.data_ptr(), n_types, _lib.ptr(range_rows), _lib.ptr(t["mg_a"]),
-            _lib.ptr(t["mg_lc"]), self.N, self.S, self.K, self.K_rec,
+            _lib.ptr(t["mg_lc"]), _lib.ptr(t["adapt"]), _lib.ptr(t["adapt_decay"]),
+            _lib.ptr(t["E_adapt"]), self.N, self.S, self.K, self.K_rec,
         )  # fmt: skip
 
 
@@ -710,7 +715,8 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
                         lambda: bound + ff_max * x_max)
     names = ("theta", "U_reset", "E_L", "C_m", "beta", "E_syn", "g_clip", "decay", "jump")
     sources = tuple(getattr(p, name) for name in names) + (
-        drive.made, drive.scale, p.dt, p.surr_scale, p.n_ref, p.mg_c, p.mg_a)
+        drive.made, drive.scale, p.dt, p.surr_scale, p.n_ref, p.mg_c, p.mg_a, p.adapt,
+        p.adapt_decay, p.E_adapt)
 
     def make_tables():
         tables = {name: _f32(getattr(p, name), device) for name in names}
@@ -726,6 +732,8 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
             tables["mg_lc"] = torch.log(p.mg_c.detach().cpu().float()).to(device)
         else:
             tables["mg_a"] = tables["mg_lc"] = None
+        for name in ("adapt", "adapt_decay", "E_adapt"):  # per neuron, when adapting
+            tables[name] = _f32(getattr(p, name), device) if p.adapt is not None else None
         return tables
 
     # the tables (and the distinct-row search) are rebuilt only when a source changes
@@ -737,14 +745,15 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
         B=B, T=T, N=N, S=S, K_rec=K_rec, K_ff=K_ff, n_in=n_in, tables=tables, rec=rec,
         ff=ff, geo=(groups, R, range_n), range_types=range_types, bound=bound,
         max_list=max_list,
-        refractory=p.n_ref is not None, probabilities=probabilities, track=track,
+        refractory=p.n_ref is not None, adapting=p.adapt is not None,
+        probabilities=probabilities, track=track,
         track_b=(-1 if track_batch_idx is None else int(track_batch_idx)) if track else 0,
         stream=torch.cuda.current_stream(device).cuda_stream, device=device,
     )  # fmt: skip
 
 
 def _launch(L: _Plan, x, scale, v, g, counter, spikes, prob, saved, tracked,
-            rec_weights=None, ff_weights=None) -> None:
+            rec_weights=None, ff_weights=None, adaptation=None, a_saved=None) -> None:
     groups, R, range_n = L.geo
     geo = L.abi_geometry()
     lib = _lib.load()
@@ -754,6 +763,12 @@ def _launch(L: _Plan, x, scale, v, g, counter, spikes, prob, saved, tracked,
     v_saved, G_saved, held, A_saved = saved if saved is not None else (None,) * 4
     tv, tI, tg = ((tracked["v"], tracked["I"], tracked["g"]) if tracked is not None
                   else (None, None, None))
+    ta = tracked.get("a") if tracked is not None else None
+    if L.adapting and (adaptation is None or adaptation.shape != (L.B, L.N)
+                       or adaptation.dtype != torch.float32 or not adaptation.is_contiguous()
+                       or adaptation.device != L.device):
+        raise ValueError(f"an adapting network needs its (B, N) float32 adaptation state on "
+                         f"{L.device}")
     pin = L.poisson
     io = _lib.RunIO(
         None if pin is not None else x.data_ptr(), L.B, L.T, L.n_in, v.data_ptr(),
@@ -762,6 +777,8 @@ def _launch(L: _Plan, x, scale, v, g, counter, spikes, prob, saved, tracked,
         _lib.ptr(A_saved), _lib.ptr(tv), _lib.ptr(tI), _lib.ptr(tg), L.track_b,
         pin.prob.data_ptr() if pin is not None else None, pin.seed if pin is not None else 0,
         pin.t0 if pin is not None else 0,
+        _lib.ptr(adaptation) if L.adapting else None, _lib.ptr(a_saved) if L.adapting else None,
+        _lib.ptr(ta) if L.adapting else None,
     )  # fmt: skip
     rec = L.rec.abi(R, range_n, L.stream, rec_weights)
     ff = L.ff.abi(R, range_n, L.stream, ff_weights)
@@ -830,7 +847,7 @@ class _Run(torch.autograd.Function):
     the input ``x``, the pathway weights and the physiology (``PHYSIOLOGY``)."""
 
     @staticmethod
-    def forward(ctx, L: _Plan, n_rec_w: int, scale, x, v, g, counter, *rest):
+    def forward(ctx, L: _Plan, n_rec_w: int, scale, x, v, g, counter, adaptation, *rest):
         weights, physiology = rest[: len(rest) - len(PHYSIOLOGY)], rest[-len(PHYSIOLOGY):]
         dev = L.device
         spikes = torch.empty((L.B, L.T, L.N), device=dev)
@@ -839,29 +856,31 @@ class _Run(torch.autograd.Function):
         G_saved = torch.empty((L.B, L.T, L.N, L.S), device=dev)
         held = torch.empty((L.B, L.T, L.N), dtype=torch.int8, device=dev) if L.refractory else None
         A_saved = torch.empty((max(L.K, 1), L.B, L.T, L.N), device=dev)
+        a_saved = torch.empty_like(spikes) if L.adapting else spikes.new_empty(0)
         want_decay = physiology[PHYSIOLOGY.index("decay")].requires_grad
         g_init = g.clone() if want_decay else None
         tracked = _tracked_buffers(L)
         _launch(L, x.detach().float().contiguous(), scale.detach().float().contiguous(), v, g,
                 counter, spikes, prob, (v_saved, G_saved, held, A_saved), tracked,
-                *_sparse_weights(L, weights, n_rec_w))
+                *_sparse_weights(L, weights, n_rec_w), adaptation=adaptation, a_saved=a_saved)
         ctx.L, ctx.n_rec_w, ctx.tracked = L, n_rec_w, tracked
         ctx.save_for_backward(scale, x, spikes, v_saved, G_saved,
                               held if held is not None else spikes.new_empty(0),
                               A_saved, g_init if g_init is not None else spikes.new_empty(0),
-                              *weights)
-        ctx.mark_non_differentiable(v, g, counter)
-        return spikes, prob, v, g, counter
+                              a_saved, *weights)
+        ctx.mark_non_differentiable(v, g, counter, adaptation)
+        return spikes, prob, v, g, counter, adaptation
 
     @staticmethod
-    def backward(ctx, grad_spikes, grad_prob, _v, _g, _c):
+    def backward(ctx, grad_spikes, grad_prob, _v, _g, _c, _a):
         check_errors(wait=True)  # the forward this backward differentiates is complete
         L, n_rec_w = ctx.L, ctx.n_rec_w
-        scale, x, spikes, v_saved, G_saved, held, A_saved, g_init, *weights = ctx.saved_tensors
+        (scale, x, spikes, v_saved, G_saved, held, A_saved, g_init, a_saved,
+         *weights) = ctx.saved_tensors
         needs = ctx.needs_input_grad
         want_scale, want_x = needs[2], needs[3]
-        w_needs = needs[7: 7 + len(weights)]
-        p_needs = needs[7 + len(weights):]
+        w_needs = needs[8: 8 + len(weights)]
+        p_needs = needs[8 + len(weights):]
         if grad_spikes is None:
             grad_spikes = torch.zeros_like(spikes)
         want_A = want_x or any(w_needs)
@@ -869,7 +888,7 @@ class _Run(torch.autograd.Function):
         B, T, N, S, K = L.B, L.T, L.N, L.S, L.K
         grad_A = torch.empty((max(K, 1), B, T, N), device=dev) if want_A else None
         partial = torch.empty((max(K, 1), B, N), device=dev) if want_scale else None
-        shapes = [(B, N)] * 5 + [(B, S, N), (B, 2, S, N), (B, 2, S, N)]
+        shapes = [(B, N)] * 5 + [(B, S, N), (B, 2, S, N), (B, 2, S, N)] + [(B, N)] * 3
         phys = [torch.empty(sh, device=dev) if want else None for sh, want in zip(shapes, p_needs)]
         io = _lib.BackwardIO(
             grad_spikes.contiguous().data_ptr(),
@@ -877,7 +896,8 @@ class _Run(torch.autograd.Function):
             spikes.data_ptr(), v_saved.data_ptr(), G_saved.data_ptr(),
             held.data_ptr() if L.refractory else None, A_saved.data_ptr(),
             g_init.data_ptr() if g_init.numel() else None, B, T,
-            _lib.ptr(grad_A), _lib.ptr(partial), *[_lib.ptr(t) for t in phys],
+            _lib.ptr(grad_A), _lib.ptr(partial), *[_lib.ptr(t) for t in phys[:8]],
+            a_saved.data_ptr() if L.adapting else None, *[_lib.ptr(t) for t in phys[8:]],
         )  # fmt: skip
         tab = L.abi_tables(scale.detach().float().contiguous())
         lib = _lib.load()
@@ -894,7 +914,7 @@ class _Run(torch.autograd.Function):
             with _timed("backward"):
                 _lib.check(lib.wt_cond_scan_backward(tab, io, L.stream), "wt_cond_scan_backward")
         grad_scale = partial.sum(dim=1) if want_scale else None
-        dims = [0] * 5 + [(0, 2), (0, 3), (0, 3)]
+        dims = [0] * 5 + [(0, 2), (0, 3), (0, 3)] + [0] * 3
         grad_phys = [t.sum(d) if t is not None else None for t, d in zip(phys, dims)]
         grad_w = [None] * len(weights)
         with _timed("weight_gradient"):
@@ -907,7 +927,7 @@ class _Run(torch.autograd.Function):
                 grad_w[n_rec_w:] = _weight_grads(L, L.ff, activity, grad_A, L.K_rec,
                                                  weights[n_rec_w:], w_needs[n_rec_w:])
         grad_x = _input_grad(L, x, grad_A, weights[n_rec_w:]) if want_x else None
-        return (None, None, grad_scale, grad_x, None, None, None, *grad_w, *grad_phys)
+        return (None, None, grad_scale, grad_x, None, None, None, None, *grad_w, *grad_phys)
 
 
 def _tracked_buffers(L: _Plan):
@@ -915,11 +935,14 @@ def _tracked_buffers(L: _Plan):
         return None
     Bt = L.B if L.track_b < 0 else 1
     dev = L.device
-    return {
+    tracked = {
         "v": torch.empty((Bt, L.T, L.N), device=dev),
         "I": torch.empty((Bt, L.T, L.N, L.S + 1), device=dev),
         "g": torch.empty((Bt, L.T, L.N, 2, L.S), device=dev),
     }
+    if L.adapting:
+        tracked["a"] = torch.empty((Bt, L.T, L.N), device=dev)
+    return tracked
 
 
 def _sparse_weights(L: _Plan, weights, n_rec_w):
@@ -1021,8 +1044,8 @@ def simulate(
     check_errors()
     if retain is not None:
         raise NotImplementedError("per-step gradient retention (track_gradients)")
-    if gating is not None or drive.gates or adaptation is not None or p.adapt is not None:
-        raise NotImplementedError("presynaptic dynamics and adaptation")
+    if gating is not None or drive.gates:
+        raise NotImplementedError("presynaptic dynamics")
     if p.spike_mode != "deterministic":
         raise NotImplementedError("sampled spikes")
     if p.storage_dtype != torch.float32:
@@ -1044,6 +1067,14 @@ def simulate(
         refractory = torch.zeros(v.shape, dtype=torch.int32, device=device)
     counter = refractory.to(device=device, dtype=torch.int32).clone(
         memory_format=torch.contiguous_format)
+    # the adaptation conductances (updated in place, like the state); none without it
+    if not L.adapting:
+        adaptation = torch.empty((0,), device=device)
+    elif adaptation is None:
+        adaptation = torch.zeros(v.shape, device=device)
+    else:
+        adaptation = adaptation.detach().to(device=device, dtype=torch.float32).clone(
+            memory_format=torch.contiguous_format)
 
     # a compressed side's weights are read by the kernels themselves: on the launch device
     # (a differentiable copy where they were built elsewhere)
@@ -1056,12 +1087,13 @@ def simulate(
     grad = torch.is_grad_enabled() and (
         scale.requires_grad or x.requires_grad
         or any(W.requires_grad for W in rec_w + ff_w)
-        or any(t.requires_grad for t in physiology)
+        or any(t is not None and t.requires_grad for t in physiology)
     )  # fmt: skip
     L.recurrent_gradients = bool(drive.recurrent_gradients and L.K_rec and L.rec.n_src)
     if grad:
-        spikes, prob, v, g_state, counter = _Run.apply(
-            L, len(rec_w), scale, x, v, g_state, counter, *rec_w, *ff_w, *physiology
+        spikes, prob, v, g_state, counter, adaptation = _Run.apply(
+            L, len(rec_w), scale, x, v, g_state, counter, adaptation, *rec_w, *ff_w,
+            *physiology
         )
         tracked = None
         if track:  # the buffers live on the autograd context; rebuild from the last run
@@ -1074,7 +1106,7 @@ def simulate(
             rw, fw = _sparse_weights(L, rec_w + ff_w, len(rec_w))
             _launch(L, x.detach().float().contiguous(),
                     scale.detach().float().contiguous(), v, g_state, counter, spikes,
-                    prob, None, tracked, rw, fw)
+                    prob, None, tracked, rw, fw, adaptation=adaptation)
     return Run(
         output=spikes,
         v=v,
@@ -1082,6 +1114,7 @@ def simulate(
         probabilities=prob,
         tracked=tracked,
         refractory=counter,
+        adaptation=adaptation if L.adapting else None,
     )
 
 
