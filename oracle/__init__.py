@@ -12,7 +12,13 @@ Modules:
   surrogate spike of ``src/wiretorch/training_utils/surrogate_gradients.py:9-33``.
   Gradients come from torch autograd through the restated step, as in the reference.
   Pinned by the reference's recorded fixtures (``tests/golden/reference/*.npz``:
-  lockstep, free run, gradients), see ``tests/test_oracle_fixtures.py``.
+  lockstep, free run, gradients), see ``tests/test_oracle_fixtures.py``. Its optional
+  terms, which no fixture exercises: the Mg block (``dynamics.py:110-129``) by the
+  tracked currents against ``B G (v - E)`` in float64 and the block-free network bit for
+  bit (``tests/test_nmda.py``); adaptation (``dynamics.py:116-143,200-202``) by the
+  exact solution of the membrane with the adaptation conductance held over a step, the
+  tracked adaptation against its recursion from the spikes, and the non-adapting network
+  bit for bit (``tests/test_adaptation.py``).
 * ``oracle.sparse`` — the compressed-connectome propagation used at fly scale, where
   the reference's dense per-pathway rows cannot be built. Pinned against the dense
   product on small networks (``tests/test_oracle_pinning.py``,

@@ -65,6 +65,34 @@ def test_adaptation_follows_the_spikes():
     torch.testing.assert_close(model.adaptation, out["adaptation"][:, -1])
 
 
+def test_membrane_term_is_the_closed_form():
+    """With no input and below threshold, each step of the exponential-Euler update with
+    the adaptation conductance g_a(t) held over the step is the exact solution of
+    C dv/dt = -g_L (v - E_L) - g_a (v - E_adapt): v_inf + (v - v_inf) exp(-dt (g_L + g_a) / C)
+    with v_inf = (g_L E_L + g_a E_adapt) / (g_L + g_a), and g_a(t) = g_a(0) decay^t.
+    Evaluated in float64 from the physiology tables; a dropped term of the conductance or
+    a wrong sign of the current fails it."""
+    model = _driven(ADAPT, n=1, batch_size=1)
+    model.reset_state()
+    with torch.no_grad():
+        model.v.fill_(-60.0)
+        model.adaptation.fill_(5.0)
+    p = model._physiology()
+    C, beta = float(p.C_m[0]), float(p.beta[0])
+    E_L, E_a, dt = float(p.E_L[0]), float(p.E_adapt[0]), float(p.dt)
+    decay = float(p.adapt_decay[0])
+    g_L = C * -math.log(beta) / dt
+    out = model(torch.zeros((1, 20, 1)))
+    assert not out["spikes"].any()
+    v, g_a = -60.0, 5.0
+    for t in range(20):
+        v_inf = (g_L * E_L + g_a * E_a) / (g_L + g_a)
+        v = v_inf + (v - v_inf) * math.exp(-dt * (g_L + g_a) / C)
+        g_a *= decay
+        assert abs(float(out["voltages"][0, t, 0]) - v) < 1e-4, t
+        assert abs(float(out["adaptation"][0, t, 0]) - g_a) < 1e-5, t
+
+
 def test_intervals_lengthen():
     """Under constant drive the intervals lengthen as the adaptation builds up; without it
     they are regular."""
