@@ -99,7 +99,16 @@ struct BackNeuron {
   float theta, E_L, C_m, beta, dt, k_surr;
   Leak lk;
   float a_decay, E_a;  // adaptation (0 without)
+  // bit k * S + s: pathway k makes synapse type s (tab.made), read once here: loads of
+  // the table between the reverse steps' stores would each wait for all of the thread's
+  // outstanding memory operations (the compiler cannot rule out that a store aliases it)
+  uint64_t made;
 };
+
+// tab.made[k * S + s] (0 or 1) from the mask.
+__device__ inline float made_at(uint64_t made, int bit) {
+  return ((made >> bit) & 1ull) ? 1.0f : 0.0f;
+}
 
 // AD: the network adapts (tab.adapt set). The backward kernels are compiled with and
 // without it, so that a network without adaptation carries none of its registers.
@@ -115,6 +124,9 @@ __device__ inline BackNeuron back_neuron(const wt_tables& tab, int64_t n) {
   c.lk = leak(c.C_m, c.beta, c.dt);
   c.a_decay = AD ? tab.adapt_decay[n] : 0.0f;
   c.E_a = AD ? tab.E_adapt[n] : 0.0f;
+  c.made = 0;
+  for (int64_t i = 0; i < tab.K * tab.S; ++i)
+    if (tab.made[i] != 0.0f) c.made |= 1ull << i;
   return c;
 }
 
@@ -194,7 +206,7 @@ __device__ inline void back_membrane_step(BackState<S>& st, const BackArgs& P,
       if (k >= K) break;
       const float as = step_A<S>(in, P, k, b, n, t) * scale[k];
 #pragma unroll
-      for (int s = 0; s < S; ++s) base[s] += as * tab.made[k * S + s];
+      for (int s = 0; s < S; ++s) base[s] += as * made_at(c.made, k * S + s);
     }
 #pragma unroll
     for (int s = 0; s < S; ++s) {
@@ -217,7 +229,7 @@ __device__ inline void back_membrane_step(BackState<S>& st, const BackArgs& P,
     float qk = 0.0f;
 #pragma unroll
     for (int s = 0; s < S; ++s)
-      qk += (syn.jump_r[s] * st.lr[s] + syn.jump_d[s] * st.ld[s]) * tab.made[k * S + s];
+      qk += (syn.jump_r[s] * st.lr[s] + syn.jump_d[s] * st.ld[s]) * made_at(c.made, k * S + s);
     const int64_t ka = ((k * B + b) * T + t) * N + n;
     const float ga = qk * scale[k];
     if (want_A) io.grad_A[ka] = ga;
@@ -324,9 +336,12 @@ __device__ inline void back_finish(const BackState<S>& st, const BackArgs& P, in
   }
 }
 
-// Recurrent activations as inputs: one thread per (trial, neuron), all steps.
+// Recurrent activations as inputs: one thread per (trial, neuron), all steps. Held to
+// three waves per SIMD (at most 168 VGPRs; a few values spill): with two, too few reverse
+// steps are in flight to cover the loads a step ahead (config 3: 3.39 ms against 3.89).
 template <int S, bool AD>
-__global__ __launch_bounds__(256) void cond_backward_kernel(BackArgs P) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void
+cond_backward_kernel(BackArgs P) {
   const int64_t N = P.tab.N, B = P.io.B, T = P.io.T;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= B * N) return;
