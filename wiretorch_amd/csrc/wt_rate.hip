@@ -890,6 +890,11 @@ static int forward_slices(const wt_rate_operand& op) {
 // Step t after a split product: per (trial, neuron), the recurrent activation (the KS
 // partials summed in slice order), the input pathways', then the currents, voltage and
 // next rate — the fused step's epilogue, one element per thread (neurons fastest).
+// Every load is issued before the first store: on gfx950 one counter tracks a wave's
+// outstanding loads and stores alike, so a load placed after a store (the compiler keeps
+// the program order where it cannot rule out aliasing) makes its use wait for the store.
+constexpr int kUpdateFF = 2;  // input pathways held in registers (the rest read in turn)
+
 template <typename T, int S>
 __global__ __launch_bounds__(kThreads) void rate_update_kernel(RateArgs a, const float* P,
                                                                int KS) {
@@ -902,41 +907,72 @@ __global__ __launch_bounds__(kThreads) void rate_update_kernel(RateArgs a, const
   const int64_t b = idx / N, n = idx - b * N;
   const int64_t el = (b * T_ + t) * N + n;
   const int64_t path = op.seg[0][2];
+  const int64_t K_ff = tb.K - tb.K_rec;
+  // ---- loads ----
   const float* q = P + b * op.N_pad + n;
   const int64_t slice = op.B_pad * op.N_pad;
-  float p[kMaxSlices];  // every slice's load first, then the sum in slice order
+  float p[kMaxSlices];
 #pragma unroll
   for (int ks = 0; ks < kMaxSlices; ++ks) p[ks] = ks < KS ? q[ks * slice] : 0.0f;
+  float jr[S], dec[S], sgn[S], I_prev[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    jr[s] = tb.jump[(path * N + n) * S + s];
+    dec[s] = tb.decay[s];
+    sgn[s] = tb.sign[s];
+  }
+  float ak[kUpdateFF], jf[kUpdateFF][S];
+#pragma unroll
+  for (int j = 0; j < kUpdateFF; ++j) {
+    const int64_t k = tb.K_rec + j;
+    ak[j] = j < K_ff ? io.A_ff[j * B * T_ * N + el] : 0.0f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) jf[j][s] = j < K_ff ? tb.jump[(k * N + n) * S + s] : 0.0f;
+  }
+  float v = io.v_saved ? io.v_saved[el] : io.v[b * N + n];
+#pragma unroll
+  for (int s = 0; s < S; ++s) I_prev[s] = dec[s] != 0.0f ? io.I[(b * S + s) * N + n] : 0.0f;
+  const float beta = tb.beta[n], gain = tb.gain[n], theta = tb.theta[n];
+  const int32_t code = tb.nonlinearity[n];
+  const int32_t pos = op.rpos ? op.rpos[n] : -1;
+  // ---- arithmetic, in the reference's order ----
   float act = p[0];
 #pragma unroll
   for (int ks = 1; ks < kMaxSlices; ++ks)
     if (ks < KS) act = act + p[ks];
   float target[S];
 #pragma unroll
-  for (int s = 0; s < S; ++s) target[s] = 0.0f + act * tb.jump[(path * N + n) * S + s];
-  if (io.A_saved) io.A_saved[((path * B + b) * T_ + t) * N + n] = act;
-  for (int64_t k = tb.K_rec; k < tb.K; ++k) {  // the input pathways, in order
-    const float ak = io.A_ff[(k - tb.K_rec) * B * T_ * N + el];
+  for (int s = 0; s < S; ++s) target[s] = 0.0f + act * jr[s];
 #pragma unroll
-    for (int s = 0; s < S; ++s) target[s] = target[s] + ak * tb.jump[(k * N + n) * S + s];
-    if (io.A_saved) io.A_saved[k * B * T_ * N + el] = ak;
+  for (int j = 0; j < kUpdateFF; ++j) {  // the input pathways, in order
+    if (j >= K_ff) break;
+#pragma unroll
+    for (int s = 0; s < S; ++s) target[s] = target[s] + ak[j] * jf[j][s];
+  }
+  // ---- stores (and the input pathways past the registers: loads after stores) ----
+  if (io.A_saved) {
+    io.A_saved[((path * B + b) * T_ + t) * N + n] = act;
+#pragma unroll
+    for (int j = 0; j < kUpdateFF; ++j)
+      if (j < K_ff) io.A_saved[(tb.K_rec + j) * B * T_ * N + el] = ak[j];
+  }
+  for (int64_t k = tb.K_rec + kUpdateFF; k < tb.K; ++k) {
+    const float a_k = io.A_ff[(k - tb.K_rec) * B * T_ * N + el];
+#pragma unroll
+    for (int s = 0; s < S; ++s) target[s] = target[s] + a_k * tb.jump[(k * N + n) * S + s];
+    if (io.A_saved) io.A_saved[k * B * T_ * N + el] = a_k;
   }
   const bool last = t + 1 == T_;
   float I[S], I_syn = 0.0f;
-  float v = io.v_saved ? io.v_saved[el] : io.v[b * N + n];
 #pragma unroll
   for (int s = 0; s < S; ++s) {
-    const float d = tb.decay[s];
-    const float I_prev = d != 0.0f ? io.I[(b * S + s) * N + n] : 0.0f;
-    I[s] = d * I_prev + (1.0f - d) * target[s];
-    I_syn = I_syn + I[s] * tb.sign[s];
+    I[s] = dec[s] * I_prev[s] + (1.0f - dec[s]) * target[s];
+    I_syn = I_syn + I[s] * sgn[s];
   }
-  const float beta = tb.beta[n];
   v = beta * v + (1.0f - beta) * I_syn;
-  const float r = tb.gain[n] * nonlin(tb.nonlinearity[n], v - tb.theta[n]);
+  const float r = gain * nonlin(code, v - theta);
   if (!last) {
     io.out[el + N] = r;
-    const int32_t pos = op.rpos ? op.rpos[n] : -1;
     if (pos >= 0)
       static_cast<T*>(op.rin)[(((t + 1) & 1) * op.B_pad + b) * op.K_rec_pad + pos] =
           to_storage<T>(r);
@@ -945,7 +981,7 @@ __global__ __launch_bounds__(kThreads) void rate_update_kernel(RateArgs a, const
   if (!io.v_saved || last) io.v[b * N + n] = v;
 #pragma unroll
   for (int s = 0; s < S; ++s)
-    if (tb.decay[s] != 0.0f || last) io.I[(b * S + s) * N + n] = I[s];
+    if (dec[s] != 0.0f || last) io.I[(b * S + s) * N + n] = I[s];
 #pragma unroll
   for (int s = 0; s < S; ++s) {
     if (io.target_saved) io.target_saved[el * S + s] = target[s];
