@@ -139,10 +139,10 @@ __global__ void weight_gradient_kernel(wt_side side, const int64_t* edge_src, in
 
 // The same sums, grouped by (pathway, target): workgroup kn = k * N + n holds the
 // target's dL/da_k over every (trial, step), row kn of grad_A_T (k, n, b*T+t), in LDS —
-// read once, contiguously — and each wave takes one incoming synapse at a time: its 64
-// lanes read 64 consecutive events of the synapse's source (one coalesced load) and add
-// the row's entries; the lanes' partial sums are then added in a fixed tree (the sum is
-// deterministic). Rows longer than the LDS chunk are taken a chunk at a time, each
+// read once, contiguously — and each wave takes its incoming synapses one at a time: its
+// 64 lanes read 64 consecutive events of the synapse's source (one coalesced load) and
+// add the row's entries; the lanes' partial sums are then added in a fixed tree (the sum
+// is deterministic). The synapses' lookups are made 64 at a time, one per lane. Rows longer than the LDS chunk are taken a chunk at a time, each
 // synapse's running sum kept in grad_w.
 constexpr int kWgBlock = 1024;
 constexpr int64_t kWgChunk = 32768;  // floats of a row in LDS (128 KB)
@@ -164,6 +164,14 @@ __global__ __launch_bounds__(256) void transpose_rows_kernel(const float* src, f
     const int64_t n = n0 + r, bt = bt0 + tx;
     if (bt < BT && n < N) d[n * BT + bt] = tile[tx][r];
   }
+}
+
+// Lane k's 64-bit value, in every lane (k wave-uniform).
+__device__ inline int64_t readlane64(int64_t v, int k) {
+  const uint64_t u = (uint64_t)v;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, k);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), k);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
 __global__ __launch_bounds__(kWgBlock) void weight_gradient_target_kernel(
@@ -198,47 +206,65 @@ __global__ __launch_bounds__(kWgBlock) void weight_gradient_target_kernel(
       for (int64_t i = threadIdx.x; i < len; i += blockDim.x) row[i] = src[c0 + i];
     }
     __syncthreads();
-    for (int64_t ei = e0 + wave; ei < e1; ei += n_waves) {
-      const int64_t e = in_edge[ei], j = edge_src[e];
-      int64_t i0 = ev_indptr[j];
-      const int64_t i1 = ev_indptr[j + 1];
-      if (c0 > 0) {  // the first event at or past the chunk (events ascend in b*T+t)
-        int64_t lo = i0, hi = i1;
-        while (lo < hi) {
-          const int64_t mid = (lo + hi) >> 1;
-          if (ev_bt[mid] < c0) lo = mid + 1; else hi = mid;
-        }
-        i0 = lo;
-      }
-      float part = 0.0f;
-      int64_t i = i0 + lane;
-      for (; i + 192 < i1; i += 256) {  // four events per lane in flight
-        int64_t bt[4];
-        float val[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          bt[u] = ev_bt[i + 64 * u] - c0;
-          val[u] = ev_val[i + 64 * u];
-        }
-        bool past = false;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (bt[u] >= len) past = true;
-          if (!past) part += val[u] * row[bt[u]];
-        }
-        if (past) {  // this lane's later events are past the chunk too
-          i = i1;
-          break;
+    // Wave w takes in-edges e0 + w, e0 + w + n_waves, ... (as one at a time would), 64 at
+    // a time: lane l looks up edge l's synapse, source and event range (and, past the
+    // first chunk, its first event in the chunk) for all 64 together, and keeps edge l's
+    // sum; the sums are stored after the 64. Done one edge after another, each edge's
+    // dependent lookups cost four round trips to memory, and its store made the next
+    // edge's loads wait (one counter covers a wave's loads and stores).
+    for (int64_t base = e0 + wave; base < e1; base += 64 * (int64_t)n_waves) {
+      const int64_t my_ei = base + (int64_t)lane * n_waves;
+      int64_t my_e = 0, my_i0 = 0, my_i1 = 0;
+      if (my_ei < e1) {
+        my_e = in_edge[my_ei];
+        const int64_t j = edge_src[my_e];
+        my_i0 = ev_indptr[j];
+        my_i1 = ev_indptr[j + 1];
+        if (c0 > 0) {  // the first event at or past the chunk (events ascend in b*T+t)
+          int64_t lo = my_i0, hi = my_i1;
+          while (lo < hi) {
+            const int64_t mid = (lo + hi) >> 1;
+            if (ev_bt[mid] < c0) lo = mid + 1; else hi = mid;
+          }
+          my_i0 = lo;
         }
       }
-      for (; i < i1; i += 64) {
-        const int64_t bt = ev_bt[i] - c0;
-        if (bt >= len) break;
-        part += ev_val[i] * row[bt];
-      }
+      const int64_t left = (e1 - base + n_waves - 1) / n_waves;
+      const int cnt = left < 64 ? (int)left : 64;
+      float mine = 0.0f;
+      for (int k = 0; k < cnt; ++k) {
+        const int64_t i0 = readlane64(my_i0, k), i1 = readlane64(my_i1, k);
+        float part = 0.0f;
+        int64_t i = i0 + lane;
+        for (; i + 192 < i1; i += 256) {  // four events per lane in flight
+          int64_t bt[4];
+          float val[4];
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
-      if (lane == 0) grad_w[e] = (c0 > 0 ? grad_w[e] : 0.0f) + part;
+          for (int u = 0; u < 4; ++u) {
+            bt[u] = ev_bt[i + 64 * u] - c0;
+            val[u] = ev_val[i + 64 * u];
+          }
+          bool past = false;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            if (bt[u] >= len) past = true;
+            if (!past) part += val[u] * row[bt[u]];
+          }
+          if (past) {  // this lane's later events are past the chunk too
+            i = i1;
+            break;
+          }
+        }
+        for (; i < i1; i += 64) {
+          const int64_t bt = ev_bt[i] - c0;
+          if (bt >= len) break;
+          part += ev_val[i] * row[bt];
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
+        if (lane == k) mine = part;
+      }
+      if (my_ei < e1) grad_w[my_e] = (c0 > 0 ? grad_w[my_e] : 0.0f) + mine;
     }
   }
 }
