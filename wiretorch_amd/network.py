@@ -532,7 +532,10 @@ class ProjectionNetwork(nn.Module):
         blocks' parameters)."""
         plan = self._edge_plan(side_no)
         if plan["parts"]:
-            w = torch.cat([block.edge_values(flat) for block, flat in plan["parts"]])[plan["order"]]
+            # index_select, not advanced indexing: the indices are distinct, and its
+            # backward scatters without the sort an index_put with accumulation makes
+            w = torch.cat([block.edge_values(flat) for block, flat in plan["parts"]])
+            w = w.index_select(0, plan["order"])
         else:
             w = torch.zeros(0, **self._float)
         return Connectome(self.n_neurons, self.n_neurons, plan["indptr"], plan["targets"], w,

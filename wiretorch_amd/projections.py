@@ -128,7 +128,10 @@ class FullRankProjection(Projection):
         return self.mask
 
     def edge_values(self, flat: torch.Tensor) -> torch.Tensor:
-        return torch.exp(self.log_weights.reshape(-1)[flat]) * self.mask.reshape(-1)[flat]
+        # (index_select: ``flat`` holds distinct positions, and the gradient is then
+        # scattered without sorting them)
+        return (torch.exp(self.log_weights.reshape(-1).index_select(0, flat))
+                * self.mask.reshape(-1).index_select(0, flat))
 
 
 class LowRankProjection(Projection):
@@ -192,7 +195,8 @@ class SignedProjection(Projection):
         return self.mask
 
     def edge_values(self, flat: torch.Tensor) -> torch.Tensor:
-        return self.weights.reshape(-1)[flat] * self.mask.reshape(-1)[flat]
+        return (self.weights.reshape(-1).index_select(0, flat)
+                * self.mask.reshape(-1).index_select(0, flat))
 
 
 def _members(types: np.ndarray, names: list[str]) -> dict[str, np.ndarray]:
