@@ -129,8 +129,12 @@ def _input_activations(L, x) -> torch.Tensor | None:
         xr = _columns(x.detach(), rows).reshape(B * T, -1).float()
         Wr = W.detach().float()
         if L.op.dtype != torch.float32:
+            # operands rounded to the storage type: their products are exact on the bf16
+            # matrix cores (x^T transposed once so that the product is the kernel's a^T b)
             xr, Wr = xr.to(L.op.dtype).float(), Wr.to(L.op.dtype).float()
-        torch.matmul(xr, Wr, out=A[j].view(B * T, N))
+            _gemm_tn(xr.t().contiguous(), Wr, out=A[j].view(B * T, N))
+        else:  # the reference's float32 product
+            torch.matmul(xr, Wr, out=A[j].view(B * T, N))
     return A
 
 
@@ -303,11 +307,13 @@ def _split(x: torch.Tensor):
     return hi, lo
 
 
-def _gemm_tn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+def _gemm_tn(a: torch.Tensor, b: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """``a^T b`` of float32 ``(K, M)`` and ``(K, N)`` matrices on the bf16 matrix cores
     (``wt_gemm_tn_split``): each operand split in registers into bf16 hi + lo, the product
     hi.hi + hi.lo + lo.hi accumulated in float32 — every term within 3 * 2^-18 of its
-    float32 value (float32's product: 2^-24), before the float32 accumulation both share."""
+    float32 value (float32's product: 2^-24), before the float32 accumulation both share;
+    exact products where both operands are bfloat16 values (lo = 0). ``out``: a
+    contiguous float32 ``(M, N)`` to write."""
     a, b = a.float(), b.float()
     if a.stride(1) != 1:
         a = a.contiguous()
@@ -315,7 +321,9 @@ def _gemm_tn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
         b = b.contiguous()
     K, M = a.shape
     N = b.shape[1]
-    C = torch.empty((M, N), dtype=torch.float32, device=a.device)
+    C = torch.empty((M, N), dtype=torch.float32, device=a.device) if out is None else out
+    if C.shape != (M, N) or C.dtype != torch.float32 or not C.is_contiguous():
+        raise ValueError("out: a contiguous float32 (M, N) tensor expected")
     _lib.check(_lib.load().wt_gemm_tn_split(
         a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), C.data_ptr(), N, K, M, N, 0,
         torch.cuda.current_stream(a.device).cuda_stream), "wt_gemm_tn_split")
