@@ -13,6 +13,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/wiretorch_amd.h"
+
 namespace wt {
 
 // A short row summed the way torch's CPU reduction associates it (checked against
@@ -50,6 +52,25 @@ struct Synapses {
   float mg_a[S], mg_lc[S];
   bool mg;
 };
+
+template <int S>
+__device__ inline void load_synapses(const wt_tables& tab, Synapses<S>& syn) {
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    syn.E[s] = tab.E_syn[s];
+    syn.clip[s] = tab.g_clip[s];
+    syn.decay_r[s] = tab.decay[s];
+    syn.decay_d[s] = tab.decay[S + s];
+    syn.jump_r[s] = tab.jump[s];
+    syn.jump_d[s] = tab.jump[S + s];
+  }
+  syn.mg = tab.mg_a != nullptr;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    syn.mg_a[s] = syn.mg ? tab.mg_a[s] : 0.0f;
+    syn.mg_lc[s] = syn.mg ? tab.mg_lc[s] : 0.0f;
+  }
+}
 
 // The Mg block at v (conductance/dynamics.py:110-113): 1 / (1 + exp(-(mg_a v - mg_lc))),
 // the product and the difference rounded as torch rounds them.

@@ -140,25 +140,6 @@ __device__ inline bool barrier_wait(uint32_t* counter, uint32_t target, uint32_t
   return *s_flag == 0;
 }
 
-template <int S>
-__device__ inline void load_synapses(const wt_tables& tab, Synapses<S>& syn) {
-#pragma unroll
-  for (int s = 0; s < S; ++s) {
-    syn.E[s] = tab.E_syn[s];
-    syn.clip[s] = tab.g_clip[s];
-    syn.decay_r[s] = tab.decay[s];
-    syn.decay_d[s] = tab.decay[S + s];
-    syn.jump_r[s] = tab.jump[s];
-    syn.jump_d[s] = tab.jump[S + s];
-  }
-  syn.mg = tab.mg_a != nullptr;
-#pragma unroll
-  for (int s = 0; s < S; ++s) {
-    syn.mg_a[s] = syn.mg ? tab.mg_a[s] : 0.0f;
-    syn.mg_lc[s] = syn.mg ? tab.mg_lc[s] : 0.0f;
-  }
-}
-
 // Exact accumulation of activations. Each product is rounded to a multiple of 2^-f and
 // added in float64: the host keeps every accumulator below 2^(53-f) in magnitude, so
 // every partial sum is exact, the order of the atomic adds does not matter, and the
