@@ -901,6 +901,15 @@ class _Run(torch.autograd.Function):
         )  # fmt: skip
         tab = L.abi_tables(scale.detach().float().contiguous())
         lib = _lib.load()
+        # the weight gradients' event lists are counted first: the host waits for their
+        # totals while the backward kernel runs
+        rec_counted = ff_counted = activity = None
+        if any(w_needs[:n_rec_w]):
+            rec_counted = _count_events(spikes, L.stream)
+        if any(w_needs[n_rec_w:]):
+            activity = (L.poisson.materialize(L.stream) if L.poisson is not None
+                        else x.detach().float())
+            ff_counted = _count_events(activity, L.stream)
         if L.recurrent_gradients:  # through the recurrent spikes: per-step coupling
             groups, R, range_n = L.geo
             rec_w = _sparse_weights(L, weights, n_rec_w)[0]
@@ -918,14 +927,14 @@ class _Run(torch.autograd.Function):
         grad_phys = [t.sum(d) if t is not None else None for t, d in zip(phys, dims)]
         grad_w = [None] * len(weights)
         with _timed("weight_gradient"):
-            if any(w_needs[:n_rec_w]):
+            if rec_counted is not None:
                 grad_w[:n_rec_w] = _weight_grads(L, L.rec, spikes, grad_A, 0,
-                                                 weights[:n_rec_w], w_needs[:n_rec_w])
-            if any(w_needs[n_rec_w:]):
-                activity = (L.poisson.materialize(L.stream) if L.poisson is not None
-                            else x.detach().float())
+                                                 weights[:n_rec_w], w_needs[:n_rec_w],
+                                                 rec_counted)
+            if ff_counted is not None:
                 grad_w[n_rec_w:] = _weight_grads(L, L.ff, activity, grad_A, L.K_rec,
-                                                 weights[n_rec_w:], w_needs[n_rec_w:])
+                                                 weights[n_rec_w:], w_needs[n_rec_w:],
+                                                 ff_counted)
         grad_x = _input_grad(L, x, grad_A, weights[n_rec_w:]) if want_x else None
         return (None, None, grad_scale, grad_x, None, None, None, None, *grad_w, *grad_phys)
 
@@ -955,10 +964,10 @@ def _sparse_weights(L: _Plan, weights, n_rec_w):
     return rec, ff
 
 
-def _events(activity: torch.Tensor, stream):
-    """Per source, its (trial*T + step) events ascending and their values:
-    ``(indptr, bt, value)`` from ``activity`` ``(B, T, n_src)`` (``wt_events_count`` /
-    ``wt_events_fill``; the host reads the number of events to size the lists)."""
+def _count_events(activity: torch.Tensor, stream):
+    """The first half of ``_events``: the per-source counts (``wt_events_count``) and
+    their total, copied to pinned host memory behind an event — so that the host can
+    queue more work (the backward kernel) before it waits for the total."""
     B, T, n = activity.shape
     BT = B * T
     flat = activity.reshape(BT, n).float().contiguous()
@@ -969,7 +978,24 @@ def _events(activity: torch.Tensor, stream):
     indptr = torch.empty(n + 1, dtype=torch.int64, device=dev)
     _lib.check(lib.wt_events_count(flat.data_ptr(), BT, n, scratch.data_ptr(),
                                    indptr.data_ptr(), stream), "wt_events_count")
-    total = int(indptr[-1])
+    total = torch.empty(1, dtype=torch.int64, pin_memory=True)
+    total.copy_(indptr[n:], non_blocking=True)
+    counted = torch.cuda.Event()
+    counted.record(torch.cuda.current_stream(dev))
+    return flat, scratch, indptr, total, counted
+
+
+def _events(activity: torch.Tensor, stream, counted=None):
+    """Per source, its (trial*T + step) events ascending and their values:
+    ``(indptr, bt, value)`` from ``activity`` ``(B, T, n_src)`` (``wt_events_count`` /
+    ``wt_events_fill``; the host reads the number of events to size the lists).
+    ``counted``: what ``_count_events`` returned for this activity, if it ran already."""
+    flat, scratch, indptr, total, done = counted or _count_events(activity, stream)
+    BT, n = flat.shape
+    dev = activity.device
+    lib = _lib.load()
+    done.synchronize()
+    total = int(total[0])
     bt = torch.empty(total, dtype=torch.int64, device=dev)
     value = torch.empty(total, dtype=torch.float32, device=dev)
     if total:
@@ -979,11 +1005,11 @@ def _events(activity: torch.Tensor, stream):
     return indptr, bt, value
 
 
-def _weight_grads(L: _Plan, side: _Side, activity, grad_A, k0, weights, needs):
+def _weight_grads(L: _Plan, side: _Side, activity, grad_A, k0, weights, needs, counted=None):
     """Gradients of a side's weight tensors from the event-driven support gradient:
     ``wt_weight_gradient_by_target`` over dL/da transposed to (pathway, target) rows."""
     c = side.conn
-    indptr, bt, value = _events(activity, L.stream)
+    indptr, bt, value = _events(activity, L.stream, counted)
     grad_e = torch.zeros(c.n_edges, device=L.device)
     edge_src = side.edge_src(L.stream)
     n_path = int(c.n_pathways)
