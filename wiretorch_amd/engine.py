@@ -550,17 +550,37 @@ def _device_scalar(value, device) -> torch.Tensor:
                                                                    device=device))
 
 
-def _type_table(tables: dict, scale: torch.Tensor, device):
+def _classes(type_of: torch.Tensor):
+    """Each neuron's class numbered from 0 in order of value, and each class's first
+    neuron (computed once per class tensor)."""
+    _, inv = torch.unique(type_of, return_inverse=True)
+    n = int(inv.max()) + 1 if inv.numel() else 0
+    first = torch.full((n,), inv.numel(), dtype=torch.int64, device=inv.device)
+    first.scatter_reduce_(0, inv, torch.arange(inv.numel(), device=inv.device), "amin")
+    return inv, first
+
+
+def _type_table(tables: dict, scale: torch.Tensor, device, type_of=None):
     """The per-neuron values the forward reads — theta, U_reset, E_L, C_m, beta, n_ref
     and each pathway's kernel scale — as rows of distinct values and each neuron's row:
-    networks built from cell types have few, which the kernel keeps in LDS."""
+    networks built from cell types have few, which the kernel keeps in LDS. With
+    ``type_of`` (classes within which the rows are equal: ``Physiology.type_of``), one
+    row per class, taken from its first neuron; every neuron's row is compared with its
+    class's on the device and a difference reported as a launch error."""
     N = tables["theta"].shape[0]
     n_ref = (tables["n_ref"].float() if tables["n_ref"] is not None
              else torch.zeros(N, device=device))
     cols = [tables[n] for n in ("theta", "U_reset", "E_L", "C_m", "beta")] + [n_ref]
     rows = torch.cat([torch.stack(cols, dim=1), _f32(scale, device).T], dim=1)
-    types, type_of = torch.unique(rows, dim=0, return_inverse=True)
-    return types.contiguous(), type_of.to(torch.int32).contiguous()
+    if type_of is None:
+        types, type_of = torch.unique(rows, dim=0, return_inverse=True)
+        return types.contiguous(), type_of.to(torch.int32).contiguous()
+    cls = type_of.detach().to(device)
+    inv, first = _cached(("classes",) + _key(cls), (cls,), lambda: _classes(cls))
+    types = rows[first].contiguous()
+    differs = (rows != types[inv]).any().to(torch.int32) * TABLE_MISMATCH
+    _watch(differs.reshape(1))
+    return types, inv.to(torch.int32).contiguous()
 
 
 def _range_types(type_of: torch.Tensor, n_rows: int, range_n: int):
@@ -716,7 +736,7 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
     names = ("theta", "U_reset", "E_L", "C_m", "beta", "E_syn", "g_clip", "decay", "jump")
     sources = tuple(getattr(p, name) for name in names) + (
         drive.made, drive.scale, p.dt, p.surr_scale, p.n_ref, p.mg_c, p.mg_a, p.adapt,
-        p.adapt_decay, p.E_adapt)
+        p.adapt_decay, p.E_adapt, p.type_of)
 
     def make_tables():
         tables = {name: _f32(getattr(p, name), device) for name in names}
@@ -725,7 +745,8 @@ def _plan(v, x, drive: Drive, p: Physiology, probabilities, track, track_batch_i
         tables["surr"] = _f32(p.surr_scale, device)
         tables["n_ref"] = (None if p.n_ref is None
                            else p.n_ref.to(device=device, dtype=torch.int32).contiguous())
-        tables["types"], tables["type_of"] = _type_table(tables, drive.scale, device)
+        tables["types"], tables["type_of"] = _type_table(tables, drive.scale, device,
+                                                         p.type_of)
         if p.mg_c is not None:  # the Mg block: log(mg_c) taken by torch on the CPU, as
             # the reference's CPU path takes it (-inf for a type without a block)
             tables["mg_a"] = _f32(p.mg_a, device)
@@ -806,6 +827,9 @@ def _launch(L: _Plan, x, scale, v, g, counter, spikes, prob, saved, tracked,
 
 #: Error words of launches not yet checked: (event after the copy, pinned host word).
 _PENDING: list = []
+#: The error bit of a type table whose rows differ within a class (the kernels' error
+#: words use the low bits).
+TABLE_MISMATCH = 1 << 30
 
 
 def _watch(word: torch.Tensor) -> None:
@@ -820,9 +844,10 @@ def _watch(word: torch.Tensor) -> None:
 
 
 def check_errors(wait: bool = False) -> None:
-    """Raise if an earlier launch reported an error (a group barrier that timed out):
-    checks every launch whose error word has reached the host (with ``wait``, waits for
-    all of them)."""
+    """Raise if an earlier launch reported an error (a group barrier that timed out, or
+    per-neuron tables that differ within a class of ``Physiology.type_of``): checks every
+    launch whose error word has reached the host (with ``wait``, waits for all of
+    them)."""
     still = []
     failed = 0
     for done, host in _PENDING:
@@ -833,6 +858,10 @@ def check_errors(wait: bool = False) -> None:
             continue
         failed |= int(host[0])
     _PENDING[:] = still
+    if failed & TABLE_MISMATCH:
+        raise RuntimeError("Physiology.type_of: per-neuron tables or kernel scales differ "
+                           "within a class; that call's results used each class's first "
+                           "neuron's values")
     if failed:
         raise RuntimeError(f"wt_cond_run: a workgroup barrier timed out (flags {failed:#x})")
 

@@ -117,7 +117,12 @@ class Physiology:
     Per neuron ``(N,)``: ``theta``, ``U_reset``, ``E_L``, ``C_m``, ``beta``. Per synapse
     type ``(S,)``: ``E_syn``, ``g_clip``; ``decay`` and ``jump`` ``(2, S)`` (rise, decay
     component). ``dt`` and ``surr_scale`` are 0-d tensors; ``n_ref`` ``(N,)`` int32 or
-    None when no neuron has a refractory period.
+    None when no neuron has a refractory period. ``type_of`` ``(N,)`` (optional): each
+    neuron's class, such that every per-neuron table and every pathway's kernel scale is
+    equal within a class (a network's cell types) — the engine then takes one row per
+    class instead of searching the tables for distinct rows (a search whose size the
+    host must read), and checks the claim on the device, raising at the next call or
+    backward if it fails.
     """
 
     theta: torch.Tensor
@@ -139,6 +144,22 @@ class Physiology:
     adapt: torch.Tensor | None = None
     adapt_decay: torch.Tensor | None = None
     E_adapt: torch.Tensor | None = None
+    type_of: torch.Tensor | None = None
+
+
+class _TypeGather(torch.autograd.Function):
+    """``table[index]`` whose backward is ``grad @ onehot`` (``onehot[n, j]`` = 1 where
+    ``index[n] == j``): one product instead of an accumulation over repeated indices."""
+
+    @staticmethod
+    def forward(ctx, table, index, onehot):
+        ctx.save_for_backward(onehot)
+        return table[index]
+
+    @staticmethod
+    def backward(ctx, grad):
+        (onehot,) = ctx.saved_tensors
+        return grad.to(onehot.dtype) @ onehot, None, None
 
 
 @dataclass
@@ -782,13 +803,29 @@ class ConductanceNetwork(ProjectionNetwork):
         if name in LEARNABLE_SYNAPSE:
             value = self.synapse_parameters.value(name)
         else:
-            value = self.cell_parameters.value(name)[self.cell_type_indices]
+            value = self._per_type(self.cell_parameters.value(name))
         if decay:
             value = torch.exp(-self.dt / value)
         return torch.where(mask, value, fixed)
 
     def _learns(self, *names: str) -> bool:
         return any(hasattr(self, f"_learnt_{n}") for n in names)
+
+    def _per_type(self, table: torch.Tensor) -> torch.Tensor:
+        """``table[cell_type_indices]``: each neuron's value of its type's entry. With
+        few types (at most 2^24 neuron-type pairs) the gradient is summed per type by one
+        matrix-vector product with the neurons' one-hot type matrix (cached), where
+        advanced indexing's backward adds the many repeats of one type index one after
+        another."""
+        idx = self.cell_type_indices
+        n_types = int(table.shape[0])
+        if idx.numel() * n_types > 1 << 24:
+            return table[idx]
+        key = (idx.data_ptr(), idx._version, n_types, table.dtype)
+        if getattr(self, "_onehot_key", None) != key:
+            self._onehot = nn.functional.one_hot(idx, n_types).to(table.dtype)
+            self._onehot_key = key
+        return _TypeGather.apply(table, idx, self._onehot)
 
     def _set_timestep(self) -> None:
         self.register_buffer("tau_syn", torch.stack((self.tau_rise, self.tau_decay)))
@@ -829,6 +866,7 @@ class ConductanceNetwork(ProjectionNetwork):
             spike_mode=self.spike_mode,
             storage_dtype=self.storage_dtype,
             n_ref=self.n_ref if self._refractory else None,
+            type_of=self.cell_type_indices,
             mg_c=self.mg_c if self._mg_block else None,
             mg_a=self.mg_a if self._mg_block else None,
             **(dict(adapt=learnt("adapt", self.adapt),
