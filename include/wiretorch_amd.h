@@ -376,24 +376,26 @@ int wt_edge_sources(const int64_t* indptr, int64_t n_src, int64_t* edge_src,
  * lists the weight gradients take. Replaces the torch nonzero / argsort / bincount that
  * form them around the reference's weight_gradient (network_simulators/engine.py:327-350).
  * count writes indptr (n+1) int64 (indptr[n] = number of events) and fills scratch
- * (wt_events_scratch_bytes); fill, with the same scratch, writes bt (indptr[n]) int64 and
- * value (indptr[n]) f32. Deterministic. BT may have at most 65535 * 256 rows. */
+ * (wt_events_scratch_bytes); fill, with the same scratch, writes bt (indptr[n]) int32 and,
+ * unless value is NULL (activity known to be 0 or 1: spikes), value (indptr[n]) f32.
+ * Deterministic. BT may have at most 65535 * 256 rows. */
 int64_t wt_events_scratch_bytes(int64_t BT, int64_t n);
 int wt_events_count(const float* activity, int64_t BT, int64_t n, void* scratch,
                     int64_t* indptr, wt_stream_t stream);
 int wt_events_fill(const float* activity, int64_t BT, int64_t n, const void* scratch,
-                   const int64_t* indptr, int64_t* bt, float* value, wt_stream_t stream);
+                   const int64_t* indptr, int32_t* bt, float* value, wt_stream_t stream);
 
 /* wt_weight_gradient — dL/dW on the connectome's support (its edges), event-driven:
  * grad_w[e] = sum over the events i of src(e) of ev_val[i] * grad_A[k, ev_bt[i], tgt(e)]
  * with k = pathway_offset + pathway(src(e)). Events of source j are ev_indptr[j] ..
- * ev_indptr[j+1]-1; ev_bt = b*T + t ascending, ev_val the presynaptic activity there.
+ * ev_indptr[j+1]-1; ev_bt = b*T + t ascending (int32), ev_val the presynaptic activity
+ * there (NULL: 1 at every event, spikes).
  * Replaces: network_simulators/engine.py:327-350 weight_gradient (a dense GEMM over
  * every (source, target) pair, most of whose products are zero); the reference's
  * learnt projections multiply the gradient by a mask that is zero off the support
  * (projections.py:164, :216). grad_A (K,B,T,N); grad_w (E,) f32 overwritten. */
 int wt_weight_gradient(const wt_side* side, const int64_t* edge_src, int64_t n_edges,
-                       const int64_t* ev_indptr, const int64_t* ev_bt, const float* ev_val,
+                       const int64_t* ev_indptr, const int32_t* ev_bt, const float* ev_val,
                        const float* grad_A, int64_t B, int64_t T, int64_t N,
                        int64_t pathway_offset, float* grad_w, wt_stream_t stream);
 
@@ -425,7 +427,7 @@ int wt_filter_backward(const float* grad_smooth, float* grad_x, float a_rise, fl
 int wt_weight_gradient_by_target(const int64_t* edge_src, int64_t n_edges,
                                  const int64_t* in_indptr, const int64_t* in_edge,
                                  int64_t n_pathways, int64_t N, const int64_t* ev_indptr,
-                                 const int64_t* ev_bt, const float* ev_val,
+                                 const int32_t* ev_bt, const float* ev_val,
                                  const float* grad_A, int64_t BT, float* rows, float* grad_w,
                                  wt_stream_t stream);
 

@@ -119,9 +119,10 @@ __global__ void split_ranges_kernel(const int64_t* indptr, const int32_t* target
 // ---------------------------------------------------------------------------------
 // Weight gradient on the support: one thread per synapse; it walks its source's
 // events (the (trial, step) where the source was active, ascending) and sums the
-// target's dL/da of that step.
+// target's dL/da of that step, times the event's value (1 for every event without
+// ev_val: spikes).
 __global__ void weight_gradient_kernel(wt_side side, const int64_t* edge_src, int64_t E,
-                                       const int64_t* ev_indptr, const int64_t* ev_bt,
+                                       const int64_t* ev_indptr, const int32_t* ev_bt,
                                        const float* ev_val, const float* grad_A, int64_t BT,
                                        int64_t N, int64_t k0, float* grad_w) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -132,7 +133,8 @@ __global__ void weight_gradient_kernel(wt_side side, const int64_t* edge_src, in
   if (k >= 0) {
     const int64_t n = side.targets[e];
     const float* gA = grad_A + (k0 + k) * BT * N + n;
-    for (int64_t i = ev_indptr[j]; i < ev_indptr[j + 1]; ++i) sum += ev_val[i] * gA[ev_bt[i] * N];
+    for (int64_t i = ev_indptr[j]; i < ev_indptr[j + 1]; ++i)
+      sum += (ev_val ? ev_val[i] : 1.0f) * gA[(int64_t)ev_bt[i] * N];
   }
   grad_w[e] = sum;
 }
@@ -174,9 +176,12 @@ __device__ inline int64_t readlane64(int64_t v, int k) {
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
+// VALUES: each event's value multiplies its term (otherwise every value is 1: spikes,
+// and the value list is not read).
+template <bool VALUES>
 __global__ __launch_bounds__(kWgBlock) void weight_gradient_target_kernel(
     const int64_t* in_indptr, const int64_t* in_edge, const int64_t* edge_src,
-    const int64_t* ev_indptr, const int64_t* ev_bt, const float* ev_val,
+    const int64_t* ev_indptr, const int32_t* ev_bt, const float* ev_val,
     const float* grad_A_T, int64_t BT, float* grad_w) {
   extern __shared__ float row[];
   const int64_t kn = blockIdx.x;
@@ -241,14 +246,14 @@ __global__ __launch_bounds__(kWgBlock) void weight_gradient_target_kernel(
           float val[4];
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
-            bt[u] = ev_bt[i + 64 * u] - c0;
-            val[u] = ev_val[i + 64 * u];
+            bt[u] = (int64_t)ev_bt[i + 64 * u] - c0;
+            val[u] = VALUES ? ev_val[i + 64 * u] : 1.0f;
           }
           bool past = false;
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             if (bt[u] >= len) past = true;
-            if (!past) part += val[u] * row[bt[u]];
+            if (!past) part += VALUES ? val[u] * row[bt[u]] : row[bt[u]];
           }
           if (past) {  // this lane's later events are past the chunk too
             i = i1;
@@ -256,9 +261,9 @@ __global__ __launch_bounds__(kWgBlock) void weight_gradient_target_kernel(
           }
         }
         for (; i < i1; i += 64) {
-          const int64_t bt = ev_bt[i] - c0;
+          const int64_t bt = (int64_t)ev_bt[i] - c0;
           if (bt >= len) break;
-          part += ev_val[i] * row[bt];
+          part += VALUES ? ev_val[i] * row[bt] : row[bt];
         }
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off);
@@ -333,7 +338,7 @@ __global__ __launch_bounds__(kRunBlock) void events_indptr_kernel(const int64_t*
 
 __global__ void events_fill_kernel(const float* __restrict__ act, int64_t BT, int64_t n,
                                    const int32_t* __restrict__ chunk,
-                                   const int64_t* __restrict__ indptr, int64_t* __restrict__ bt,
+                                   const int64_t* __restrict__ indptr, int32_t* __restrict__ bt,
                                    float* __restrict__ value) {
   const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= n) return;
@@ -347,8 +352,8 @@ __global__ void events_fill_kernel(const float* __restrict__ act, int64_t BT, in
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       if (a[u] != 0.0f) {
-        bt[pos] = rb + u;
-        value[pos] = a[u];
+        bt[pos] = (int32_t)(rb + u);
+        if (value) value[pos] = a[u];
         ++pos;
       }
     }
@@ -711,7 +716,7 @@ extern "C" int64_t wt_events_scratch_bytes(int64_t BT, int64_t n) {
 
 extern "C" int wt_events_count(const float* activity, int64_t BT, int64_t n, void* scratch,
                                int64_t* indptr, wt_stream_t stream) {
-  if (!indptr || BT < 0 || n < 0) return hipErrorInvalidValue;
+  if (!indptr || BT < 0 || n < 0 || BT > INT32_MAX) return hipErrorInvalidValue;
   const int64_t n_chunks = (BT + kEvChunk - 1) / kEvChunk;
   if (n_chunks > 65535) return hipErrorInvalidValue;
   if (n > 0 && BT > 0 && (!activity || !scratch)) return hipErrorInvalidValue;
@@ -735,11 +740,11 @@ extern "C" int wt_events_count(const float* activity, int64_t BT, int64_t n, voi
 }
 
 extern "C" int wt_events_fill(const float* activity, int64_t BT, int64_t n, const void* scratch,
-                              const int64_t* indptr, int64_t* bt, float* value,
+                              const int64_t* indptr, int32_t* bt, float* value,
                               wt_stream_t stream) {
-  if (BT < 0 || n < 0) return hipErrorInvalidValue;
+  if (BT < 0 || n < 0 || BT > INT32_MAX) return hipErrorInvalidValue;
   if (BT == 0 || n == 0) return hipSuccess;
-  if (!activity || !scratch || !indptr || !bt || !value) return hipErrorInvalidValue;
+  if (!activity || !scratch || !indptr || !bt) return hipErrorInvalidValue;
   const int64_t n_chunks = (BT + kEvChunk - 1) / kEvChunk;
   if (n_chunks > 65535) return hipErrorInvalidValue;
   hipLaunchKernelGGL(events_fill_kernel,
@@ -750,13 +755,13 @@ extern "C" int wt_events_fill(const float* activity, int64_t BT, int64_t n, cons
 }
 
 extern "C" int wt_weight_gradient(const wt_side* side, const int64_t* edge_src, int64_t n_edges,
-                                  const int64_t* ev_indptr, const int64_t* ev_bt,
+                                  const int64_t* ev_indptr, const int32_t* ev_bt,
                                   const float* ev_val, const float* grad_A, int64_t B,
                                   int64_t T, int64_t N, int64_t pathway_offset, float* grad_w,
                                   wt_stream_t stream) {
   if (pathway_offset < 0 || n_edges < 0) return hipErrorInvalidValue;
   if (n_edges == 0) return hipSuccess;  // nothing to write (pointers of empty tensors may be null)
-  if (!side || !edge_src || !ev_indptr || !ev_bt || !ev_val || !grad_A || !grad_w)
+  if (!side || !edge_src || !ev_indptr || !ev_bt || !grad_A || !grad_w)
     return hipErrorInvalidValue;
   const int block = 256;
   hipLaunchKernelGGL(weight_gradient_kernel, dim3((unsigned)((n_edges + block - 1) / block)),
@@ -768,15 +773,16 @@ extern "C" int wt_weight_gradient(const wt_side* side, const int64_t* edge_src, 
 extern "C" int wt_weight_gradient_by_target(const int64_t* edge_src, int64_t n_edges,
                                             const int64_t* in_indptr, const int64_t* in_edge,
                                             int64_t n_pathways, int64_t N,
-                                            const int64_t* ev_indptr, const int64_t* ev_bt,
+                                            const int64_t* ev_indptr, const int32_t* ev_bt,
                                             const float* ev_val, const float* grad_A,
                                             int64_t BT, float* rows, float* grad_w,
                                             wt_stream_t stream) {
-  if (n_edges < 0 || n_pathways < 0 || N < 0 || BT < 0) return hipErrorInvalidValue;
+  if (n_edges < 0 || n_pathways < 0 || N < 0 || BT < 0 || BT > INT32_MAX)
+    return hipErrorInvalidValue;
   const int64_t n_rows = n_pathways * N;
   if (n_edges == 0 || n_rows == 0) return hipSuccess;
-  if (!edge_src || !in_indptr || !in_edge || !ev_indptr || !ev_bt || !ev_val || !grad_A ||
-      !rows || !grad_w || BT == 0)
+  if (!edge_src || !in_indptr || !in_edge || !ev_indptr || !ev_bt || !grad_A || !rows ||
+      !grad_w || BT == 0)
     return hipErrorInvalidValue;
   if (n_rows > 0x7fffffff || (N + 63) / 64 > 0x7fffffff || (BT + 63) / 64 > 65535 ||
       n_pathways > 65535)
@@ -786,13 +792,19 @@ extern "C" int wt_weight_gradient_by_target(const int64_t* edge_src, int64_t n_e
                           (unsigned)n_pathways),
                      dim3(256), 0, (hipStream_t)stream, grad_A, rows, BT, N);
   const int64_t chunk = BT < kWgChunk ? BT : kWgChunk;
-  const hipError_t e = hipFuncSetAttribute((const void*)weight_gradient_target_kernel,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+  const void* fn = ev_val ? (const void*)weight_gradient_target_kernel<true>
+                          : (const void*)weight_gradient_target_kernel<false>;
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                            (int)(chunk * sizeof(float)));
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(weight_gradient_target_kernel, dim3((unsigned)n_rows), dim3(kWgBlock),
-                     (size_t)chunk * sizeof(float), (hipStream_t)stream, in_indptr, in_edge,
-                     edge_src, ev_indptr, ev_bt, ev_val, rows, BT, grad_w);
+  if (ev_val)
+    hipLaunchKernelGGL(weight_gradient_target_kernel<true>, dim3((unsigned)n_rows),
+                       dim3(kWgBlock), (size_t)chunk * sizeof(float), (hipStream_t)stream,
+                       in_indptr, in_edge, edge_src, ev_indptr, ev_bt, ev_val, rows, BT, grad_w);
+  else
+    hipLaunchKernelGGL(weight_gradient_target_kernel<false>, dim3((unsigned)n_rows),
+                       dim3(kWgBlock), (size_t)chunk * sizeof(float), (hipStream_t)stream,
+                       in_indptr, in_edge, edge_src, ev_indptr, ev_bt, ev_val, rows, BT, grad_w);
   return hipGetLastError();
 }
 

@@ -959,11 +959,11 @@ class _Run(torch.autograd.Function):
             if rec_counted is not None:
                 grad_w[:n_rec_w] = _weight_grads(L, L.rec, spikes, grad_A, 0,
                                                  weights[:n_rec_w], w_needs[:n_rec_w],
-                                                 rec_counted)
+                                                 rec_counted, spikes=True)
             if ff_counted is not None:
                 grad_w[n_rec_w:] = _weight_grads(L, L.ff, activity, grad_A, L.K_rec,
                                                  weights[n_rec_w:], w_needs[n_rec_w:],
-                                                 ff_counted)
+                                                 ff_counted, spikes=L.poisson is not None)
         grad_x = _input_grad(L, x, grad_A, weights[n_rec_w:]) if want_x else None
         return (None, None, grad_scale, grad_x, None, None, None, None, *grad_w, *grad_phys)
 
@@ -1014,31 +1014,34 @@ def _count_events(activity: torch.Tensor, stream):
     return flat, scratch, indptr, total, counted
 
 
-def _events(activity: torch.Tensor, stream, counted=None):
-    """Per source, its (trial*T + step) events ascending and their values:
+def _events(activity: torch.Tensor, stream, counted=None, values=True):
+    """Per source, its (trial*T + step) events ascending (int32) and their values:
     ``(indptr, bt, value)`` from ``activity`` ``(B, T, n_src)`` (``wt_events_count`` /
     ``wt_events_fill``; the host reads the number of events to size the lists).
-    ``counted``: what ``_count_events`` returned for this activity, if it ran already."""
+    ``counted``: what ``_count_events`` returned for this activity, if it ran already;
+    without ``values`` (an activity of spikes, 0 or 1) ``value`` is None."""
     flat, scratch, indptr, total, done = counted or _count_events(activity, stream)
     BT, n = flat.shape
     dev = activity.device
     lib = _lib.load()
     done.synchronize()
     total = int(total[0])
-    bt = torch.empty(total, dtype=torch.int64, device=dev)
-    value = torch.empty(total, dtype=torch.float32, device=dev)
+    bt = torch.empty(total, dtype=torch.int32, device=dev)
+    value = torch.empty(total, dtype=torch.float32, device=dev) if values else None
     if total:
         _lib.check(lib.wt_events_fill(flat.data_ptr(), BT, n, scratch.data_ptr(),
-                                      indptr.data_ptr(), bt.data_ptr(), value.data_ptr(),
+                                      indptr.data_ptr(), bt.data_ptr(), _lib.ptr(value),
                                       stream), "wt_events_fill")
     return indptr, bt, value
 
 
-def _weight_grads(L: _Plan, side: _Side, activity, grad_A, k0, weights, needs, counted=None):
+def _weight_grads(L: _Plan, side: _Side, activity, grad_A, k0, weights, needs, counted=None,
+                  spikes=False):
     """Gradients of a side's weight tensors from the event-driven support gradient:
-    ``wt_weight_gradient_by_target`` over dL/da transposed to (pathway, target) rows."""
+    ``wt_weight_gradient_by_target`` over dL/da transposed to (pathway, target) rows.
+    ``spikes``: the activity is 0 or 1 (its events carry no values)."""
     c = side.conn
-    indptr, bt, value = _events(activity, L.stream, counted)
+    indptr, bt, value = _events(activity, L.stream, counted, values=not spikes)
     grad_e = torch.zeros(c.n_edges, device=L.device)
     edge_src = side.edge_src(L.stream)
     n_path = int(c.n_pathways)
@@ -1050,7 +1053,7 @@ def _weight_grads(L: _Plan, side: _Side, activity, grad_A, k0, weights, needs, c
         _lib.check(
             _lib.load().wt_weight_gradient_by_target(
                 edge_src.data_ptr(), c.n_edges, in_indptr.data_ptr(), in_edge.data_ptr(),
-                n_path, L.N, indptr.data_ptr(), bt.data_ptr(), value.data_ptr(),
+                n_path, L.N, indptr.data_ptr(), bt.data_ptr(), _lib.ptr(value),
                 gA.data_ptr(), BT, rows.data_ptr(), grad_e.data_ptr(), L.stream),
             "wt_weight_gradient_by_target",
         )  # fmt: skip
