@@ -564,19 +564,24 @@ def _type_table(tables: dict, scale: torch.Tensor, device, type_of=None):
     """The per-neuron values the forward reads — theta, U_reset, E_L, C_m, beta, n_ref
     and each pathway's kernel scale — as rows of distinct values and each neuron's row:
     networks built from cell types have few, which the kernel keeps in LDS. With
-    ``type_of`` (classes within which the rows are equal: ``Physiology.type_of``), one
-    row per class, taken from its first neuron; every neuron's row is compared with its
-    class's on the device and a difference reported as a launch error."""
+    ``type_of`` (classes within which the rows are equal: ``Physiology.type_of``) of at
+    most ``MAX_TYPES`` classes, one row per class, taken from its first neuron; every
+    neuron's row is compared with its class's on the device and a difference reported as
+    a launch error. (More classes than one table holds are searched for their distinct
+    rows as without ``type_of``: classes often share a row.)"""
     N = tables["theta"].shape[0]
     n_ref = (tables["n_ref"].float() if tables["n_ref"] is not None
              else torch.zeros(N, device=device))
     cols = [tables[n] for n in ("theta", "U_reset", "E_L", "C_m", "beta")] + [n_ref]
     rows = torch.cat([torch.stack(cols, dim=1), _f32(scale, device).T], dim=1)
+    if type_of is not None:
+        cls = type_of.detach().to(device)
+        inv, first = _cached(("classes",) + _key(cls), (cls,), lambda: _classes(cls))
+        if first.numel() > MAX_TYPES:  # more classes than one table: search (fewer rows)
+            type_of = None
     if type_of is None:
         types, type_of = torch.unique(rows, dim=0, return_inverse=True)
         return types.contiguous(), type_of.to(torch.int32).contiguous()
-    cls = type_of.detach().to(device)
-    inv, first = _cached(("classes",) + _key(cls), (cls,), lambda: _classes(cls))
     types = rows[first].contiguous()
     differs = (rows != types[inv]).any().to(torch.int32) * TABLE_MISMATCH
     _watch(differs.reshape(1))
