@@ -71,6 +71,31 @@ def er_events(wl, spikes, x):
                  + (x != 0).double().sum(dim=(0, 1)) @ out_ff)
 
 
+#: The phases of a forward step the in-kernel timer (``wt_cond_run_timed``) separates,
+#: in its order.
+PHASE_NAMES = ("loads", "listing", "lookups+update", "slowest wave", "publish+arrival",
+               "barrier", "appends", "scan+push")
+
+
+def phase_split(model, x, T):
+    """One more forward of ``model`` under the in-kernel phase timer: microseconds per
+    step of each phase (thread 0 of each workgroup, 100 MHz wall clock; averaged over the
+    workgroups). Printed to stderr and returned."""
+    engine.PHASE_TIMING = []
+    try:
+        with torch.no_grad():
+            model.reset_state()
+            model(x)
+        torch.cuda.synchronize()
+        ticks = engine.PHASE_TIMING[0].double().mean(dim=0).cpu().numpy()
+    finally:
+        engine.PHASE_TIMING = None
+    us = {n: float(v) / 100.0 / T for n, v in zip(PHASE_NAMES, ticks)}
+    print("# phases (us per step): " + ", ".join(f"{n} {v:.2f}" for n, v in us.items())
+          + f"; total {sum(us.values()):.2f}", file=sys.stderr, flush=True)
+    return us
+
+
 def _part_ms(events):
     return {k: float(np.mean([a.elapsed_time(b) for a, b in v])) for k, v in events.items()}
 
@@ -167,6 +192,7 @@ def bench_config1(args):
     rate_hz = float(spikes.mean()) / 0.1e-3
     print(f"# config{args.config}: kernel {parts['forward']:.3f} ms, wall {ms_per_step:.3f} ms/step, "
           f"rate {rate_hz:.2f} Hz", file=sys.stderr, flush=True)
+    extra = {"phases_us_per_step": phase_split(model, x, T)} if args.phases else {}
     cpu = _er_cpu_baseline(model, wl.x, args.cpu_steps, False) if args.cpu_steps > 0 else None
     _line(B * N * T / (ms_per_step / 1e3), ms_per_step, args, "f32",
           {"workload": ("config1: mid-size conductance-LIF forward" if args.config == 1 else
@@ -176,7 +202,7 @@ def bench_config1(args):
           {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
            "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "wt_cond_run",
            "kernel_ms": parts["forward"], "algorithmic_bytes_per_launch": bytes_per_launch},
-          cpu, synaptic_events_per_s=events / (ms_per_step / 1e3), mean_rate_hz=rate_hz)
+          cpu, synaptic_events_per_s=events / (ms_per_step / 1e3), mean_rate_hz=rate_hz, **extra)
 
 
 def bench_config3(args):
@@ -454,6 +480,9 @@ def main():
                     help="configuration 2 with its input drawn on the device")
     ap.add_argument("--filter", action="store_true",
                     help="measure the spike-train loss filter instead of a configuration")
+    ap.add_argument("--phases", action="store_true",
+                    help="configurations 0-2: one more forward under the in-kernel phase "
+                         "timer, its per-step split reported beside the line")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run one device-to-device copy of this many bytes (the "
                          "reference kernel for calibrating rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -573,6 +602,8 @@ def main():
         },
         "cpu_baseline": cpu,
     }
+    if args.phases:
+        line["phases_us_per_step"] = phase_split(model, x, T)
     print(json.dumps(line), flush=True)
 
 
