@@ -385,6 +385,20 @@ int wt_events_count(const float* activity, int64_t BT, int64_t n, void* scratch,
 int wt_events_fill(const float* activity, int64_t BT, int64_t n, const void* scratch,
                    const int64_t* indptr, int32_t* bt, float* value, wt_stream_t stream);
 
+/* wt_gate_scan — a feedforward pathway's presynaptic dynamics stepped through a chunk,
+ * replacing gate_scan (network_simulators/kernels.py:87-129; the step of
+ * network_simulators/network.py:186-223). x (B, T, n_in) f32 the chunk's input; the
+ * pathway's n source rows are input columns rows[0 .. n-1] (int64, each in [0, n_in));
+ * params (5,) f32: saturation c, gating decay d, release probability at rest U, decays
+ * d_D, d_F. gating (B, R) f32, updated in place: with stp_col >= 0 the release
+ * probabilities u (columns stp_col ..) and resources (stp_col + n ..), with sat_col >= 0
+ * the receptors' gating (sat_col ..); at least one of them. factors (B, T, n) f32: each
+ * step's factor f (the pathway's input is x f). Every operation rounded as torch rounds
+ * it on the CPU. */
+int wt_gate_scan(const float* x, int64_t B, int64_t T, int64_t n_in, const int64_t* rows,
+                 int64_t n, const float* params, float* gating, int64_t R, int64_t stp_col,
+                 int64_t sat_col, float* factors, wt_stream_t stream);
+
 /* wt_weight_gradient — dL/dW on the connectome's support (its edges), event-driven:
  * grad_w[e] = sum over the events i of src(e) of ev_val[i] * grad_A[k, ev_bt[i], tgt(e)]
  * with k = pathway_offset + pathway(src(e)). Events of source j are ev_indptr[j] ..

@@ -18,7 +18,11 @@ Modules:
   bit (``tests/test_nmda.py``); adaptation (``dynamics.py:116-143,200-202``) by the
   exact solution of the membrane with the adaptation conductance held over a step, the
   tracked adaptation against its recursion from the spikes, and the non-adapting network
-  bit for bit (``tests/test_adaptation.py``).
+  bit for bit (``tests/test_adaptation.py``); presynaptic dynamics of feedforward
+  pathways (``gate_step`` / ``gate_feedforward``, ``network_simulators/network.py:
+  186-250``) by short-term plasticity's factors against the event-by-event map of
+  Markram, Wang & Tsodyks (1998) and saturation against its recursion, both in float64
+  (``tests/test_gating.py``).
 * ``oracle.sparse`` — the compressed-connectome propagation used at fly scale, where
   the reference's dense per-pathway rows cannot be built. Pinned against the dense
   product on small networks (``tests/test_oracle_pinning.py``,

@@ -10,7 +10,10 @@ bit for bit (same torch CPU kernels, same association order):
 * ``mg_block`` — ``conductance/dynamics.py:110-113``;
 * ``membrane`` — ``conductance/dynamics.py:116-143`` (the Mg block and the adaptation
   conductance);
-* ``simulate`` — ``conductance/dynamics.py:146-237`` (adaptation; no gating);
+* ``simulate`` — ``conductance/dynamics.py:146-237`` (adaptation; presynaptic dynamics
+  on feedforward pathways, not on recurrent ones);
+* ``gate_step`` / ``gate_feedforward`` — ``network_simulators/network.py:186-250``
+  (short-term plasticity and receptor saturation of a feedforward pathway's inputs);
 * ``refractory_mask`` / ``held_at_reset`` / ``count_down`` —
   ``network_simulators/network.py:294-318``;
 * ``recurrent_activations`` — ``network_simulators/network.py:260-271``;
@@ -134,18 +137,76 @@ def recurrent_activations(drive, s):
     return [product(s[:, rows], W) for rows, W in drive.recurrent]
 
 
-def feedforward_activations(drive, x):
-    """``(K_ff, B, T, N)``."""
+def feedforward_activations(drive, x, factors=None):
+    """``(K_ff, B, T, N)``; a pathway with presynaptic dynamics takes its rows' input
+    times its ``factors`` (``network.py:143-157``)."""
     if drive.sparse_feedforward is not None:
+        if factors is not None:
+            raise NotImplementedError("presynaptic dynamics on a compressed side")
         B, T, n_in = x.shape
         A = _sparse.activations(drive.sparse_feedforward, x.reshape(B * T, n_in))
         return A.reshape(A.shape[0], B, T, -1)
     if SUMS == "float32":
-        return drive.feedforward_activations(x)
+        return drive.feedforward_activations(x, factors)
     B, T = x.shape[:2]
     if not drive.feedforward:
         return x.new_zeros((0, B, T, 0))
-    return torch.stack([product(x[:, :, rows], W) for rows, W in drive.feedforward])
+    factors = factors or [None] * len(drive.feedforward)
+    return torch.stack([product(x[:, :, rows] if f is None else x[:, :, rows] * f, W)
+                        for (rows, W), f in zip(drive.feedforward, factors)])
+
+
+def gate_step(state, s, gate):
+    """One step of a pathway's presynaptic variables ``state`` ``(B, width)`` given its
+    source rows' activity ``s`` ``(B, n)`` (``network_simulators/network.py:186-223``):
+    returns ``(f, state)``, ``s f`` being the pathway's input in place of ``s``.
+    Short-term plasticity (Markram, Wang & Tsodyks 1998): ``x <- 1 - (1 - x) d_D``,
+    ``u <- U + (u - U) d_F``, ``f = u x / U``, ``x <- x - s u x``, ``u <- u + s U (1 - u)``;
+    saturation: ``g <- g d``, ``f <- min(c f (1 - g), 1 - g)`` (``c (1 - g)`` without
+    STP), ``g <- min(g + s f, 1)``. Nothing carries a gradient."""
+    c, d, U, d_D, d_F = gate.params.unbind()
+    n = gate.n
+    s = s.detach()
+    f, parts = None, []
+    if gate.stp:
+        u, r = state[:, :n], state[:, n : 2 * n]
+        r = 1 - (1 - r) * d_D
+        u = U + (u - U) * d_F
+        release = u * r
+        f = release / U
+        r = r - s * release
+        u = u + s * U * (1 - u)
+        parts += [u, r]
+    if gate.saturates:
+        g = state[:, -n:] * d
+        closed = 1 - g
+        f = c * closed if f is None else torch.minimum(c * f * closed, closed)
+        parts.append(torch.clamp(g + s * f, max=1.0))
+    return f, torch.cat(parts, dim=1)
+
+
+def gate_feedforward(drive, x, gating):
+    """The factors ``(B, T, n_rows)`` of the feedforward pathways with presynaptic
+    dynamics (None for the others) over the chunk ``x``, and the gating state after it
+    (``network_simulators/network.py:226-250``): a step at a time."""
+    K_rec = len(drive.recurrent)
+    gates = [drive.gate(K_rec + k) for k in range(len(drive.feedforward))]
+    if not any(gates):
+        return None, gating
+    gating = gating.clone()
+    factors = []
+    x = x.detach()
+    for (rows, _), gate in zip(drive.feedforward, gates):
+        if gate is None:
+            factors.append(None)
+            continue
+        state, fs = gating[:, gate.columns], []
+        for t in range(x.shape[1]):
+            f, state = gate_step(state, x[:, t, rows], gate)
+            fs.append(f)
+        gating[:, gate.columns] = state
+        factors.append(torch.stack(fs, dim=1))
+    return factors, gating
 
 
 def fold(drive):
@@ -201,9 +262,10 @@ def simulate(
     """Simulate ``x.shape[1]`` steps from ``(v, g)``; returns a ``Run``."""
     from wiretorch_amd.network import Run
 
-    if gating is not None:
-        raise NotImplementedError("presynaptic gating is not restated")
-    A_ff = feedforward_activations(drive, x)
+    if any(drive.gate(k) is not None for k in range(len(drive.recurrent))):
+        raise NotImplementedError("presynaptic dynamics on recurrent pathways")
+    factors, gating = gate_feedforward(drive, x, gating)
+    A_ff = feedforward_activations(drive, x, factors)
     kernels = jumps(drive, p.jump)
     keep = (
         slice(None)
@@ -252,5 +314,6 @@ def simulate(
         probabilities=torch.stack(probs, dim=1) if probabilities else None,
         tracked={k: stack_steps(val) for k, val in tracked.items() if val} if track else None,
         refractory=refractory,
+        gating=gating,
         adaptation=g_a,
     )

@@ -128,6 +128,7 @@ SIGNATURES = {
     "wt_events_scratch_bytes": (I64, [I64, I64]),
     "wt_events_count": (ctypes.c_int, [P, I64, I64, P, P, P]),
     "wt_events_fill": (ctypes.c_int, [P, I64, I64, P, P, P, P, P]),
+    "wt_gate_scan": (ctypes.c_int, [P, I64, I64, I64, P, I64, P, P, I64, I64, I64, P, P]),
     "wt_weight_gradient": (ctypes.c_int, [ctypes.POINTER(Side), P, I64, P, P, P, P, I64,
                                           I64, I64, I64, P, P]),
     "wt_weight_gradient_by_target": (ctypes.c_int, [P, I64, P, P, I64, I64, P, P, P, P, I64,

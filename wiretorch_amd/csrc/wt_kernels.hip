@@ -360,6 +360,49 @@ __global__ void events_fill_kernel(const float* __restrict__ act, int64_t BT, in
   }
 }
 
+// ---- Presynaptic dynamics of a feedforward pathway (network_simulators/network.py:
+// 186-250): one thread per (trial, source row), the chunk's steps in order. Each
+// operation is rounded as torch rounds it on the CPU (-ffp-contract=off, left to right).
+__global__ void gate_scan_kernel(const float* __restrict__ x, int64_t B, int64_t T,
+                                 int64_t n_in, const int64_t* __restrict__ rows, int64_t n,
+                                 const float* __restrict__ params, float* __restrict__ gating,
+                                 int64_t R, int64_t stp_col, int64_t sat_col,
+                                 float* __restrict__ factors) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= B * n) return;
+  const int64_t b = idx / n, i = idx - b * n;
+  const int64_t row = rows[i];
+  float* base = gating + b * R;
+  const float c = params[0], d = params[1], U = params[2], d_D = params[3], d_F = params[4];
+  const bool stp = stp_col >= 0, sat = sat_col >= 0;
+  float u = stp ? base[stp_col + i] : 0.0f, r = stp ? base[stp_col + n + i] : 0.0f;
+  float g = sat ? base[sat_col + i] : 0.0f;
+  for (int64_t t = 0; t < T; ++t) {
+    const float s = x[(b * T + t) * n_in + row];
+    float f = 1.0f;
+    if (stp) {  // resources recover, facilitation relaxes; a spike releases u r
+      r = 1.0f - (1.0f - r) * d_D;
+      u = U + (u - U) * d_F;
+      const float release = u * r;
+      f = release / U;
+      r = r - s * release;
+      u = u + s * U * (1.0f - u);
+    }
+    if (sat) {  // the receptors' gating decays; a release opens c f of the closed
+      g = g * d;
+      const float closed = 1.0f - g;
+      f = stp ? fminf(c * f * closed, closed) : c * closed;
+      g = fminf(g + s * f, 1.0f);
+    }
+    factors[(b * T + t) * n + i] = f;
+  }
+  if (stp) {
+    base[stp_col + i] = u;
+    base[stp_col + n + i] = r;
+  }
+  if (sat) base[sat_col + i] = g;
+}
+
 }  // namespace wt
 
 // ===================================================================================
@@ -751,6 +794,23 @@ extern "C" int wt_events_fill(const float* activity, int64_t BT, int64_t n, cons
                      dim3((unsigned)((n + kEvBlock - 1) / kEvBlock), (unsigned)n_chunks),
                      dim3(kEvBlock), 0, (hipStream_t)stream, activity, BT, n,
                      static_cast<const int32_t*>(scratch), indptr, bt, value);
+  return hipGetLastError();
+}
+
+extern "C" int wt_gate_scan(const float* x, int64_t B, int64_t T, int64_t n_in,
+                            const int64_t* rows, int64_t n, const float* params,
+                            float* gating, int64_t R, int64_t stp_col, int64_t sat_col,
+                            float* factors, wt_stream_t stream) {
+  if (B < 0 || T < 0 || n_in < 0 || n < 0 || R < 0) return hipErrorInvalidValue;
+  if (stp_col < 0 && sat_col < 0) return hipErrorInvalidValue;  // no dynamics to step
+  if ((stp_col >= 0 && stp_col + 2 * n > R) || (sat_col >= 0 && sat_col + n > R))
+    return hipErrorInvalidValue;
+  if (B * n == 0 || T == 0) return hipSuccess;
+  if (!x || !rows || !params || !gating || !factors || n_in == 0) return hipErrorInvalidValue;
+  const int block = 256;
+  hipLaunchKernelGGL(gate_scan_kernel, dim3((unsigned)((B * n + block - 1) / block)),
+                     dim3(block), 0, (hipStream_t)stream, x, B, T, n_in, rows, n, params,
+                     gating, R, stp_col, sat_col, factors);
   return hipGetLastError();
 }
 

@@ -31,7 +31,7 @@ from __future__ import annotations
 
 import math
 from collections import OrderedDict
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 
 import torch
 
@@ -1107,8 +1107,18 @@ def simulate(
     check_errors()
     if retain is not None:
         raise NotImplementedError("per-step gradient retention (track_gradients)")
-    if gating is not None or drive.gates:
-        raise NotImplementedError("presynaptic dynamics")
+    gates = list(drive.gates or [])
+    if any(gate is not None for gate in gates[: drive.K_rec]):
+        raise NotImplementedError("presynaptic dynamics on recurrent pathways")
+    if any(gate is not None for gate in gates):
+        if gating is None:
+            raise ValueError("a drive with presynaptic dynamics needs the gating state")
+        x, drive, gating = _gate_inputs(drive, x, gating)
+        run = simulate(v, g, x, drive, p, refractory=refractory, adaptation=adaptation,
+                       probabilities=probabilities, track=track,
+                       track_batch_idx=track_batch_idx)
+        run.gating = gating
+        return run
     if p.spike_mode != "deterministic":
         raise NotImplementedError("sampled spikes")
     if p.storage_dtype != torch.float32:
@@ -1177,8 +1187,69 @@ def simulate(
         probabilities=prob,
         tracked=tracked,
         refractory=counter,
+        gating=gating,
         adaptation=adaptation if L.adapting else None,
     )
+
+
+def _gated_rows(rows_list, n_in: int, device):
+    """Each feedforward pathway's rows as a block of input columns of its own (pathway k:
+    columns off_k .. off_k + n_k - 1), after checking the rows against the input width
+    once per rows tensor (a host read)."""
+    out, off = [], 0
+    for rows in rows_list:
+        rows = rows.to(device).long()
+        if rows.numel() and (int(rows.min()) < 0 or int(rows.max()) >= n_in):
+            raise ValueError(f"feedforward rows outside the {n_in} input columns")
+        out.append((rows.contiguous(), torch.arange(off, off + rows.numel(), device=device)))
+        off += rows.numel()
+    return out
+
+
+def _gate_inputs(drive: Drive, x, gating):
+    """Feedforward pathways with presynaptic dynamics (``network.py:226-250``): their
+    factors stepped through the chunk on the device (``wt_gate_scan``), and every
+    feedforward pathway's rows' input — times its factors where it has them — as a block
+    of input columns of its own (pathways sharing source rows then take their own
+    factors). Returns that input, the drive with those blocks as its rows and no gates,
+    and the gating state after the chunk. The factors carry no gradient: dL/dx reaches
+    the input times them (``network_simulators/engine.py:99-111``)."""
+    if isinstance(x, PoissonInput) or drive.sparse_feedforward is not None:
+        raise NotImplementedError("presynaptic dynamics on a drawn input or a compressed "
+                                  "feedforward side")
+    dev = x.device
+    B, T, n_in = x.shape
+    rows_list = [rows for rows, _ in drive.feedforward]
+    blocks = _cached(("gated rows", n_in, str(dev)) + _key(*rows_list), tuple(rows_list),
+                     lambda: _gated_rows(rows_list, n_in, dev))
+    gating = gating.detach().to(device=dev, dtype=torch.float32).clone(
+        memory_format=torch.contiguous_format)
+    if gating.dim() != 2 or gating.shape[0] != B:
+        raise ValueError(f"gating state of shape {tuple(gating.shape)} for {B} trials")
+    R = gating.shape[1]
+    xs = x.detach().float().contiguous()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    lib = _lib.load()
+    cols, feedforward = [], []
+    for k, ((rows, W), (src, own)) in enumerate(zip(drive.feedforward, blocks)):
+        gate = drive.gate(drive.K_rec + k)
+        xr = x[:, :, src]
+        if gate is not None:
+            if gate.n != src.numel() or gate.start < 0 or gate.start + gate.width > R:
+                raise ValueError(f"feedforward pathway {k}: its gate does not match its "
+                                 f"{src.numel()} rows and the {R} gating columns")
+            f = torch.empty((B, T, gate.n), device=dev)
+            params = gate.params.detach().to(device=dev, dtype=torch.float32).contiguous()
+            stp_col = gate.start if gate.stp else -1
+            sat_col = gate.start + 2 * gate.n * gate.stp if gate.saturates else -1
+            _lib.check(lib.wt_gate_scan(xs.data_ptr(), B, T, n_in, src.data_ptr(), gate.n,
+                                        params.data_ptr(), gating.data_ptr(), R, stp_col,
+                                        sat_col, f.data_ptr(), stream), "wt_gate_scan")
+            xr = xr * f
+        cols.append(xr)
+        feedforward.append((own, W))
+    x = torch.cat(cols, dim=2) if cols else x[:, :, :0]
+    return x, replace(drive, feedforward=feedforward, gates=[]), gating
 
 
 def _last_tracked(spikes):

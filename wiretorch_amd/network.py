@@ -102,12 +102,45 @@ class Drive:
             return self.sparse_feedforward.n_pathways
         return len(self.feedforward)
 
-    def feedforward_activations(self, x: torch.Tensor) -> torch.Tensor:
-        """``(K_ff, B, T, N)``: each feedforward pathway's input times its weights."""
+    def gate(self, k: int) -> "Gate | None":
+        """Pathway ``k``'s presynaptic dynamics (recurrent pathways first), if any."""
+        return self.gates[k] if self.gates else None
+
+    def feedforward_activations(self, x: torch.Tensor, factors=None) -> torch.Tensor:
+        """``(K_ff, B, T, N)``: each feedforward pathway's input times its weights; a
+        pathway with presynaptic dynamics takes its input times its ``factors``
+        ``(B, T, n_rows)`` (``network.py:143-157``)."""
         B, T = x.shape[:2]
         if not self.feedforward:
             return x.new_zeros((0, B, T, 0))
-        return torch.stack([x[:, :, rows] @ W for rows, W in self.feedforward])
+        factors = factors or [None] * len(self.feedforward)
+        return torch.stack([(x[:, :, rows] if f is None else x[:, :, rows] * f) @ W
+                            for (rows, W), f in zip(self.feedforward, factors)])
+
+
+@dataclass(frozen=True)
+class Gate:
+    """A pathway's presynaptic dynamics over its ``n`` source rows
+    (``network_simulators/network.py:160-183``): ``params`` ``(5,)`` — the saturation
+    ``c`` and per-step decay ``d`` of the receptors' gating, the release probability at
+    rest ``U`` and the per-step decays ``d_D``, ``d_F`` of the resources' deficit and of
+    the facilitation; its columns of the gating state ``(B, R)`` from ``start``: with
+    ``stp`` the release probabilities ``u`` then the resources ``x`` (``n`` each), then,
+    if it ``saturates``, the receptors' gating ``g``."""
+
+    params: torch.Tensor
+    stp: bool
+    saturates: bool
+    start: int
+    n: int
+
+    @property
+    def width(self) -> int:
+        return self.n * (2 * self.stp + self.saturates)
+
+    @property
+    def columns(self) -> slice:
+        return slice(self.start, self.start + self.width)
 
 
 @dataclass
