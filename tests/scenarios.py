@@ -84,6 +84,28 @@ def adapting(cells, adapt, tau_adapt=200.0):
             for c in cells]
 
 
+def saturating(synapses, saturation):
+    """``synapses`` with the NMDA types saturating by ``saturation`` (unchanged if None;
+    reference ``tests/networks.py:120-127``)."""
+    if saturation is None:
+        return synapses
+    return [{**s, "saturation": saturation} if s["name"] == "NMDA" else s for s in synapses]
+
+
+def stp_pairs(sources, recurrent_names=("excitatory", "inhibitory")):
+    """Depressing onto excitatory cells, facilitating onto inhibitory ones, per source
+    type: a source type then has two STP sets, its rows shared by two pathways
+    (reference ``tests/networks.py:130-143``)."""
+    from wiretorch_amd.stp import DEPRESSING, FACILITATING
+
+    excitatory, inhibitory = recurrent_names
+    pairs = {}
+    for source in sources:
+        pairs[(source, excitatory)] = DEPRESSING
+        pairs[(source, inhibitory)] = FACILITATING
+    return pairs
+
+
 def combined_physiology():
     cells = [dict(c) for c in MITRAL_CELLS]
     cells += [{**c, "cell_id": c["cell_id"] + 1} for c in CELLS]
@@ -172,10 +194,12 @@ def _input_rng(seed, input_seed):
 
 def recurrent(batch_size, seed, scaling_factors=False, n=N, n_ff=N_FF, n_steps=200,
               input_seed=0, learn=None, learnt_weights=False, tau_ref=None,
-              recurrent_gradients=False, dt=DT, surrgrad_scale=5.0, mg=None, adapt=None):
+              recurrent_gradients=False, dt=DT, surrgrad_scale=5.0, mg=None, adapt=None,
+              saturation=None, stp=False):
     """``ConductanceLIFNetwork``: frozen weights, perturbed scaling factors, or learnt
     recurrent weights; ``mg`` mM of Mg block on the NMDA types, ``adapt`` the excitatory
-    cells' adaptation (reference ``tests/networks.py:276-355``)."""
+    cells' adaptation, ``saturation`` the NMDA types' and ``stp`` short-term plasticity
+    of the excitatory and input sources (reference ``tests/networks.py:276-355``)."""
     rng, types, w_rec, w_ff = _structure(seed, n, n_ff)
     ff_types = np.zeros(n_ff, dtype=np.int64)
     rec_blocks = per_type_blocks(w_rec, types, types, REC_NAMES, REC_NAMES)
@@ -192,9 +216,12 @@ def recurrent(batch_size, seed, scaling_factors=False, n=N, n_ff=N_FF, n_steps=2
         dt=dt, rec_projections=rec, ff_projections=ff,
         cell_type_indices=types, cell_type_indices_FF=ff_types,
         cell_params=adapting(with_refractory(CELLS, tau_ref), adapt), cell_params_FF=MITRAL_CELLS,
-        synapse_params=mg_block(SYNAPSES, mg), synapse_params_FF=mg_block(MITRAL_SYNAPSES, mg),
+        synapse_params=saturating(mg_block(SYNAPSES, mg), saturation),
+        synapse_params_FF=saturating(mg_block(MITRAL_SYNAPSES, mg), saturation),
         surrgrad_scale=surrgrad_scale, batch_size=batch_size, learn=learn,
         recurrent_gradients=recurrent_gradients,
+        rec_stp=stp_pairs(["excitatory"]) if stp else None,
+        ff_stp=stp_pairs(["mitral"]) if stp else None,
     )  # fmt: skip
     sfs = (
         move_scaling_factors(rng, [*rec.values(), *ff.values()])
@@ -208,12 +235,12 @@ def recurrent(batch_size, seed, scaling_factors=False, n=N, n_ff=N_FF, n_steps=2
 
 def feedforward(batch_size, seed, learnt_weights=False, probabilities=False, n=N,
                 n_ff=N_FF, n_steps=200, input_seed=0, learn=None, tau_ref=None, mg=None,
-                adapt=None):
+                adapt=None, stp=False, saturation=None):
     """``FeedforwardConductanceLIFNetwork`` on external inputs and a recurrent network's
     neurons; ``mg`` as for ``recurrent`` (reference ``tests/networks.py:358-429``)."""
     rng, types, w_rec, w_ff = _structure(seed, n, n_ff)
     cells, synapses = combined_physiology()
-    synapses = mg_block(synapses, mg)
+    synapses = saturating(mg_block(synapses, mg), saturation)
     names = [c["name"] for c in cells]
     row_types = np.concatenate([np.zeros(n_ff, dtype=np.int64), types + 1])
     weights = np.concatenate([w_ff, w_rec])
@@ -239,6 +266,7 @@ def feedforward(batch_size, seed, learnt_weights=False, probabilities=False, n=N
         cell_type_indices_FF=row_types, cell_params=adapting(with_refractory(CELLS, tau_ref), adapt),
         cell_params_FF=cells, synapse_params_FF=synapses, surrgrad_scale=5.0,
         batch_size=batch_size, return_probabilities=probabilities, learn=learn,
+        stp=stp_pairs(["mitral"]) if stp else None,
     )  # fmt: skip
     scaled = [p for p in projections.values() if isinstance(p, ScalingFactorProjection)]
     drawn["sf"] = move_scaling_factors(rng, scaled)

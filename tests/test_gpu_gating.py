@@ -142,3 +142,17 @@ def test_recurrent_presynaptic_dynamics_raise():
     ff_only = replace(drive, gates=[None] * drive.K_rec + [gate] * drive.K_ff)
     with pytest.raises(ValueError, match="gating state"):
         engine.simulate(model.v, model._synaptic, x, ff_only, model._physiology())
+
+
+def test_network_with_presynaptic_dynamics_matches_oracle():
+    """Through the network API (reference ``tests/test_stp.py:302-312``,
+    ``tests/test_saturation.py:332-347``): a feed-forward network whose input sources
+    have depressing and facilitating STP onto different targets and saturating NMDA
+    synapses, every physiology parameter learnt but the saturating types' tau_decay,
+    spike probabilities in the loss — the oracle's spikes, voltages and gradients
+    (``test_gpu_nmda._engine_vs_oracle``)."""
+    from test_gpu_nmda import LEARN, _engine_vs_oracle
+
+    learn = {**LEARN, "tau_decay": ["AMPA", "GABA_A"]}
+    _engine_vs_oracle(lambda: sc.feedforward(sc.BATCH_SIZE, sc.SEED, probabilities=True,
+                                             learn=learn, stp=True, saturation=0.63))

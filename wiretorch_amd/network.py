@@ -43,6 +43,7 @@ from torch import nn
 
 from wiretorch_amd.connectome import Connectome
 from wiretorch_amd.projections import Projection, SparseProjection, projection_mask
+from wiretorch_amd.stp import as_stp
 from wiretorch_amd.synapses import SynapseRegistry, mg_block_tables
 from wiretorch_amd.type_parameters import (
     TypeParameters,
@@ -218,12 +219,15 @@ class Run:
         return self.syn
 
 
-def conductance_kernel(tau_rise, tau_decay, g_bar) -> torch.Tensor:
+def conductance_kernel(tau_rise, tau_decay, g_bar, saturating=None) -> torch.Tensor:
     """``(2, S)`` jump of the rise and decay components per unit input: ``-g_bar`` and
     ``+g_bar`` over the peak of the difference of exponentials, so the waveform peaks at
-    ``g_bar`` (``conductance/synapses.py:70-87``)."""
+    ``g_bar`` — unnormalised for the ``saturating`` types, whose input is the fraction of
+    receptors opened (``g_bar``: every receptor open) (``conductance/synapses.py:70-87``)."""
     r = tau_rise / tau_decay
     peak = r ** (r / (1 - r)) - r ** (1 / (1 - r))
+    if saturating is not None:
+        peak = torch.where(saturating, torch.ones_like(peak), peak)
     return torch.stack([-g_bar, g_bar], dim=0) / peak
 
 
@@ -238,16 +242,34 @@ class InputSide:
     recurrent: bool
     attribute: str
     mask_buffer: str
+    stp: dict | None = None  # (source name, target name) -> STP (or a dict of its fields)
 
 
 @dataclass(frozen=True)
 class Pathway:
-    """One source cell type on one input side."""
+    """One source cell type on one input side (``network.py:80-102``). A source type
+    with presynaptic dynamics has several: one per (saturating synapse type ``gate``, or
+    the rest) and per group of target types sharing one ``stp`` (``targets``: the target
+    cell types it reaches, None for all), all over the rows and weights of pathway
+    ``source``."""
 
     index: int
     side: int
     cell_type: int
     mode: str
+    gate: int | None = None
+    stp: object | None = None
+    targets: tuple | None = None
+    source: int = -1
+
+    @property
+    def presynaptic(self) -> bool:
+        return self.gate is not None or self.stp is not None
+
+    @property
+    def owner(self) -> int:
+        """The pathway whose rows and weights this one shares (itself if none)."""
+        return self.source if self.source >= 0 else self.index
 
 
 def _long(values) -> torch.Tensor:
@@ -292,15 +314,6 @@ def validate(dt, cell_params, cell_type_indices, sides) -> None:
 def is_sparse(side: InputSide) -> bool:
     """Whether a side is one ``SparseProjection`` (rather than per-type-pair blocks)."""
     return isinstance(side.projections, SparseProjection)
-
-
-def _unsupported(cell_params, synapse_lists, stp) -> None:
-    for synapses in synapse_lists:
-        for syn in synapses:
-            if syn.get("saturation", 0.0):
-                raise NotImplementedError("saturating synapses are not supported")
-    if any(stp):
-        raise NotImplementedError("short-term plasticity is not supported")
 
 
 # =====================================================================
@@ -411,13 +424,35 @@ class ProjectionNetwork(nn.Module):
             lookup[cell["cell_id"]] = cell[name] if default is None else cell.get(name, default)
         return torch.from_numpy(lookup[self.cell_type_indices.cpu().numpy()])
 
+    def _saturation(self) -> torch.Tensor:
+        """``(S,)``: each synapse type's saturation (0: none)."""
+        return torch.zeros(len(self.registry))
+
     def _build_pathways(self) -> list[Pathway]:
+        """Pathways by side and source cell type (``network.py:640-729``); a source type
+        that makes saturating synapse types or has short-term plasticity gets one per
+        (saturating type, or the rest) x (target types sharing one STP), sharing its rows
+        and weights. Presynaptic dynamics are taken on feedforward sides of per-type-pair
+        blocks only."""
+        saturating = self._saturation() > 0
         pathways, made = [], []
         for side_no, side in enumerate(self._sides):
+            side_makes = self.registry.made_by(side_no, side.synapse_params).values()
+            presynaptic = bool(side.stp) or any(bool((m & saturating).any()) for m in side_makes)
+            if presynaptic and (side.recurrent or is_sparse(side)):
+                raise NotImplementedError(
+                    f"{side.attribute}: presynaptic dynamics (short-term plasticity, saturating "
+                    "synapse types) are supported on feedforward sides of per-type-pair "
+                    "projections only")
             if is_sparse(side):
                 self._sparse_pathways(side_no, side, pathways, made)
                 continue
             names = {c["cell_id"]: c["name"] for c in side.cell_params}
+            stp = {key: as_stp(value) for key, value in (side.stp or {}).items()}
+            unknown = set(stp) - set(side.projections)
+            if unknown:
+                raise ValueError(f"{side.attribute}: short-term plasticity for "
+                                 f"{sorted(unknown)}, which have no projection")
             modes: dict[str, str] = {}
             for (src, _), projection in side.projections.items():
                 mode = modes.setdefault(src, projection.caching_mode)
@@ -431,18 +466,76 @@ class ProjectionNetwork(nn.Module):
                 mode = modes.get(names[cell_type])
                 if mode is None:
                     continue
-                index = len(pathways)
+                source = len(pathways)
                 rows = np.flatnonzero(side.cell_type_indices == cell_type)
-                self.register_buffer(f"_rows_{index}", _long(rows), persistent=False)
-                pathways.append(Pathway(index, side_no, cell_type, mode))
-                made.append(synapses)
+                plain = synapses & ~saturating
+                parts = [(None, plain)] if bool(plain.any()) else []
+                for gate in torch.nonzero(synapses & saturating).flatten().tolist():
+                    one = torch.zeros_like(synapses)
+                    one[gate] = True
+                    parts.append((gate, one))
+                groups: dict = {}  # STP (or None) -> the target cell types it reaches
+                for target, target_name in sorted(self._names.items()):
+                    groups.setdefault(stp.get((names[cell_type], target_name)), []).append(target)
+                for plasticity, targets in groups.items():
+                    targets = None if len(groups) == 1 else tuple(targets)
+                    for gate, mask in parts:
+                        index = len(pathways)
+                        self.register_buffer(f"_rows_{index}", _long(rows), persistent=False)
+                        pathways.append(Pathway(index, side_no, cell_type, mode, gate, plasticity,
+                                                targets, -1 if index == source else source))
+                        made.append(mask)
+                        if targets is not None:
+                            reached = np.isin(self.cell_type_indices.cpu().numpy(), targets)
+                            self.register_buffer(f"_targets_{index}",
+                                                 torch.from_numpy(reached.astype(np.float32)),
+                                                 persistent=False)
         self.register_buffer(
             "_made",
             torch.stack(made) if made else torch.zeros((0, len(self.registry)), dtype=torch.bool),
             persistent=False,
         )
         # Recurrent pathways first: the order the dynamics inject them in.
-        return sorted(pathways, key=lambda p: not self._sides[p.side].recurrent)
+        pathways = sorted(pathways, key=lambda p: not self._sides[p.side].recurrent)
+        # The gating state's columns: each presynaptic pathway's (see ``Gate``), in order,
+        # and their values at rest (u = U, x = 1, g = 0).
+        columns, rest = {}, []
+        for p in pathways:
+            if p.presynaptic:
+                n = getattr(self, f"_rows_{p.index}").numel()
+                columns[p.index] = (int(sum(map(len, rest))), int(n))
+                if p.stp is not None:
+                    rest += [np.full(n, p.stp.U), np.ones(n)]
+                if p.gate is not None:
+                    rest.append(np.zeros(n))
+        self._gate_columns = columns
+        self.register_buffer("_gating_rest", torch.from_numpy(
+            np.concatenate(rest or [np.zeros(0)]).astype(np.float32)), persistent=False)
+        self.n_gating = int(self._gating_rest.numel())
+        return pathways
+
+    def _gate(self, pathway: Pathway) -> Gate | None:
+        """A presynaptic pathway's ``Gate`` (its parameters at this time step), else None."""
+        if not pathway.presynaptic:
+            return None
+        return Gate(getattr(self, f"_gate_{pathway.index}"), pathway.stp is not None,
+                    pathway.gate is not None, *self._gate_columns[pathway.index])
+
+    def _set_gates(self, saturation: torch.Tensor, gate_decay: torch.Tensor) -> None:
+        """Each presynaptic pathway's ``Gate.params`` at this time step, on the device: the
+        saturating type's saturation and gating decay, the STP's ``U`` and decays
+        (``network.py:855-874``)."""
+        dt = float(self.dt)
+        for p in self.pathways:
+            if not p.presynaptic:
+                continue
+            zero = torch.zeros((), device=self.device)
+            c, d = ((saturation[p.gate], gate_decay[p.gate]) if p.gate is not None
+                    else (zero, zero))
+            U, d_D, d_F = (p.stp.U, *p.stp.decays(dt)) if p.stp is not None else (1.0, 0.0, 0.0)
+            params = torch.cat([torch.stack([c, d]).float(),
+                                torch.tensor([U, d_D, d_F], device=self.device)])
+            self.register_buffer(f"_gate_{p.index}", params, persistent=False)
 
     def _sparse_pathways(self, side_no: int, side: InputSide, pathways, made) -> None:
         """A ``SparseProjection`` side's pathways: one per distinct set of synapse types
@@ -483,10 +576,13 @@ class ProjectionNetwork(nn.Module):
         return W
 
     def _cache_weights(self) -> None:
-        for pathway in self.pathways:
+        for pathway in sorted(self.pathways, key=lambda p: p.index):  # owners first
             if pathway.mode not in ("weights", "sparse"):
-                W = self._assemble(pathway, connectome=pathway.mode == "scaling_factors")
-                self.register_buffer(f"_weights_{pathway.index}", W.detach(), persistent=False)
+                if pathway.owner != pathway.index:  # the very tensor of its source pathway
+                    W = getattr(self, f"_weights_{pathway.owner}")
+                else:
+                    W = self._assemble(pathway, connectome=pathway.mode == "scaling_factors").detach()
+                self.register_buffer(f"_weights_{pathway.index}", W, persistent=False)
 
     def set_timestep(self, dt: float) -> None:
         """Set the time step, recompute what depends on it, reset the state."""
@@ -618,18 +714,22 @@ class ProjectionNetwork(nn.Module):
                 continue
             if pathway.mode != "weights":
                 W = getattr(self, f"_weights_{pathway.index}")
+            elif pathway.owner in assembled:  # the very tensor of its source pathway
+                W = assembled[pathway.owner]
             else:
-                W = assembled[pathway.index] = self._assemble(pathway)
+                W = assembled[pathway.owner] = self._assemble(pathway)
             if pathway.mode == "scaling_factors":
                 if pathway.side not in scaling:
                     scaling[pathway.side] = self._scaling_matrix(pathway.side)
                 scales.append(scaling[pathway.side][pathway.cell_type, self.cell_type_indices])
             else:
                 scales.append(ones)
+            if pathway.targets is not None:  # it reaches only these target types
+                scales[-1] = scales[-1] * getattr(self, f"_targets_{pathway.index}")
             rows = getattr(self, f"_rows_{pathway.index}")
             target = recurrent if self._sides[pathway.side].recurrent else feedforward
             target.append((rows, W))
-        if any(p.mode == "scaling_factors" for p in self.pathways):
+        if any(p.mode == "scaling_factors" or p.targets is not None for p in self.pathways):
             scale = torch.stack(scales)
         else:  # every kernel scale is 1: the same tensor each call
             scale = unit
@@ -640,6 +740,7 @@ class ProjectionNetwork(nn.Module):
             feedforward=feedforward,
             differentiable_inputs=self.differentiable_inputs,
             recurrent_gradients=self.recurrent_gradients,
+            gates=[self._gate(p) for p in self.pathways] if self.n_gating else [],
             sparse_recurrent=next((c for i, c in sparse.items() if self._sides[i].recurrent), None),
             sparse_feedforward=next((c for i, c in sparse.items() if not self._sides[i].recurrent),
                                     None),
@@ -766,6 +867,12 @@ class ConductanceNetwork(ProjectionNetwork):
         for name in SYNAPSE_PARAMETERS:
             self.register_buffer(name, self.registry.table(name))
         self.register_buffer("g_clip", self.registry.table("g_clip", default=float("inf")))
+        # receptor saturation (conductance/synapses.py:59-67): the fraction of a source's
+        # closed receptors of a type that one of its spikes opens (0: none)
+        saturation = self.registry.table("saturation", default=0.0)
+        assert bool(((saturation >= 0) & (saturation <= 1)).all()), (
+            "synapse params: saturation must be in [0, 1]")
+        self.register_buffer("saturation", saturation, persistent=False)
         # from the synapse parameters, not saved with the module (state dicts load between
         # networks with and without a block)
         for name, table in mg_block_tables(self.registry).items():
@@ -826,6 +933,12 @@ class ConductanceNetwork(ProjectionNetwork):
                 mask = torch.zeros(len(synapses), dtype=torch.bool)
                 mask[types] = True
                 self.register_buffer(f"_learnt_{name}", mask, persistent=False)
+            tau_decay = getattr(self, "_learnt_tau_decay", None)
+            if tau_decay is not None and bool((tau_decay & (self.saturation > 0)).any()):
+                fixed = [synapses[i]["name"] for i in
+                         torch.nonzero(tau_decay & (self.saturation > 0)).flatten().tolist()]
+                raise ValueError(f"tau_decay of the saturating synapse types {fixed} cannot be "
+                                 "learnt: their gating decays with it, fixed per time step")
 
     def _learnt(self, name: str, fixed: torch.Tensor, decay: bool = False):
         """``fixed`` with the learnt types' values in place (``decay``: as
@@ -860,13 +973,19 @@ class ConductanceNetwork(ProjectionNetwork):
             self._onehot_key = key
         return _TypeGather.apply(table, idx, self._onehot)
 
+    def _saturation(self) -> torch.Tensor:
+        return self.saturation
+
     def _set_timestep(self) -> None:
         self.register_buffer("tau_syn", torch.stack((self.tau_rise, self.tau_decay)))
         self.register_buffer("alpha", torch.exp(-self.dt / self.tau_syn))
         self.register_buffer("beta", torch.exp(-self.dt / self.tau_mem))
         self.register_buffer(
-            "g_scale", conductance_kernel(self.tau_rise, self.tau_decay, self.g_bar)
+            "g_scale", conductance_kernel(self.tau_rise, self.tau_decay, self.g_bar,
+                                          self.saturation > 0)
         )
+        # the saturating types' gating decays as their conductances do
+        self._set_gates(self.saturation, self.alpha[1])
         n_ref = torch.round(self.tau_ref / self.dt).to(torch.int32)
         self.register_buffer("n_ref", n_ref, persistent=False)
         self._refractory = bool(n_ref.any())
@@ -883,7 +1002,8 @@ class ConductanceNetwork(ProjectionNetwork):
             tau_rise = learnt("tau_rise", self.tau_rise)
             tau_decay = learnt("tau_decay", self.tau_decay)
             decay = torch.exp(-self.dt / torch.stack((tau_rise, tau_decay)))
-            jump = conductance_kernel(tau_rise, tau_decay, learnt("g_bar", self.g_bar))
+            jump = conductance_kernel(tau_rise, tau_decay, learnt("g_bar", self.g_bar),
+                                      self.saturation > 0)
         return Physiology(
             theta=learnt("theta", self.theta),
             U_reset=learnt("U_reset", self.U_reset),
@@ -916,11 +1036,14 @@ class ConductanceNetwork(ProjectionNetwork):
 
     def _engine_kwargs(self) -> dict:
         return {"refractory": self.refractory,
+                **({"gating": self.gating} if self.n_gating else {}),
                 **({"adaptation": self.adaptation} if self._adapting else {})}
 
     def _after_run(self, run: Run) -> None:
         if run.refractory is not None:
             self.refractory = run.refractory
+        if run.gating is not None and self.n_gating:
+            self.gating = run.gating.detach()
         if run.adaptation is not None:  # the next chunk starts from it, without its graph
             self.adaptation = run.adaptation.detach()
 
@@ -930,6 +1053,8 @@ class ConductanceNetwork(ProjectionNetwork):
         self.register_buffer("refractory", counter, persistent=False)
         self.register_buffer("adaptation", torch.zeros((self.batch_size, self.n_neurons),
                                                        device=self.device), persistent=False)
+        self.register_buffer("gating", self._gating_rest.to(self.device).expand(
+            self.batch_size, -1).clone(), persistent=False)
 
     def get_checkpoint_state(self) -> dict[str, np.ndarray]:
         state = super().get_checkpoint_state()
@@ -937,6 +1062,8 @@ class ConductanceNetwork(ProjectionNetwork):
             state["refractory"] = self.refractory.cpu().numpy()
         if self._adapting:
             state["adaptation"] = self.adaptation.cpu().numpy()
+        if self.n_gating:
+            state["gating"] = self.gating.cpu().numpy()
         return state
 
     def load_checkpoint_state(self, state: dict[str, np.ndarray]) -> None:
@@ -948,6 +1075,8 @@ class ConductanceNetwork(ProjectionNetwork):
         )
         self.adaptation = (torch.from_numpy(state["adaptation"]).to(self.device)
                            if "adaptation" in state else torch.zeros_like(self.v))
+        self.gating = (torch.from_numpy(state["gating"]).to(self.device) if "gating" in state
+                       else self._gating_rest.to(self.device).expand(self.v.shape[0], -1).clone())
 
 
 def _engine_module():
@@ -995,7 +1124,6 @@ class ConductanceLIFNetwork(ConductanceNetwork):
         ff_stp: dict | None = None,
         unify_synapses: bool = True,
     ):
-        _unsupported(cell_params, (synapse_params, synapse_params_FF), (rec_stp, ff_stp))
         self.synapse_params = synapse_params
         self.cell_params_FF = cell_params_FF
         self.synapse_params_FF = synapse_params_FF
@@ -1008,9 +1136,10 @@ class ConductanceLIFNetwork(ConductanceNetwork):
             cell_type_indices=cell_type_indices,
             sides=[
                 InputSide(rec_projections, cell_params, synapse_params, cell_type_indices,
-                          True, "rec_projections", "weights_mask"),
+                          True, "rec_projections", "weights_mask", rec_stp),
                 InputSide(ff_projections, cell_params_FF, synapse_params_FF,
-                          cell_type_indices_FF, False, "ff_projections", "weights_mask_FF"),
+                          cell_type_indices_FF, False, "ff_projections", "weights_mask_FF",
+                          ff_stp),
             ],
             unify_synapses=unify_synapses,
             surrgrad_scale=surrgrad_scale,
@@ -1079,7 +1208,6 @@ class FeedforwardConductanceLIFNetwork(ConductanceNetwork):
         learn: dict | None = None,
         stp: dict | None = None,
     ):
-        _unsupported(cell_params, (synapse_params_FF,), (stp,))
         self.cell_params_FF = cell_params_FF
         self.synapse_params_FF = synapse_params_FF
         self.n_cell_types_FF = len(cell_params_FF)
@@ -1092,7 +1220,7 @@ class FeedforwardConductanceLIFNetwork(ConductanceNetwork):
             cell_type_indices=cell_type_indices,
             sides=[
                 InputSide(projections, cell_params_FF, synapse_params_FF,
-                          cell_type_indices_FF, False, "projections", "weights_mask_FF"),
+                          cell_type_indices_FF, False, "projections", "weights_mask_FF", stp),
             ],
             unify_synapses=False,
             surrgrad_scale=surrgrad_scale,
