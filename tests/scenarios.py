@@ -199,7 +199,8 @@ def recurrent(batch_size, seed, scaling_factors=False, n=N, n_ff=N_FF, n_steps=2
     """``ConductanceLIFNetwork``: frozen weights, perturbed scaling factors, or learnt
     recurrent weights; ``mg`` mM of Mg block on the NMDA types, ``adapt`` the excitatory
     cells' adaptation, ``saturation`` the NMDA types' and ``stp`` short-term plasticity
-    of the excitatory and input sources (reference ``tests/networks.py:276-355``)."""
+    of the excitatory and input sources (``"feedforward"``: of the input sources only)
+    (reference ``tests/networks.py:276-355``)."""
     rng, types, w_rec, w_ff = _structure(seed, n, n_ff)
     ff_types = np.zeros(n_ff, dtype=np.int64)
     rec_blocks = per_type_blocks(w_rec, types, types, REC_NAMES, REC_NAMES)
@@ -220,7 +221,7 @@ def recurrent(batch_size, seed, scaling_factors=False, n=N, n_ff=N_FF, n_steps=2
         synapse_params_FF=saturating(mg_block(MITRAL_SYNAPSES, mg), saturation),
         surrgrad_scale=surrgrad_scale, batch_size=batch_size, learn=learn,
         recurrent_gradients=recurrent_gradients,
-        rec_stp=stp_pairs(["excitatory"]) if stp else None,
+        rec_stp=stp_pairs(["excitatory"]) if stp is True else None,
         ff_stp=stp_pairs(["mitral"]) if stp else None,
     )  # fmt: skip
     sfs = (

@@ -156,3 +156,16 @@ def test_network_with_presynaptic_dynamics_matches_oracle():
     learn = {**LEARN, "tau_decay": ["AMPA", "GABA_A"]}
     _engine_vs_oracle(lambda: sc.feedforward(sc.BATCH_SIZE, sc.SEED, probabilities=True,
                                              learn=learn, stp=True, saturation=0.63))
+
+
+@pytest.mark.parametrize("recurrent_gradients", [False, True], ids=["off", "on"])
+def test_recurrent_network_with_plastic_inputs_matches_oracle(recurrent_gradients):
+    """A recurrent network whose input source has depressing and facilitating STP onto
+    its two target types (its recurrent pathways have none), scaling factors and the
+    physiology learnt: the oracle's spikes, voltages and gradients through both backward
+    passes."""
+    from test_gpu_nmda import LEARN, _engine_vs_oracle, _with_flag
+
+    builder = lambda: sc.recurrent(sc.BATCH_SIZE, sc.SEED, scaling_factors=True,  # noqa: E731
+                                   learn=LEARN, stp="feedforward")
+    _engine_vs_oracle(_with_flag(builder, recurrent_gradients))
