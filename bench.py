@@ -1,7 +1,7 @@
 """Benchmark: neuron-steps/s and synaptic events/s of the fly-scale conductance-LIF
-forward on one MI355X.
+forward (configuration 2, the headline workload) on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1|2|3|4]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 0|1|2|3|4] [--phases]
 
 A step is one forward call of the hot path over one batch of synthetic input: 8 trials
 x 2000 time steps (dt 0.1 ms) of a 140k-neuron, ~50M-synapse network from rest, with
