@@ -235,6 +235,12 @@ typedef struct {
   float* grad_adapt;
   float* grad_adapt_decay;
   float* grad_E_adapt;
+  /* Optional, wt_cond_scan_backward only: dL/da written as rows instead of grad_A — row
+   * k*N + n (pitch B*T_pad floats) holds pathway k's dL/da onto target n at b*T_pad + t,
+   * T_pad a multiple of 16 and >= T (entries t >= T hold no value) — the layout that
+   * wt_weight_gradient_by_target takes with grad_A NULL. grad_A is then not written. */
+  float* grad_A_rows;
+  int64_t T_pad;
 } wt_backward_io;
 
 int wt_cond_scan_backward(const wt_tables* tab, const wt_backward_io* io,
@@ -378,12 +384,15 @@ int wt_edge_sources(const int64_t* indptr, int64_t n_src, int64_t* edge_src,
  * count writes indptr (n+1) int64 (indptr[n] = number of events) and fills scratch
  * (wt_events_scratch_bytes); fill, with the same scratch, writes bt (indptr[n]) int32 and,
  * unless value is NULL (activity known to be 0 or 1: spikes), value (indptr[n]) f32.
- * Deterministic. BT may have at most 65535 * 256 rows. */
+ * BT = B*T rows (b*T + t); fill writes each event's row as b*T_pad + t (T_pad >= T: the
+ * pitch of rows padded per trial; T_pad = T for the rows as they are). Deterministic. BT
+ * may have at most 65535 * 256 rows. */
 int64_t wt_events_scratch_bytes(int64_t BT, int64_t n);
 int wt_events_count(const float* activity, int64_t BT, int64_t n, void* scratch,
                     int64_t* indptr, wt_stream_t stream);
 int wt_events_fill(const float* activity, int64_t BT, int64_t n, const void* scratch,
-                   const int64_t* indptr, int32_t* bt, float* value, wt_stream_t stream);
+                   const int64_t* indptr, int32_t* bt, float* value, int64_t T,
+                   int64_t T_pad, wt_stream_t stream);
 
 /* wt_gate_scan — a feedforward pathway's presynaptic dynamics stepped through a chunk,
  * replacing gate_scan (network_simulators/kernels.py:87-129; the step of
@@ -437,7 +446,9 @@ int wt_filter_backward(const float* grad_smooth, float* grad_x, float a_rise, fl
  * b*T+t for target n; the incoming synapses of row kn are in_edge[in_indptr[kn] ..
  * in_indptr[kn+1]-1] (edge indices, each edge in the row of its source's pathway). One
  * workgroup per row reads it once into LDS. Every edge listed is overwritten; edges
- * listed in no row are left alone. Replaces: as wt_weight_gradient. */
+ * listed in no row are left alone. With grad_A NULL, rows already holds the rows (row
+ * length BT, e.g. B*T_pad from wt_cond_scan_backward's grad_A_rows, the events' rows in
+ * that pitch) and nothing is transposed. Replaces: as wt_weight_gradient. */
 int wt_weight_gradient_by_target(const int64_t* edge_src, int64_t n_edges,
                                  const int64_t* in_indptr, const int64_t* in_edge,
                                  int64_t n_pathways, int64_t N, const int64_t* ev_indptr,

@@ -57,7 +57,7 @@ class BackwardIO(ctypes.Structure):
         ("grad_A", P), ("grad_scale", P), ("grad_theta", P), ("grad_reset", P),
         ("grad_E_L", P), ("grad_C_m", P), ("grad_beta", P), ("grad_E_syn", P),
         ("grad_decay", P), ("grad_jump", P), ("a_saved", P), ("grad_adapt", P),
-        ("grad_adapt_decay", P), ("grad_E_adapt", P),
+        ("grad_adapt_decay", P), ("grad_E_adapt", P), ("grad_A_rows", P), ("T_pad", I64),
     ]  # fmt: skip
 
 
@@ -127,7 +127,7 @@ SIGNATURES = {
     "wt_split_bf16": (ctypes.c_int, [P, I64, P, P, P]),
     "wt_events_scratch_bytes": (I64, [I64, I64]),
     "wt_events_count": (ctypes.c_int, [P, I64, I64, P, P, P]),
-    "wt_events_fill": (ctypes.c_int, [P, I64, I64, P, P, P, P, P]),
+    "wt_events_fill": (ctypes.c_int, [P, I64, I64, P, P, P, P, I64, I64, P]),
     "wt_gate_scan": (ctypes.c_int, [P, I64, I64, I64, P, I64, P, P, I64, I64, I64, P, P]),
     "wt_weight_gradient": (ctypes.c_int, [ctypes.POINTER(Side), P, I64, P, P, P, P, I64,
                                           I64, I64, I64, P, P]),

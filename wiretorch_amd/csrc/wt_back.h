@@ -134,6 +134,7 @@ __device__ inline BackNeuron back_neuron(const wt_tables& tab, int64_t n) {
 // spike's gradient. The reverse loop loads them a step ahead, so that their latency
 // passes during the step before.
 constexpr int kPreK = 4;  // pathways whose activations are loaded ahead (the rest in step)
+constexpr int kBackBlock = 256;  // threads (items) of a scan backward workgroup
 
 template <int S>
 struct StepIn {
@@ -181,7 +182,8 @@ __device__ inline void back_membrane_step(BackState<S>& st, const BackArgs& P,
                                           const Synapses<S>& syn, const BackNeuron& c,
                                           int64_t b, int64_t n, int64_t t,
                                           const StepIn<S>& in, const float (&scale)[WT_MAX_K],
-                                          float* ga_rec = nullptr) {
+                                          float* ga_rec = nullptr, float* ga_stage = nullptr,
+                                          int stage_stride = 0) {
   const wt_tables& tab = P.tab;
   const wt_backward_io& io = P.io;
   const int64_t N = tab.N, K = tab.K, B = io.B, T = io.T;
@@ -234,6 +236,7 @@ __device__ inline void back_membrane_step(BackState<S>& st, const BackArgs& P,
     const float ga = qk * scale[k];
     if (want_A) io.grad_A[ka] = ga;
     if (ga_rec && k < tab.K_rec) ga_rec[k] = ga;
+    if (ga_stage) ga_stage[k * stage_stride] = ga;
     if (want_scale) st.acc_scale[k] += qk * step_A<S>(in, P, k, b, n, t);
   }
   // The adaptation after step t, g_a(t) adapt_decay + adapt s_t: st.la is its adjoint
@@ -336,15 +339,80 @@ __device__ inline void back_finish(const BackState<S>& st, const BackArgs& P, in
   }
 }
 
+// The scan backward with dL/da written as rows (see cond_backward_kernel). Each wave
+// stages its own 64 items ([16 steps][K][64 lanes] of the workgroup's LDS) and writes
+// them out itself: no workgroup barrier, so the waves stay apart in time (a wave's LDS
+// accesses are executed in its program order). A lane past the last item runs item 0's
+// steps and writes nothing.
+template <int S, bool AD>
+__device__ inline void rows_backward(const BackArgs& P, float* stage) {
+  const int64_t N = P.tab.N, B = P.io.B, T = P.io.T, Tp = P.io.T_pad;
+  const int K = (int)P.tab.K;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t first = (int64_t)blockIdx.x * kBackBlock + wave * 64;  // the wave's items
+  stage += wave * 16 * K * 64;
+  const int64_t idx = first + lane;
+  const bool valid = idx < B * N;
+  const int64_t item = valid ? idx : 0;
+  const int64_t b = item / N, n = item - b * N;
+  Synapses<S> syn;
+  load_synapses<S>(P.tab, syn);
+  const BackNeuron c = back_neuron<AD>(P.tab, n);
+  float scale[WT_MAX_K];
+#pragma unroll
+  for (int k = 0; k < WT_MAX_K; ++k) scale[k] = k < K ? P.tab.scale[k * N + n] : 0.0f;
+  BackState<S> st;
+  state_zero(st);
+  StepIn<S> cur, next;
+  load_step<S, AD>(cur, P, b, n, T - 1);
+  for (int64_t t = T - 1; t >= 0; --t) {
+    if (t > 0) load_step<S, AD>(next, P, b, n, t - 1);  // a step ahead
+    back_membrane_step<S, AD>(st, P, syn, c, b, n, t, cur, scale, nullptr,
+                              stage + (int)(t & 15) * K * 64 + lane, 64);
+    back_spike_step<S>(st, P, c, 0.0f, cur);
+    cur = next;
+    if ((t & 15) == 0) {  // steps t .. t + 15 are staged: 64 bytes per (pathway, item)
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      const int64_t pitch = B * Tp;
+      for (int w = lane; w < K * 64 * 4; w += 64) {
+        const int k = w >> 8, i = (w >> 2) & 63, q = w & 3;
+        const int64_t it = first + i;
+        if (it >= B * N) continue;
+        const int64_t bi = it / N, ni = it - bi * N;
+        float4 v;
+        v.x = stage[((4 * q + 0) * K + k) * 64 + i];
+        v.y = stage[((4 * q + 1) * K + k) * 64 + i];
+        v.z = stage[((4 * q + 2) * K + k) * 64 + i];
+        v.w = stage[((4 * q + 3) * K + k) * 64 + i];
+        *reinterpret_cast<float4*>(P.io.grad_A_rows + ((int64_t)k * N + ni) * pitch +
+                                   bi * Tp + t + 4 * q) = v;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();  // the stage is written again from the next step on
+    }
+  }
+  if (valid) back_finish<S>(st, P, b, n);
+}
+
 // Recurrent activations as inputs: one thread per (trial, neuron), all steps. Held to
 // three waves per SIMD (at most 168 VGPRs; a few values spill): with two, too few reverse
 // steps are in flight to cover the loads a step ahead (config 3: 3.39 ms against 3.89).
-template <int S, bool AD>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void
+// ROWS: dL/da goes to io.grad_A_rows as (pathway, target) rows of pitch B*T_pad: each
+// step's K values per item are staged in LDS ([16 steps][K][256 items], dynamic) and
+// every 16 steps (t a multiple of 16) the workgroup writes each item's 16 consecutive
+// steps of each pathway as 64 aligned bytes.
+template <int S, bool AD, bool ROWS>
+__global__ __launch_bounds__(kBackBlock) __attribute__((amdgpu_waves_per_eu(3))) void
 cond_backward_kernel(BackArgs P) {
+  extern __shared__ float stage[];
   const int64_t N = P.tab.N, B = P.io.B, T = P.io.T;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= B * N) return;
+  if (!ROWS && idx >= B * N) return;
+  if (ROWS) {  // the whole workgroup takes part in the staging; items past the end idle
+    rows_backward<S, AD>(P, stage);
+    return;
+  }
   const int64_t b = idx / N, n = idx - b * N;
   Synapses<S> syn;
   load_synapses<S>(P.tab, syn);
@@ -595,12 +663,25 @@ struct BackLaunch {
 template <int S>
 hipError_t BackLaunch<S>::run(BackArgs& a, hipStream_t stream) {
   const int64_t total = a.io.B * a.tab.N;
-  const int block = 256;
+  const int block = kBackBlock;
   const dim3 grid((unsigned)((total + block - 1) / block));
+  if (a.io.grad_A_rows) {  // dL/da as rows: the stage of 16 steps in dynamic LDS
+    const size_t lds = (size_t)16 * a.tab.K * kBackBlock * sizeof(float);
+    const void* fn = a.tab.adapt ? (const void*)cond_backward_kernel<S, true, true>
+                                 : (const void*)cond_backward_kernel<S, false, true>;
+    const hipError_t e =
+        hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    if (a.tab.adapt)
+      hipLaunchKernelGGL((cond_backward_kernel<S, true, true>), grid, dim3(block), lds, stream, a);
+    else
+      hipLaunchKernelGGL((cond_backward_kernel<S, false, true>), grid, dim3(block), lds, stream, a);
+    return hipGetLastError();
+  }
   if (a.tab.adapt)
-    hipLaunchKernelGGL((cond_backward_kernel<S, true>), grid, dim3(block), 0, stream, a);
+    hipLaunchKernelGGL((cond_backward_kernel<S, true, false>), grid, dim3(block), 0, stream, a);
   else
-    hipLaunchKernelGGL((cond_backward_kernel<S, false>), grid, dim3(block), 0, stream, a);
+    hipLaunchKernelGGL((cond_backward_kernel<S, false, false>), grid, dim3(block), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -339,7 +339,7 @@ __global__ __launch_bounds__(kRunBlock) void events_indptr_kernel(const int64_t*
 __global__ void events_fill_kernel(const float* __restrict__ act, int64_t BT, int64_t n,
                                    const int32_t* __restrict__ chunk,
                                    const int64_t* __restrict__ indptr, int32_t* __restrict__ bt,
-                                   float* __restrict__ value) {
+                                   float* __restrict__ value, int64_t T, int64_t T_pad) {
   const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= n) return;
   const int64_t r0 = (int64_t)blockIdx.y * kEvChunk;
@@ -352,7 +352,8 @@ __global__ void events_fill_kernel(const float* __restrict__ act, int64_t BT, in
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       if (a[u] != 0.0f) {
-        bt[pos] = (int32_t)(rb + u);
+        const int64_t row = rb + u;  // b*T + t, written as b*T_pad + t
+        bt[pos] = (int32_t)(T_pad == T ? row : row + (row / T) * (T_pad - T));
         if (value) value[pos] = a[u];
         ++pos;
       }
@@ -698,6 +699,9 @@ extern "C" int wt_cond_scan_backward(const wt_tables* tab, const wt_backward_io*
   if (io->grad_decay && !io->g_init) return hipErrorInvalidValue;
   if (tab->adapt && (!tab->adapt_decay || !tab->E_adapt || !io->a_saved))
     return hipErrorInvalidValue;
+  if (io->grad_A_rows &&
+      (io->T_pad < io->T || io->T_pad % 16 || io->B * io->T_pad > INT32_MAX || tab->K < 1))
+    return hipErrorInvalidValue;
   if (io->B * tab->N == 0 || io->T == 0) return hipSuccess;
   BackArgs a = {};
   a.tab = *tab;
@@ -727,7 +731,7 @@ extern "C" int wt_cond_recurrent_backward(const wt_tables* tab, const wt_side* r
   if (io->grad_decay && !io->g_init) return hipErrorInvalidValue;
   if (tab->adapt && (!tab->adapt_decay || !tab->E_adapt || !io->a_saved))
     return hipErrorInvalidValue;
-  if (rec->n_src != tab->N) return hipErrorInvalidValue;
+  if (rec->n_src != tab->N || io->grad_A_rows) return hipErrorInvalidValue;
   if (io->B * tab->N == 0 || io->T == 0) return hipSuccess;
   if (!rec->indptr || !rec->pathway) return hipErrorInvalidValue;
   BackArgs a = {};
@@ -783,9 +787,10 @@ extern "C" int wt_events_count(const float* activity, int64_t BT, int64_t n, voi
 }
 
 extern "C" int wt_events_fill(const float* activity, int64_t BT, int64_t n, const void* scratch,
-                              const int64_t* indptr, int32_t* bt, float* value,
-                              wt_stream_t stream) {
-  if (BT < 0 || n < 0 || BT > INT32_MAX) return hipErrorInvalidValue;
+                              const int64_t* indptr, int32_t* bt, float* value, int64_t T,
+                              int64_t T_pad, wt_stream_t stream) {
+  if (BT < 0 || n < 0 || T < 1 || T_pad < T || BT % T) return hipErrorInvalidValue;
+  if ((BT / T) * T_pad > INT32_MAX) return hipErrorInvalidValue;
   if (BT == 0 || n == 0) return hipSuccess;
   if (!activity || !scratch || !indptr || !bt) return hipErrorInvalidValue;
   const int64_t n_chunks = (BT + kEvChunk - 1) / kEvChunk;
@@ -793,7 +798,7 @@ extern "C" int wt_events_fill(const float* activity, int64_t BT, int64_t n, cons
   hipLaunchKernelGGL(events_fill_kernel,
                      dim3((unsigned)((n + kEvBlock - 1) / kEvBlock), (unsigned)n_chunks),
                      dim3(kEvBlock), 0, (hipStream_t)stream, activity, BT, n,
-                     static_cast<const int32_t*>(scratch), indptr, bt, value);
+                     static_cast<const int32_t*>(scratch), indptr, bt, value, T, T_pad);
   return hipGetLastError();
 }
 
@@ -841,16 +846,17 @@ extern "C" int wt_weight_gradient_by_target(const int64_t* edge_src, int64_t n_e
     return hipErrorInvalidValue;
   const int64_t n_rows = n_pathways * N;
   if (n_edges == 0 || n_rows == 0) return hipSuccess;
-  if (!edge_src || !in_indptr || !in_edge || !ev_indptr || !ev_bt || !grad_A || !rows ||
-      !grad_w || BT == 0)
+  if (!edge_src || !in_indptr || !in_edge || !ev_indptr || !ev_bt || !rows || !grad_w ||
+      BT == 0)
     return hipErrorInvalidValue;
   if (n_rows > 0x7fffffff || (N + 63) / 64 > 0x7fffffff || (BT + 63) / 64 > 65535 ||
       n_pathways > 65535)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(transpose_rows_kernel,
-                     dim3((unsigned)((N + 63) / 64), (unsigned)((BT + 63) / 64),
-                          (unsigned)n_pathways),
-                     dim3(256), 0, (hipStream_t)stream, grad_A, rows, BT, N);
+  if (grad_A)  // (else rows holds them already)
+    hipLaunchKernelGGL(transpose_rows_kernel,
+                       dim3((unsigned)((N + 63) / 64), (unsigned)((BT + 63) / 64),
+                            (unsigned)n_pathways),
+                       dim3(256), 0, (hipStream_t)stream, grad_A, rows, BT, N);
   const int64_t chunk = BT < kWgChunk ? BT : kWgChunk;
   const void* fn = ev_val ? (const void*)weight_gradient_target_kernel<true>
                           : (const void*)weight_gradient_target_kernel<false>;

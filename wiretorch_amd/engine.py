@@ -920,7 +920,13 @@ class _Run(torch.autograd.Function):
         want_A = want_x or any(w_needs)
         dev = L.device
         B, T, N, S, K = L.B, L.T, L.N, L.S, L.K
-        grad_A = torch.empty((max(K, 1), B, T, N), device=dev) if want_A else None
+        # Only the weight gradients want dL/da: the scan backward writes it directly as
+        # the (pathway, target) rows they read, each trial's steps padded to 16
+        T_pad = -(-T // 16) * 16
+        as_rows = want_A and not want_x and not L.recurrent_gradients and K >= 1
+        grad_A = (torch.empty((max(K, 1), B, T, N), device=dev) if want_A and not as_rows
+                  else None)
+        rows = (torch.empty((K * N, B * T_pad), device=dev), T_pad) if as_rows else None
         partial = torch.empty((max(K, 1), B, N), device=dev) if want_scale else None
         shapes = [(B, N)] * 5 + [(B, S, N), (B, 2, S, N), (B, 2, S, N)] + [(B, N)] * 3
         phys = [torch.empty(sh, device=dev) if want else None for sh, want in zip(shapes, p_needs)]
@@ -932,6 +938,7 @@ class _Run(torch.autograd.Function):
             g_init.data_ptr() if g_init.numel() else None, B, T,
             _lib.ptr(grad_A), _lib.ptr(partial), *[_lib.ptr(t) for t in phys[:8]],
             a_saved.data_ptr() if L.adapting else None, *[_lib.ptr(t) for t in phys[8:]],
+            rows[0].data_ptr() if rows else None, T_pad if rows else 0,
         )  # fmt: skip
         tab = L.abi_tables(scale.detach().float().contiguous())
         lib = _lib.load()
@@ -964,11 +971,12 @@ class _Run(torch.autograd.Function):
             if rec_counted is not None:
                 grad_w[:n_rec_w] = _weight_grads(L, L.rec, spikes, grad_A, 0,
                                                  weights[:n_rec_w], w_needs[:n_rec_w],
-                                                 rec_counted, spikes=True)
+                                                 rec_counted, spikes=True, rows=rows)
             if ff_counted is not None:
                 grad_w[n_rec_w:] = _weight_grads(L, L.ff, activity, grad_A, L.K_rec,
                                                  weights[n_rec_w:], w_needs[n_rec_w:],
-                                                 ff_counted, spikes=L.poisson is not None)
+                                                 ff_counted, spikes=L.poisson is not None,
+                                                 rows=rows)
         grad_x = _input_grad(L, x, grad_A, weights[n_rec_w:]) if want_x else None
         return (None, None, grad_scale, grad_x, None, None, None, None, *grad_w, *grad_phys)
 
@@ -1019,12 +1027,13 @@ def _count_events(activity: torch.Tensor, stream):
     return flat, scratch, indptr, total, counted
 
 
-def _events(activity: torch.Tensor, stream, counted=None, values=True):
-    """Per source, its (trial*T + step) events ascending (int32) and their values:
-    ``(indptr, bt, value)`` from ``activity`` ``(B, T, n_src)`` (``wt_events_count`` /
-    ``wt_events_fill``; the host reads the number of events to size the lists).
-    ``counted``: what ``_count_events`` returned for this activity, if it ran already;
-    without ``values`` (an activity of spikes, 0 or 1) ``value`` is None."""
+def _events(activity: torch.Tensor, stream, counted=None, values=True, T_pad=None):
+    """Per source, its (trial*T_pad + step) events ascending (int32; ``T_pad`` = T unless
+    given) and their values: ``(indptr, bt, value)`` from ``activity`` ``(B, T, n_src)``
+    (``wt_events_count`` / ``wt_events_fill``; the host reads the number of events to size
+    the lists). ``counted``: what ``_count_events`` returned for this activity, if it ran
+    already; without ``values`` (an activity of spikes, 0 or 1) ``value`` is None."""
+    T = activity.shape[1]
     flat, scratch, indptr, total, done = counted or _count_events(activity, stream)
     BT, n = flat.shape
     dev = activity.device
@@ -1035,31 +1044,37 @@ def _events(activity: torch.Tensor, stream, counted=None, values=True):
     value = torch.empty(total, dtype=torch.float32, device=dev) if values else None
     if total:
         _lib.check(lib.wt_events_fill(flat.data_ptr(), BT, n, scratch.data_ptr(),
-                                      indptr.data_ptr(), bt.data_ptr(), _lib.ptr(value),
-                                      stream), "wt_events_fill")
+                                      indptr.data_ptr(), bt.data_ptr(), _lib.ptr(value), T,
+                                      T_pad or T, stream), "wt_events_fill")
     return indptr, bt, value
 
 
 def _weight_grads(L: _Plan, side: _Side, activity, grad_A, k0, weights, needs, counted=None,
-                  spikes=False):
+                  spikes=False, rows=None):
     """Gradients of a side's weight tensors from the event-driven support gradient:
-    ``wt_weight_gradient_by_target`` over dL/da transposed to (pathway, target) rows.
-    ``spikes``: the activity is 0 or 1 (its events carry no values)."""
+    ``wt_weight_gradient_by_target`` over dL/da as (pathway, target) rows — ``rows``
+    ``(all rows, T_pad)`` as the scan backward wrote them, else transposed from
+    ``grad_A``. ``spikes``: the activity is 0 or 1 (its events carry no values)."""
     c = side.conn
-    indptr, bt, value = _events(activity, L.stream, counted, values=not spikes)
+    indptr, bt, value = _events(activity, L.stream, counted, values=not spikes,
+                                T_pad=rows[1] if rows else None)
     grad_e = torch.zeros(c.n_edges, device=L.device)
     edge_src = side.edge_src(L.stream)
     n_path = int(c.n_pathways)
     if c.n_edges and n_path:
         in_indptr, in_edge = side.by_target(L.N, n_path, L.stream)
-        BT = L.B * L.T
-        rows = torch.empty((n_path * L.N, BT), device=L.device)
-        gA = grad_A[k0: k0 + n_path]
+        if rows is not None:  # the rows of this side's pathways, as written
+            BT = L.B * rows[1]
+            side_rows, gA = rows[0][k0 * L.N: (k0 + n_path) * L.N], None
+        else:
+            BT = L.B * L.T
+            side_rows = torch.empty((n_path * L.N, BT), device=L.device)
+            gA = grad_A[k0: k0 + n_path]
         _lib.check(
             _lib.load().wt_weight_gradient_by_target(
                 edge_src.data_ptr(), c.n_edges, in_indptr.data_ptr(), in_edge.data_ptr(),
                 n_path, L.N, indptr.data_ptr(), bt.data_ptr(), _lib.ptr(value),
-                gA.data_ptr(), BT, rows.data_ptr(), grad_e.data_ptr(), L.stream),
+                _lib.ptr(gA), BT, side_rows.data_ptr(), grad_e.data_ptr(), L.stream),
             "wt_weight_gradient_by_target",
         )  # fmt: skip
     if side.row_local is None:  # compressed side: the gradient of its weights
