@@ -382,8 +382,10 @@ int wt_edge_sources(const int64_t* indptr, int64_t n_src, int64_t* edge_src,
  * lists the weight gradients take. Replaces the torch nonzero / argsort / bincount that
  * form them around the reference's weight_gradient (network_simulators/engine.py:327-350).
  * count writes indptr (n+1) int64 (indptr[n] = number of events) and fills scratch
- * (wt_events_scratch_bytes); fill, with the same scratch, writes bt (indptr[n]) int32 and,
- * unless value is NULL (activity known to be 0 or 1: spikes), value (indptr[n]) f32.
+ * (wt_events_scratch_bytes: per 256-row chunk and source, the count and the nonzero rows
+ * as bits); fill, with the same scratch, writes bt (indptr[n]) int32 and, unless value is
+ * NULL (activity known to be 0 or 1: spikes; the rows then come from the bits, without a
+ * second read of the activity), value (indptr[n]) f32.
  * BT = B*T rows (b*T + t); fill writes each event's row as b*T_pad + t (T_pad >= T: the
  * pitch of rows padded per trial; T_pad = T for the rows as they are). Deterministic. BT
  * may have at most 65535 * 256 rows. */

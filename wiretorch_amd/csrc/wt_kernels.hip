@@ -283,20 +283,54 @@ __global__ void edge_source_kernel(const int64_t* indptr, int64_t n_src, int64_t
 // ---- Events by source: the nonzero entries of a (BT, n) activity, per column j in
 // ascending row order. Rows are taken in chunks of kEvChunk; thread (chunk c, column j)
 // counts, then writes, its chunk's entries of column j (a wave reads 64 consecutive
-// columns of one row at a time).
+// columns of one row at a time). The count also records which rows of the chunk are
+// nonzero, as 8 words of bits (word w of chunk c, column j at bits[(c * 8 + w) * n + j]):
+// a fill that wants no values (spikes) reads those instead of the activity again.
 constexpr int64_t kEvChunk = 256;
 constexpr int kEvBlock = 256;
+constexpr int kEvWords = (int)kEvChunk / 32;
 
 __global__ void events_count_kernel(const float* __restrict__ act, int64_t BT, int64_t n,
-                                    int32_t* __restrict__ chunk) {
+                                    int32_t* __restrict__ chunk, uint32_t* __restrict__ bits) {
   const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (j >= n) return;
   const int64_t r0 = (int64_t)blockIdx.y * kEvChunk;
   const int64_t r1 = r0 + kEvChunk < BT ? r0 + kEvChunk : BT;
   int32_t count = 0;
+  for (int w = 0; w < kEvWords; ++w) {
+    uint32_t word = 0u;
 #pragma unroll 8
-  for (int64_t r = r0; r < r1; ++r) count += act[r * n + j] != 0.0f ? 1 : 0;
+    for (int u = 0; u < 32; ++u) {
+      const int64_t r = r0 + 32 * w + u;
+      if (r < r1 && act[r * n + j] != 0.0f) word |= 1u << u;
+    }
+    count += __builtin_popcount(word);
+    bits[((int64_t)blockIdx.y * kEvWords + w) * n + j] = word;
+  }
   chunk[blockIdx.y * n + j] = count;
+}
+
+// The fill of a value-free list (every value 1) from the count's bits.
+__global__ void events_fill_bits_kernel(const uint32_t* __restrict__ bits, int64_t n,
+                                        const int32_t* __restrict__ chunk,
+                                        const int64_t* __restrict__ indptr,
+                                        int32_t* __restrict__ bt, int64_t T, int64_t T_pad) {
+  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  const int64_t r0 = (int64_t)blockIdx.y * kEvChunk;
+  int64_t pos = indptr[j] + chunk[blockIdx.y * n + j];
+  uint32_t words[kEvWords];
+#pragma unroll
+  for (int w = 0; w < kEvWords; ++w) words[w] = bits[((int64_t)blockIdx.y * kEvWords + w) * n + j];
+#pragma unroll
+  for (int w = 0; w < kEvWords; ++w) {
+    uint32_t word = words[w];
+    while (word) {
+      const int64_t row = r0 + 32 * w + __builtin_ctz(word);  // b*T + t, as b*T_pad + t
+      word &= word - 1u;
+      bt[pos++] = (int32_t)(T_pad == T ? row : row + (row / T) * (T_pad - T));
+    }
+  }
 }
 
 // Per column: each chunk's count becomes its offset within the column; the column's
@@ -758,7 +792,7 @@ extern "C" int wt_edge_sources(const int64_t* indptr, int64_t n_src, int64_t* ed
 
 extern "C" int64_t wt_events_scratch_bytes(int64_t BT, int64_t n) {
   if (BT < 0 || n < 0) return 0;
-  return ((BT + kEvChunk - 1) / kEvChunk) * n * 4;
+  return ((BT + kEvChunk - 1) / kEvChunk) * n * 4 * (1 + kEvWords);  // counts, then bits
 }
 
 extern "C" int wt_events_count(const float* activity, int64_t BT, int64_t n, void* scratch,
@@ -771,7 +805,8 @@ extern "C" int wt_events_count(const float* activity, int64_t BT, int64_t n, voi
   const dim3 cols((unsigned)((n + kEvBlock - 1) / kEvBlock));
   if (n > 0 && BT > 0) {
     hipLaunchKernelGGL(events_count_kernel, dim3(cols.x, (unsigned)n_chunks), dim3(kEvBlock), 0,
-                       (hipStream_t)stream, activity, BT, n, chunk);
+                       (hipStream_t)stream, activity, BT, n, chunk,
+                       reinterpret_cast<uint32_t*>(chunk + n_chunks * n));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -795,10 +830,15 @@ extern "C" int wt_events_fill(const float* activity, int64_t BT, int64_t n, cons
   if (!activity || !scratch || !indptr || !bt) return hipErrorInvalidValue;
   const int64_t n_chunks = (BT + kEvChunk - 1) / kEvChunk;
   if (n_chunks > 65535) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(events_fill_kernel,
-                     dim3((unsigned)((n + kEvBlock - 1) / kEvBlock), (unsigned)n_chunks),
-                     dim3(kEvBlock), 0, (hipStream_t)stream, activity, BT, n,
-                     static_cast<const int32_t*>(scratch), indptr, bt, value, T, T_pad);
+  const int32_t* chunk = static_cast<const int32_t*>(scratch);
+  const dim3 grid((unsigned)((n + kEvBlock - 1) / kEvBlock), (unsigned)n_chunks);
+  if (value)
+    hipLaunchKernelGGL(events_fill_kernel, grid, dim3(kEvBlock), 0, (hipStream_t)stream,
+                       activity, BT, n, chunk, indptr, bt, value, T, T_pad);
+  else  // positions only: from the count's bits
+    hipLaunchKernelGGL(events_fill_bits_kernel, grid, dim3(kEvBlock), 0, (hipStream_t)stream,
+                       reinterpret_cast<const uint32_t*>(chunk + n_chunks * n), n, chunk, indptr,
+                       bt, T, T_pad);
   return hipGetLastError();
 }
 
