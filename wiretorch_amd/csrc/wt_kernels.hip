@@ -296,16 +296,36 @@ __global__ void events_count_kernel(const float* __restrict__ act, int64_t BT, i
   if (j >= n) return;
   const int64_t r0 = (int64_t)blockIdx.y * kEvChunk;
   const int64_t r1 = r0 + kEvChunk < BT ? r0 + kEvChunk : BT;
-  int32_t count = 0;
-  for (int w = 0; w < kEvWords; ++w) {
-    uint32_t word = 0u;
+  // Every load before the first store (one counter covers a wave's loads and stores: a
+  // store between them would make the later loads' use wait for it).
+  const float* p = act + r0 * n + j;  // row r0 of column j; rows n floats apart
+  const int rows = (int)(r1 - r0);
+  uint32_t words[kEvWords];
+  if (rows == (int)kEvChunk) {  // a whole chunk: no branch around the loads
+#pragma unroll
+    for (int w = 0; w < kEvWords; ++w) {
+      uint32_t word = 0u;
 #pragma unroll 8
-    for (int u = 0; u < 32; ++u) {
-      const int64_t r = r0 + 32 * w + u;
-      if (r < r1 && act[r * n + j] != 0.0f) word |= 1u << u;
+      for (int u = 0; u < 32; ++u)
+        word |= (p[(int64_t)(32 * w + u) * n] != 0.0f ? 1u : 0u) << u;
+      words[w] = word;
     }
-    count += __builtin_popcount(word);
-    bits[((int64_t)blockIdx.y * kEvWords + w) * n + j] = word;
+  } else {
+#pragma unroll
+    for (int w = 0; w < kEvWords; ++w) {
+      uint32_t word = 0u;
+      for (int u = 0; u < 32; ++u) {
+        const int r = 32 * w + u;
+        if (r < rows && p[(int64_t)r * n] != 0.0f) word |= 1u << u;
+      }
+      words[w] = word;
+    }
+  }
+  int32_t count = 0;
+#pragma unroll
+  for (int w = 0; w < kEvWords; ++w) {
+    count += __builtin_popcount(words[w]);
+    bits[((int64_t)blockIdx.y * kEvWords + w) * n + j] = words[w];
   }
   chunk[blockIdx.y * n + j] = count;
 }
